@@ -1,0 +1,1133 @@
+// SPDX-License-Identifier: Apache-2.0
+//
+// CPU oracle (TEST INFRASTRUCTURE ONLY) for the StripedHyena2 prefill path.
+// Restates the reference's CPU F32 algorithm; see oracle.h for the citation
+// of every entry point and what pins it. Built by oracle/Makefile with the
+// same language mode as the reference (ISO C++17, -O3) so that the compiler
+// makes the same floating-point contraction decisions.
+#include "oracle.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <fcntl.h>
+#include <limits>
+#include <map>
+#include <memory>
+#include <string>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+#include <vector>
+
+#if defined(__x86_64__)
+#include <immintrin.h>
+#endif
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(const std::string &message) {
+  g_error = message;
+  return 1;
+}
+
+float bf16_bits_to_float(const uint16_t bits) {
+  const uint32_t wide = static_cast<uint32_t>(bits) << 16U;
+  float value;
+  std::memcpy(&value, &wide, sizeof(value));
+  return value;
+}
+
+uint16_t float_to_bf16_rne(const float value) {
+  uint32_t bits;
+  std::memcpy(&bits, &value, sizeof(bits));
+  if ((bits & 0x7fffffffU) > 0x7f800000U)
+    return static_cast<uint16_t>((bits >> 16U) | 0x40U);
+  const uint32_t rounding = 0x7fffU + ((bits >> 16U) & 1U);
+  return static_cast<uint16_t>((bits + rounding) >> 16U);
+}
+
+// ---- E4M3FN: src/fp8.cpp:10-19 (decode_positive), :26-58 (encode).
+float e4m3_positive(const uint8_t magnitude) {
+  const unsigned exponent = (magnitude >> 3U) & 0x0fU;
+  const unsigned mantissa = magnitude & 0x07U;
+  if (exponent == 0U)
+    return std::ldexp(static_cast<float>(mantissa), -9);
+  return std::ldexp(1.0F + static_cast<float>(mantissa) / 8.0F,
+                    static_cast<int>(exponent) - 7);
+}
+
+// ---- QGMMA helpers: tests/test_cuda_ops.cu:119-146.
+uint32_t float_bits(const float value) {
+  uint32_t bits;
+  std::memcpy(&bits, &value, sizeof(bits));
+  return bits;
+}
+
+float bits_to_float(const uint32_t bits) {
+  float value;
+  std::memcpy(&value, &bits, sizeof(value));
+  return value;
+}
+
+int unbiased_exponent(const float value) {
+  return static_cast<int>((float_bits(std::fabs(value)) >> 23U) & 0xffU) - 127;
+}
+
+// Aligns a value whose binade is `own_exponent` (for a product of two E4M3
+// numbers the sum of the operand exponents) to `top_exponent`, keeping 13
+// fractional bits below the top binade (significand >> 10).
+int32_t align_to(const float value, const int own_exponent,
+                 const int top_exponent, const bool product) {
+  if (value == 0.0F)
+    return 0;
+  const uint32_t bits = float_bits(value);
+  const uint32_t magnitude = bits & 0x7fffffffU;
+  uint32_t significand = (magnitude & 0x7fffffU) | 0x800000U;
+  if (product) {
+    const int actual = static_cast<int>((magnitude >> 23U) & 0xffU) - 127;
+    significand <<= static_cast<unsigned>(actual - own_exponent);
+  }
+  significand >>= 10U;
+  const int shift = top_exponent - own_exponent;
+  if (shift > 31)
+    significand = 0;
+  else if (shift > 0)
+    significand >>= static_cast<unsigned>(shift);
+  const auto aligned = static_cast<int32_t>(significand);
+  return (bits & 0x80000000U) == 0U ? aligned : -aligned;
+}
+
+// ---- BF16-weight dot: src/cpu/model.cpp:205-261. Eight FMA lanes over the
+// 8-aligned prefix, lanes summed 0..7 left to right, then a scalar tail.
+#if defined(__x86_64__)
+__attribute__((target("avx2,fma"))) float
+dot_bf16_avx2(const float *const input, const uint16_t *const weight,
+              const std::size_t size) {
+  __m256 total = _mm256_setzero_ps();
+  std::size_t index = 0;
+  for (; index + 8 <= size; index += 8) {
+    const auto packed =
+        _mm_loadu_si128(reinterpret_cast<const __m128i *>(weight + index));
+    const auto wide = _mm256_slli_epi32(_mm256_cvtepu16_epi32(packed), 16);
+    total = _mm256_fmadd_ps(_mm256_loadu_ps(input + index),
+                            _mm256_castsi256_ps(wide), total);
+  }
+  alignas(32) float lanes[8];
+  _mm256_store_ps(lanes, total);
+  float result = lanes[0] + lanes[1] + lanes[2] + lanes[3] + lanes[4] +
+                 lanes[5] + lanes[6] + lanes[7];
+  for (; index < size; ++index)
+    result += input[index] * bf16_bits_to_float(weight[index]);
+  return result;
+}
+
+bool cpu_has_avx2_fma() {
+  __builtin_cpu_init();
+  return __builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma");
+}
+#endif
+
+float dot_bf16(const float *const input, const uint16_t *const weight,
+               const std::size_t size) {
+#if defined(__x86_64__)
+  static const bool avx2 = cpu_has_avx2_fma();
+  if (avx2)
+    return dot_bf16_avx2(input, weight, size);
+#endif
+  float result = 0.0F;
+  for (std::size_t index = 0; index < size; ++index)
+    result += input[index] * bf16_bits_to_float(weight[index]);
+  return result;
+}
+
+float gelu_erf(const float value) {
+  return 0.5F * value * (1.0F + std::erf(value * 0.7071067811865475244F));
+}
+
+// ---- Safetensors reader (only what the oracle needs; the format is the
+// public Safetensors layout plus evo2-runtime-v1 typed metadata).
+struct Json {
+  enum Kind { kNull, kString, kNumber, kArray, kObject } kind{kNull};
+  std::string text;
+  double number{0};
+  std::vector<Json> items;
+  std::vector<std::pair<std::string, Json>> members;
+  const Json *get(const std::string &key) const {
+    for (const auto &member : members)
+      if (member.first == key)
+        return &member.second;
+    return nullptr;
+  }
+};
+
+class JsonReader {
+public:
+  JsonReader(const char *begin, const char *end) : p_(begin), end_(end) {}
+  bool value(Json *out) {
+    space();
+    if (p_ >= end_)
+      return false;
+    if (*p_ == '{') {
+      ++p_;
+      out->kind = Json::kObject;
+      space();
+      if (p_ < end_ && *p_ == '}') {
+        ++p_;
+        return true;
+      }
+      while (true) {
+        Json key;
+        space();
+        if (!string(&key.text))
+          return false;
+        space();
+        if (p_ >= end_ || *p_++ != ':')
+          return false;
+        Json item;
+        if (!value(&item))
+          return false;
+        out->members.emplace_back(key.text, std::move(item));
+        space();
+        if (p_ < end_ && *p_ == ',') {
+          ++p_;
+          continue;
+        }
+        if (p_ < end_ && *p_ == '}') {
+          ++p_;
+          return true;
+        }
+        return false;
+      }
+    }
+    if (*p_ == '[') {
+      ++p_;
+      out->kind = Json::kArray;
+      space();
+      if (p_ < end_ && *p_ == ']') {
+        ++p_;
+        return true;
+      }
+      while (true) {
+        Json item;
+        if (!value(&item))
+          return false;
+        out->items.push_back(std::move(item));
+        space();
+        if (p_ < end_ && *p_ == ',') {
+          ++p_;
+          continue;
+        }
+        if (p_ < end_ && *p_ == ']') {
+          ++p_;
+          return true;
+        }
+        return false;
+      }
+    }
+    if (*p_ == '"') {
+      out->kind = Json::kString;
+      return string(&out->text);
+    }
+    out->kind = Json::kNumber;
+    const char *start = p_;
+    while (p_ < end_ && (std::isdigit(static_cast<unsigned char>(*p_)) ||
+                         *p_ == '-' || *p_ == '.' || *p_ == 'e' ||
+                         *p_ == 'E' || *p_ == '+'))
+      ++p_;
+    if (p_ == start)
+      return false;
+    out->text.assign(start, p_);
+    out->number = std::strtod(out->text.c_str(), nullptr);
+    return true;
+  }
+
+private:
+  void space() {
+    while (p_ < end_ && (*p_ == ' ' || *p_ == '\n' || *p_ == '\t' ||
+                         *p_ == '\r'))
+      ++p_;
+  }
+  bool string(std::string *out) {
+    if (p_ >= end_ || *p_ != '"')
+      return false;
+    ++p_;
+    out->clear();
+    while (p_ < end_ && *p_ != '"') {
+      if (*p_ == '\\') {
+        ++p_;
+        if (p_ >= end_)
+          return false;
+        const char c = *p_;
+        out->push_back(c == 'n' ? '\n' : c == 't' ? '\t' : c);
+      } else {
+        out->push_back(*p_);
+      }
+      ++p_;
+    }
+    if (p_ >= end_)
+      return false;
+    ++p_;
+    return true;
+  }
+  const char *p_;
+  const char *end_;
+};
+
+struct Tensor {
+  std::string dtype;
+  std::vector<size_t> shape;
+  const uint8_t *data{nullptr};
+  size_t bytes{0};
+  size_t elements() const {
+    size_t count = 1;
+    for (auto d : shape)
+      count *= d;
+    return count;
+  }
+  float at(const size_t index) const {
+    if (dtype == "BF16") {
+      uint16_t bits;
+      std::memcpy(&bits, data + index * 2, 2);
+      return bf16_bits_to_float(bits);
+    }
+    if (dtype == "F8_E4M3")
+      return oracle_e4m3_decode(data[index]);
+    float value;
+    std::memcpy(&value, data + index * 4, 4);
+    return value;
+  }
+  const uint16_t *bf16() const {
+    return reinterpret_cast<const uint16_t *>(data);
+  }
+};
+
+enum class Mixer { kHcs, kHcm, kHcl, kAttention };
+
+struct Layer {
+  Mixer type{Mixer::kHcs};
+  const Tensor *pre_norm{nullptr}, *post_norm{nullptr}, *projection{nullptr},
+      *out_weight{nullptr}, *out_bias{nullptr}, *short_filter{nullptr},
+      *inner_filter{nullptr}, *direct{nullptr}, *log_poles{nullptr},
+      *residues{nullptr}, *inv_freq{nullptr}, *l1{nullptr}, *l2{nullptr},
+      *l3{nullptr};
+  float fp8_input_scale{0}, fp8_output_scale{0};
+};
+
+struct Model {
+  void *map{nullptr};
+  size_t map_size{0};
+  std::map<std::string, Tensor> tensors;
+  std::map<std::string, std::string> metadata;
+  size_t vocab{0}, width{0}, layers{0}, heads{0}, state{0}, inner{0},
+      short_len{0}, hcs_len{0}, hcm_len{0}, hcs_groups{0}, hcm_groups{0};
+  float eps{0}, rope_scale{0};
+  bool column_split{false};
+  const Tensor *embedding{nullptr}, *final_norm{nullptr};
+  std::vector<Layer> layer;
+  ~Model() {
+    if (map != nullptr)
+      munmap(map, map_size);
+  }
+};
+
+bool meta_u64(const Model &m, const std::string &key, size_t *out) {
+  auto it = m.metadata.find(key);
+  if (it == m.metadata.end() || it->second.rfind("u:", 0) != 0)
+    return false;
+  *out = static_cast<size_t>(std::stoull(it->second.substr(2)));
+  return true;
+}
+
+bool meta_f32(const Model &m, const std::string &key, float *out) {
+  auto it = m.metadata.find(key);
+  if (it == m.metadata.end() || it->second.rfind("f:", 0) != 0)
+    return false;
+  const uint64_t bits = std::stoull(it->second.substr(2), nullptr, 16);
+  double value;
+  std::memcpy(&value, &bits, sizeof(value));
+  *out = static_cast<float>(value);
+  return true;
+}
+
+bool meta_list(const Model &m, const std::string &key,
+               std::vector<size_t> *out) {
+  auto it = m.metadata.find(key);
+  if (it == m.metadata.end() || it->second.rfind("l:", 0) != 0)
+    return false;
+  out->clear();
+  std::string rest = it->second.substr(2);
+  size_t start = 0;
+  while (start < rest.size()) {
+    size_t comma = rest.find(',', start);
+    if (comma == std::string::npos)
+      comma = rest.size();
+    out->push_back(static_cast<size_t>(std::stoull(rest.substr(start, comma - start))));
+    start = comma + 1;
+  }
+  return true;
+}
+
+const Tensor *need(const Model &m, const std::string &name,
+                   std::vector<size_t> shape) {
+  auto it = m.tensors.find(name);
+  if (it == m.tensors.end() || it->second.shape != shape)
+    return nullptr;
+  return &it->second;
+}
+
+// ---- Model-path primitives (src/cpu/model.cpp:284-453).
+void linear_model(const std::vector<float> &input, size_t rows, size_t in,
+                  const Tensor &weight, size_t out_width, const Tensor *bias,
+                  std::vector<float> *output, int threads) {
+  output->assign(rows * out_width, 0.0F);
+  const long long total = static_cast<long long>(rows * out_width);
+#pragma omp parallel for schedule(static) num_threads(threads > 0 ? threads : 1)
+  for (long long item = 0; item < total; ++item) {
+    const size_t row = static_cast<size_t>(item) / out_width;
+    const size_t target = static_cast<size_t>(item) % out_width;
+    const float *source = input.data() + row * in;
+    float value;
+    if (weight.dtype == "BF16") {
+      value = dot_bf16(source, weight.bf16() + target * in, in);
+    } else {
+      value = 0.0F;
+      for (size_t index = 0; index < in; ++index)
+        value += source[index] * weight.at(target * in + index);
+    }
+    if (bias != nullptr)
+      value += bias->at(target);
+    (*output)[static_cast<size_t>(item)] = value;
+  }
+}
+
+// FP8 projection with CUDA-reference semantics: codes of bf16(x)*input_scale,
+// QGMMA K=32 accumulation, bf16(acc*output_scale).
+void linear_fp8(const std::vector<float> &input, size_t rows, size_t in,
+                const Tensor &weight, size_t out_width, float input_scale,
+                float output_scale, std::vector<float> *output, int threads) {
+  std::vector<uint8_t> codes(rows * in);
+  oracle_e4m3_quantize_f32(input.data(), codes.size(), input_scale,
+                           codes.data());
+  output->assign(rows * out_width, 0.0F);
+  const long long total = static_cast<long long>(rows);
+#pragma omp parallel for schedule(static) num_threads(threads > 0 ? threads : 1)
+  for (long long row = 0; row < total; ++row) {
+    oracle_qgmma_linear(codes.data() + static_cast<size_t>(row) * in,
+                        weight.data, 1, in, out_width, output_scale, 32,
+                        output->data() + static_cast<size_t>(row) * out_width);
+  }
+}
+
+void rms_norm_model(const std::vector<float> &input, size_t rows, size_t width,
+                    const Tensor &scale, float eps,
+                    std::vector<float> *output) {
+  output->resize(input.size());
+  for (size_t row = 0; row < rows; ++row) {
+    float sum = 0.0F;
+    for (size_t column = 0; column < width; ++column) {
+      const float value = input[row * width + column];
+      sum += value * value;
+    }
+    const float denominator = std::sqrt(sum / static_cast<float>(width)) + eps;
+    for (size_t column = 0; column < width; ++column)
+      (*output)[row * width + column] =
+          input[row * width + column] / denominator * scale.at(column);
+  }
+}
+
+// Grouped causal FIR with an explicit [channels, k-1] history (oldest first),
+// src/cpu/model.cpp:426-453 with update_fir_state :342-350.
+template <typename Tap, typename Direct>
+void fir_model(const std::vector<float> &input, size_t rows, size_t channels,
+               Tap tap_at, size_t groups, size_t kernel, bool causal,
+               Direct direct_at, bool has_direct, std::vector<float> *cache,
+               std::vector<float> *output) {
+  const size_t history = kernel - 1;
+  output->resize(input.size());
+  const size_t per_group = channels / groups;
+  for (size_t row = 0; row < rows; ++row) {
+    for (size_t channel = 0; channel < channels; ++channel) {
+      const size_t group = channel / per_group;
+      float total = 0.0F;
+      for (size_t old = 0; old < history; ++old) {
+        const size_t tap = causal ? kernel - 1 - old : old;
+        total += (*cache)[channel * history + old] * tap_at(group * kernel + tap);
+      }
+      const float current = input[row * channels + channel];
+      total += current * tap_at(group * kernel + (causal ? 0 : history));
+      if (has_direct)
+        total += direct_at(channel) * current;
+      (*output)[row * channels + channel] = total;
+      if (history != 0) {
+        float *begin = cache->data() + channel * history;
+        std::memmove(begin, begin + 1, (history - 1) * sizeof(float));
+        begin[history - 1] = current;
+      }
+    }
+  }
+}
+
+struct LayerState {
+  std::vector<float> short_state, inner_state, iir_state, key, value;
+};
+
+template <typename TapShort, typename TapInner, typename DirectAt,
+          typename PoleAt, typename ResidueAt>
+void hyena_model(Mixer type, const std::vector<float> &projection, size_t rows,
+                 size_t width, TapShort short_at, size_t short_len,
+                 TapInner inner_at, size_t hcs_groups, size_t hcs_len,
+                 size_t hcm_groups, size_t hcm_len, DirectAt direct_at,
+                 PoleAt log_pole_at, ResidueAt residue_at, size_t state_size,
+                 LayerState *cache, std::vector<float> *output) {
+  std::vector<float> filtered;
+  fir_model(projection, rows, width * 3, short_at, width * 3, short_len, false,
+            direct_at, false, &cache->short_state, &filtered);
+  std::vector<float> x2(rows * width), gated(rows * width);
+  for (size_t row = 0; row < rows; ++row) {
+    for (size_t channel = 0; channel < width; ++channel) {
+      const size_t source = row * width * 3 + channel * 3;
+      x2[row * width + channel] = filtered[source];
+      gated[row * width + channel] = filtered[source + 1] * filtered[source + 2];
+    }
+  }
+  std::vector<float> mixed;
+  if (type == Mixer::kHcs) {
+    fir_model(gated, rows, width, inner_at, hcs_groups, hcs_len, false,
+              direct_at, false, &cache->inner_state, &mixed);
+  } else if (type == Mixer::kHcm) {
+    fir_model(gated, rows, width, inner_at, hcm_groups, hcm_len, true,
+              direct_at, true, &cache->inner_state, &mixed);
+  } else {
+    mixed.resize(rows * width);
+    for (size_t row = 0; row < rows; ++row) {
+      for (size_t channel = 0; channel < width; ++channel) {
+        float modal = 0.0F;
+        for (size_t mode = 0; mode < state_size; ++mode) {
+          const size_t index = channel * state_size + mode;
+          cache->iir_state[index] =
+              std::exp(log_pole_at(index)) * cache->iir_state[index] +
+              gated[row * width + channel];
+          modal += residue_at(index) * cache->iir_state[index];
+        }
+        mixed[row * width + channel] =
+            modal + direct_at(channel) * gated[row * width + channel];
+      }
+    }
+  }
+  output->resize(rows * width);
+  for (size_t index = 0; index < output->size(); ++index)
+    (*output)[index] = x2[index] * mixed[index];
+}
+
+// Attention block body, src/cpu/model.cpp:455-544.
+void attention_model(const Model &m, const std::vector<float> &projected,
+                     size_t rows, const Layer &layer, LayerState *cache,
+                     std::vector<float> *output) {
+  const size_t width = m.width;
+  const size_t head_dim = width / m.heads;
+  std::vector<float> query(rows * width), key(rows * width),
+      value(rows * width);
+  for (size_t row = 0; row < rows; ++row)
+    for (size_t component = 0; component < 3; ++component)
+      for (size_t head = 0; head < m.heads; ++head)
+        for (size_t dimension = 0; dimension < head_dim; ++dimension) {
+          const size_t destination = row * width + head * head_dim + dimension;
+          const size_t source =
+              m.column_split
+                  ? head * 3 * head_dim + component * head_dim + dimension
+                  : component * width + head * head_dim + dimension;
+          const float item = projected[row * width * 3 + source];
+          (component == 0 ? query : component == 1 ? key : value)[destination] =
+              item;
+        }
+  const size_t prefix = cache->key.size() / width;
+  const size_t half = head_dim / 2;
+  for (size_t row = 0; row < rows; ++row) {
+    const float position = static_cast<float>(prefix + row) / m.rope_scale;
+    for (size_t head = 0; head < m.heads; ++head) {
+      const size_t base = row * width + head * head_dim;
+      for (size_t pair = 0; pair < half; ++pair) {
+        const float angle = position * layer.inv_freq->at(pair);
+        const float cosine = std::cos(angle);
+        const float sine = std::sin(angle);
+        for (std::vector<float> *tensor : {&query, &key}) {
+          const float first = (*tensor)[base + pair];
+          const float second = (*tensor)[base + half + pair];
+          (*tensor)[base + pair] = first * cosine - second * sine;
+          (*tensor)[base + half + pair] = second * cosine + first * sine;
+        }
+      }
+    }
+  }
+  cache->key.insert(cache->key.end(), key.begin(), key.end());
+  cache->value.insert(cache->value.end(), value.begin(), value.end());
+  output->assign(rows * width, 0.0F);
+  const float score_scale = 1.0F / std::sqrt(static_cast<float>(head_dim));
+  const long long jobs = static_cast<long long>(rows * m.heads);
+#pragma omp parallel for schedule(dynamic, 1)
+  for (long long job = 0; job < jobs; ++job) {
+    const size_t row = static_cast<size_t>(job) / m.heads;
+    const size_t head = static_cast<size_t>(job) % m.heads;
+    const size_t sources = prefix + row + 1;
+    std::vector<float> scores(sources);
+    const size_t query_base = row * width + head * head_dim;
+    float maximum = -std::numeric_limits<float>::infinity();
+    for (size_t source = 0; source < sources; ++source) {
+      float score = 0.0F;
+      const size_t key_base = source * width + head * head_dim;
+      for (size_t dimension = 0; dimension < head_dim; ++dimension)
+        score += query[query_base + dimension] * cache->key[key_base + dimension];
+      scores[source] = score * score_scale;
+      maximum = std::max(maximum, scores[source]);
+    }
+    float denominator = 0.0F;
+    for (auto &score : scores) {
+      score = std::exp(score - maximum);
+      denominator += score;
+    }
+    for (size_t dimension = 0; dimension < head_dim; ++dimension) {
+      float total = 0.0F;
+      for (size_t source = 0; source < sources; ++source)
+        total += scores[source] / denominator *
+                 cache->value[source * width + head * head_dim + dimension];
+      (*output)[query_base + dimension] = total;
+    }
+  }
+}
+
+int load_model(const char *path, Model *m) {
+  const int fd = open(path, O_RDONLY);
+  if (fd < 0)
+    return fail(std::string("cannot open ") + path);
+  struct stat info {};
+  if (fstat(fd, &info) != 0) {
+    close(fd);
+    return fail("cannot stat artifact");
+  }
+  m->map_size = static_cast<size_t>(info.st_size);
+  m->map = mmap(nullptr, m->map_size, PROT_READ, MAP_PRIVATE, fd, 0);
+  close(fd);
+  if (m->map == MAP_FAILED) {
+    m->map = nullptr;
+    return fail("mmap failed");
+  }
+  const auto *bytes = static_cast<const uint8_t *>(m->map);
+  uint64_t header = 0;
+  std::memcpy(&header, bytes, 8);
+  if (header + 8 > m->map_size)
+    return fail("header beyond file");
+  Json root;
+  JsonReader reader(reinterpret_cast<const char *>(bytes + 8),
+                    reinterpret_cast<const char *>(bytes + 8 + header));
+  if (!reader.value(&root) || root.kind != Json::kObject)
+    return fail("invalid header JSON");
+  const uint8_t *data = bytes + 8 + header;
+  for (const auto &member : root.members) {
+    if (member.first == "__metadata__") {
+      for (const auto &entry : member.second.members)
+        m->metadata[entry.first] = entry.second.text;
+      continue;
+    }
+    Tensor tensor;
+    tensor.dtype = member.second.get("dtype")->text;
+    for (const auto &d : member.second.get("shape")->items)
+      tensor.shape.push_back(static_cast<size_t>(d.number));
+    const auto &offsets = member.second.get("data_offsets")->items;
+    tensor.data = data + static_cast<size_t>(offsets[0].number);
+    tensor.bytes = static_cast<size_t>(offsets[1].number - offsets[0].number);
+    m->tensors[member.first] = tensor;
+  }
+  const std::pair<const char *, size_t *> sizes[] = {
+      {"config.vocab_size", &m->vocab},
+      {"config.hidden_size", &m->width},
+      {"config.num_layers", &m->layers},
+      {"config.num_attention_heads", &m->heads},
+      {"config.state_size", &m->state},
+      {"config.inner_mlp_size", &m->inner},
+      {"config.short_filter_length", &m->short_len},
+      {"config.hcs_filter_length", &m->hcs_len},
+      {"config.hcm_filter_length", &m->hcm_len},
+      {"config.hcs_filter_groups", &m->hcs_groups},
+      {"config.hcm_filter_groups", &m->hcm_groups}};
+  for (const auto &item : sizes)
+    if (!meta_u64(*m, item.first, item.second))
+      return fail(std::string("missing metadata ") + item.first);
+  if (!meta_f32(*m, "config.eps", &m->eps) ||
+      !meta_f32(*m, "config.rotary_emb_scaling_factor", &m->rope_scale))
+    return fail("missing eps/rope metadata");
+  auto split = m->metadata.find("config.column_split");
+  m->column_split = split != m->metadata.end() && split->second == "b:1";
+  std::vector<size_t> hcs, hcm, hcl, attn;
+  if (!meta_list(*m, "config.hcs_layer_idxs", &hcs) ||
+      !meta_list(*m, "config.hcm_layer_idxs", &hcm) ||
+      !meta_list(*m, "config.hcl_layer_idxs", &hcl) ||
+      !meta_list(*m, "config.attn_layer_idxs", &attn))
+    return fail("missing layer lists");
+  m->layer.assign(m->layers, Layer{});
+  for (auto i : hcm)
+    m->layer.at(i).type = Mixer::kHcm;
+  for (auto i : hcl)
+    m->layer.at(i).type = Mixer::kHcl;
+  for (auto i : attn)
+    m->layer.at(i).type = Mixer::kAttention;
+  const size_t w = m->width;
+  m->embedding = need(*m, "embedding_layer.weight", {m->vocab, w});
+  m->final_norm = need(*m, "norm.scale", {w});
+  if (m->embedding == nullptr || m->final_norm == nullptr)
+    return fail("missing embedding/final norm");
+  const size_t hd = w / m->heads;
+  for (size_t i = 0; i < m->layers; ++i) {
+    Layer &layer = m->layer[i];
+    const std::string p = "blocks." + std::to_string(i);
+    layer.pre_norm = need(*m, p + ".pre_norm.scale", {w});
+    layer.post_norm = need(*m, p + ".post_norm.scale", {w});
+    layer.l1 = need(*m, p + ".mlp.l1.weight", {m->inner, w});
+    layer.l2 = need(*m, p + ".mlp.l2.weight", {m->inner, w});
+    layer.l3 = need(*m, p + ".mlp.l3.weight", {w, m->inner});
+    if (layer.type == Mixer::kAttention) {
+      layer.projection = need(*m, p + ".inner_mha_cls.Wqkv.weight", {3 * w, w});
+      layer.out_weight = need(*m, p + ".inner_mha_cls.out_proj.weight", {w, w});
+      layer.out_bias = need(*m, p + ".inner_mha_cls.out_proj.bias", {w});
+      layer.inv_freq =
+          need(*m, p + ".inner_mha_cls.rotary_emb.inv_freq", {hd / 2});
+      if (!layer.inv_freq)
+        return fail("missing inv_freq for " + p);
+    } else {
+      layer.projection = need(*m, p + ".projections.weight", {3 * w, w});
+      layer.out_weight = need(*m, p + ".out_filter_dense.weight", {w, w});
+      layer.out_bias = need(*m, p + ".out_filter_dense.bias", {w});
+      layer.short_filter =
+          need(*m, p + ".filter.short_filter_weight", {3 * w, 1, m->short_len});
+      if (!layer.short_filter)
+        return fail("missing short filter for " + p);
+      if (layer.type == Mixer::kHcs) {
+        layer.inner_filter =
+            need(*m, p + ".filter.h", {m->hcs_groups, 1, m->hcs_len});
+        if (!layer.inner_filter)
+          return fail("missing HCS filter for " + p);
+      } else {
+        layer.direct = need(*m, p + ".filter.D", {w});
+        if (!layer.direct)
+          return fail("missing D for " + p);
+        if (layer.type == Mixer::kHcm) {
+          layer.inner_filter =
+              need(*m, p + ".filter.h", {m->hcm_groups, 1, m->hcm_len});
+          if (!layer.inner_filter)
+            return fail("missing HCM filter for " + p);
+        } else {
+          layer.log_poles = need(*m, p + ".filter.log_poles", {w, m->state, 1});
+          layer.residues = need(*m, p + ".filter.residues", {w, m->state});
+          if (!layer.log_poles || !layer.residues)
+            return fail("missing HCL filter for " + p);
+        }
+      }
+      if (layer.projection && layer.projection->dtype == "F8_E4M3") {
+        const Tensor *scales =
+            need(*m, p + ".projections.fp8_runtime_scales", {2});
+        if (!scales)
+          return fail("missing fp8 runtime scales for " + p);
+        layer.fp8_input_scale = scales->at(0);
+        layer.fp8_output_scale = scales->at(1);
+      }
+    }
+    if (!layer.pre_norm || !layer.post_norm || !layer.l1 || !layer.l2 ||
+        !layer.l3 || !layer.projection || !layer.out_weight || !layer.out_bias)
+      return fail("missing tensors for " + p);
+  }
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *oracle_last_error(void) { return g_error.c_str(); }
+
+uint8_t oracle_e4m3_encode(const float value) {
+  const bool negative = std::signbit(value);
+  const auto sign = static_cast<uint8_t>(negative ? 0x80U : 0x00U);
+  if (std::isnan(value))
+    return static_cast<uint8_t>(sign | 0x7fU);
+  const float magnitude = std::fabs(value);
+  if (!std::isfinite(magnitude) || magnitude >= 448.0F)
+    return static_cast<uint8_t>(sign | 0x7eU);
+  // Largest code whose value does not exceed the magnitude, found by
+  // bisection over the monotone positive code range [0, 0x7e].
+  unsigned low = 0, high = 0x7e;
+  while (high - low > 1U) {
+    const unsigned mid = (low + high) / 2U;
+    if (e4m3_positive(static_cast<uint8_t>(mid)) <= magnitude)
+      low = mid;
+    else
+      high = mid;
+  }
+  const float below = magnitude - e4m3_positive(static_cast<uint8_t>(low));
+  const float above = e4m3_positive(static_cast<uint8_t>(high)) - magnitude;
+  unsigned chosen = low;
+  if (above < below || (above == below && (high & 1U) == 0U))
+    chosen = high;
+  return static_cast<uint8_t>(sign | chosen);
+}
+
+float oracle_e4m3_decode(const uint8_t code) {
+  const auto magnitude = static_cast<uint8_t>(code & 0x7fU);
+  const float sign = (code & 0x80U) == 0U ? 1.0F : -1.0F;
+  if (magnitude == 0x7fU)
+    return std::copysign(std::numeric_limits<float>::quiet_NaN(), sign);
+  return std::copysign(e4m3_positive(magnitude), sign);
+}
+
+void oracle_e4m3_quantize_f32(const float *x, size_t n, float scale,
+                              uint8_t *codes) {
+  for (size_t i = 0; i < n; ++i)
+    codes[i] = oracle_e4m3_encode(
+        bf16_bits_to_float(float_to_bf16_rne(x[i])) * scale);
+}
+
+void oracle_e4m3_quantize_bf16(const uint16_t *x, size_t n, float scale,
+                               uint8_t *codes) {
+  for (size_t i = 0; i < n; ++i)
+    codes[i] = oracle_e4m3_encode(bf16_bits_to_float(x[i]) * scale);
+}
+
+int oracle_qgmma_linear(const uint8_t *input_codes, const uint8_t *weight_codes,
+                        size_t rows, size_t inner, size_t cols,
+                        float output_scale, size_t group_k, float *out) {
+  if (group_k == 0 || inner % group_k != 0)
+    return fail("qgmma inner dimension must be a multiple of the group");
+  std::vector<float> a(inner), b(inner);
+  for (size_t row = 0; row < rows; ++row) {
+    for (size_t k = 0; k < inner; ++k)
+      a[k] = oracle_e4m3_decode(input_codes[row * inner + k]);
+    for (size_t col = 0; col < cols; ++col) {
+      for (size_t k = 0; k < inner; ++k)
+        b[k] = oracle_e4m3_decode(weight_codes[col * inner + k]);
+      float acc = 0.0F;
+      for (size_t start = 0; start < inner; start += group_k) {
+        int top = acc == 0.0F ? -1024 : unbiased_exponent(acc);
+        for (size_t k = start; k < start + group_k; ++k)
+          if (a[k] != 0.0F && b[k] != 0.0F)
+            top = std::max(top, unbiased_exponent(a[k]) + unbiased_exponent(b[k]));
+        int32_t sum =
+            acc == 0.0F ? 0 : align_to(acc, unbiased_exponent(acc), top, false);
+        for (size_t k = start; k < start + group_k; ++k)
+          if (a[k] != 0.0F && b[k] != 0.0F)
+            sum += align_to(a[k] * b[k],
+                            unbiased_exponent(a[k]) + unbiased_exponent(b[k]),
+                            top, true);
+        acc = sum == 0 ? 0.0F
+                       : bits_to_float(float_bits(std::ldexp(
+                                           static_cast<float>(sum), top - 13)) &
+                                       0xfffffc00U);
+      }
+      out[row * cols + col] =
+          bf16_bits_to_float(float_to_bf16_rne(acc * output_scale));
+    }
+  }
+  return 0;
+}
+
+int oracle_rms_norm(const float *x, size_t rows, size_t width,
+                    const float *scale, float eps, float *out) {
+  for (size_t row = 0; row < rows; ++row) {
+    float sum = 0.0F;
+    for (size_t c = 0; c < width; ++c)
+      sum += x[row * width + c] * x[row * width + c];
+    const float denominator = std::sqrt(sum / static_cast<float>(width)) + eps;
+    for (size_t c = 0; c < width; ++c)
+      out[row * width + c] = x[row * width + c] / denominator * scale[c];
+  }
+  return 0;
+}
+
+int oracle_linear_f32(const float *x, size_t rows, size_t in_features,
+                      const float *weight, size_t out_features,
+                      const float *bias, float *out) {
+  for (size_t row = 0; row < rows; ++row)
+    for (size_t o = 0; o < out_features; ++o) {
+      float total = bias == nullptr ? 0.0F : bias[o];
+      for (size_t i = 0; i < in_features; ++i)
+        total += x[row * in_features + i] * weight[o * in_features + i];
+      out[row * out_features + o] = total;
+    }
+  return 0;
+}
+
+int oracle_gated_mlp_f32(const float *x, size_t rows, size_t width,
+                         size_t inner, const float *l1, const float *l2,
+                         const float *l3, int gelu, float *out) {
+  std::vector<float> first(rows * inner), second(rows * inner);
+  oracle_linear_f32(x, rows, width, l1, inner, nullptr, first.data());
+  oracle_linear_f32(x, rows, width, l2, inner, nullptr, second.data());
+  for (size_t i = 0; i < first.size(); ++i)
+    first[i] = (gelu ? gelu_erf(first[i]) : first[i]) * second[i];
+  return oracle_linear_f32(first.data(), rows, inner, l3, width, nullptr, out);
+}
+
+int oracle_causal_fir(const float *x, size_t length, size_t channels,
+                      const float *weight, size_t kernel, const float *bias,
+                      int orientation, int bias_mode, float *out) {
+  for (size_t t = 0; t < length; ++t)
+    for (size_t c = 0; c < channels; ++c) {
+      float total = (bias == nullptr || bias_mode == 1) ? 0.0F : bias[c];
+      for (size_t tap = 0; tap < kernel; ++tap) {
+        const size_t delay = orientation == 0 ? kernel - 1 - tap : tap;
+        if (t >= delay)
+          total += x[(t - delay) * channels + c] * weight[c * kernel + tap];
+      }
+      if (bias != nullptr && bias_mode == 1)
+        total += bias[c] * x[t * channels + c];
+      out[t * channels + c] = total;
+    }
+  return 0;
+}
+
+int oracle_hcl_recurrence(const float *x2, const float *x1, const float *v,
+                          size_t length, size_t width, const float *direct,
+                          const float *log_poles, const float *residues,
+                          size_t state_size, float *state, float *out) {
+  for (size_t t = 0; t < length; ++t)
+    for (size_t c = 0; c < width; ++c) {
+      const size_t i = t * width + c;
+      const float u = x1[i] * v[i];
+      float modal = 0.0F;
+      for (size_t m = 0; m < state_size; ++m) {
+        const size_t s = c * state_size + m;
+        state[s] = std::exp(log_poles[s]) * state[s] + u;
+        modal += residues[s] * state[s];
+      }
+      out[i] = x2[i] * (modal + direct[c] * u);
+    }
+  return 0;
+}
+
+int oracle_apply_rope(float *q, float *k, size_t length, size_t heads,
+                      size_t head_dim, const float *inv_freq,
+                      size_t position_offset, float position_scale) {
+  const size_t half = head_dim / 2;
+  for (float *tensor : {q, k})
+    for (size_t t = 0; t < length; ++t) {
+      const float position =
+          static_cast<float>(position_offset + t) / position_scale;
+      for (size_t h = 0; h < heads; ++h) {
+        const size_t base = (t * heads + h) * head_dim;
+        for (size_t d = 0; d < half; ++d) {
+          const float angle = position * inv_freq[d];
+          const float cosine = std::cos(angle), sine = std::sin(angle);
+          const float first = tensor[base + d], second = tensor[base + half + d];
+          tensor[base + d] = first * cosine - second * sine;
+          tensor[base + half + d] = second * cosine + first * sine;
+        }
+      }
+    }
+  return 0;
+}
+
+int oracle_causal_attention(const float *q, const float *k, const float *v,
+                            size_t length, size_t heads, size_t head_dim,
+                            float *out) {
+  std::fill(out, out + length * heads * head_dim, 0.0F);
+  std::vector<float> scores(length);
+  const float scale = 1.0F / std::sqrt(static_cast<float>(head_dim));
+  for (size_t t = 0; t < length; ++t)
+    for (size_t h = 0; h < heads; ++h) {
+      float maximum = -std::numeric_limits<float>::infinity();
+      const size_t qb = (t * heads + h) * head_dim;
+      for (size_t s = 0; s <= t; ++s) {
+        const size_t kb = (s * heads + h) * head_dim;
+        float dot = 0.0F;
+        for (size_t d = 0; d < head_dim; ++d)
+          dot += q[qb + d] * k[kb + d];
+        scores[s] = dot * scale;
+        maximum = std::max(maximum, scores[s]);
+      }
+      float denominator = 0.0F;
+      for (size_t s = 0; s <= t; ++s) {
+        scores[s] = std::exp(scores[s] - maximum);
+        denominator += scores[s];
+      }
+      for (size_t s = 0; s <= t; ++s) {
+        const float p = scores[s] / denominator;
+        const size_t vb = (s * heads + h) * head_dim;
+        for (size_t d = 0; d < head_dim; ++d)
+          out[qb + d] += p * v[vb + d];
+      }
+    }
+  return 0;
+}
+
+int oracle_linear_bf16w(const float *x, size_t rows, size_t in_features,
+                        const uint16_t *weight, size_t out_features,
+                        const uint16_t *bias, float *out, int threads) {
+  const long long total = static_cast<long long>(rows * out_features);
+#pragma omp parallel for schedule(static) num_threads(threads > 0 ? threads : 1)
+  for (long long item = 0; item < total; ++item) {
+    const size_t row = static_cast<size_t>(item) / out_features;
+    const size_t o = static_cast<size_t>(item) % out_features;
+    float value = dot_bf16(x + row * in_features, weight + o * in_features,
+                           in_features);
+    if (bias != nullptr)
+      value += bf16_bits_to_float(bias[o]);
+    out[static_cast<size_t>(item)] = value;
+  }
+  return 0;
+}
+
+int oracle_hyena_mixer(int kind, const float *projection, size_t length,
+                       size_t width, const float *short_w, size_t short_len,
+                       const float *inner_w, size_t groups, size_t inner_len,
+                       const float *direct, const float *log_poles,
+                       const float *residues, size_t state_size, float *out) {
+  if (kind < 0 || kind > 2)
+    return fail("hyena kind must be 0 (HCS), 1 (HCM) or 2 (HCL)");
+  LayerState cache;
+  cache.short_state.assign(width * 3 * (short_len - 1), 0.0F);
+  if (kind != 2)
+    cache.inner_state.assign(width * (inner_len - 1), 0.0F);
+  else
+    cache.iir_state.assign(width * state_size, 0.0F);
+  std::vector<float> input(projection, projection + length * 3 * width);
+  std::vector<float> output;
+  auto at = [](const float *p) { return [p](size_t i) { return p[i]; }; };
+  auto none = [](size_t) { return 0.0F; };
+  const Mixer type = kind == 0 ? Mixer::kHcs : kind == 1 ? Mixer::kHcm
+                                                         : Mixer::kHcl;
+  if (kind == 2) {
+    hyena_model(type, input, length, width, at(short_w), short_len, none, 1,
+                2, 1, 2, at(direct), at(log_poles), at(residues), state_size,
+                &cache, &output);
+  } else if (kind == 1) {
+    hyena_model(type, input, length, width, at(short_w), short_len, at(inner_w),
+                1, 2, groups, inner_len, at(direct), none, none, 0, &cache,
+                &output);
+  } else {
+    hyena_model(type, input, length, width, at(short_w), short_len, at(inner_w),
+                groups, inner_len, 1, 2, none, none, none, 0, &cache, &output);
+  }
+  std::copy(output.begin(), output.end(), out);
+  return 0;
+}
+
+void *oracle_model_load(const char *path, char *error, size_t error_size) {
+  auto model = std::make_unique<Model>();
+  if (load_model(path, model.get()) != 0) {
+    if (error != nullptr && error_size != 0)
+      std::snprintf(error, error_size, "%s", g_error.c_str());
+    return nullptr;
+  }
+  return model.release();
+}
+
+void oracle_model_free(void *model) { delete static_cast<Model *>(model); }
+size_t oracle_model_width(const void *m) {
+  return static_cast<const Model *>(m)->width;
+}
+size_t oracle_model_vocab(const void *m) {
+  return static_cast<const Model *>(m)->vocab;
+}
+size_t oracle_model_layers(const void *m) {
+  return static_cast<const Model *>(m)->layers;
+}
+
+int oracle_model_prefill(void *model_handle, const uint32_t *tokens, size_t n,
+                         size_t chunk, float *logits, size_t capture_layer,
+                         float *capture, int threads) {
+  auto &m = *static_cast<Model *>(model_handle);
+  if (n == 0 || chunk == 0)
+    return fail("prefill needs tokens and a positive chunk");
+#ifdef _OPENMP
+  omp_set_num_threads(threads > 0 ? threads : 1);
+#endif
+  const size_t w = m.width;
+  std::vector<LayerState> state(m.layers);
+  for (size_t i = 0; i < m.layers; ++i) {
+    const auto type = m.layer[i].type;
+    if (type == Mixer::kAttention)
+      continue;
+    state[i].short_state.assign(w * 3 * (m.short_len - 1), 0.0F);
+    if (type == Mixer::kHcs)
+      state[i].inner_state.assign(w * (m.hcs_len - 1), 0.0F);
+    else if (type == Mixer::kHcm)
+      state[i].inner_state.assign(w * (m.hcm_len - 1), 0.0F);
+    else
+      state[i].iir_state.assign(w * m.state, 0.0F);
+  }
+  for (size_t offset = 0; offset < n; offset += chunk) {
+    const size_t rows = std::min(chunk, n - offset);
+    std::vector<float> hidden(rows * w);
+    for (size_t r = 0; r < rows; ++r) {
+      const uint32_t token = tokens[offset + r];
+      if (token >= m.vocab)
+        return fail("token exceeds model vocabulary");
+      for (size_t c = 0; c < w; ++c)
+        hidden[r * w + c] = m.embedding->at(static_cast<size_t>(token) * w + c);
+    }
+    std::vector<float> normalized, mixed, residual, first, second, gated;
+    for (size_t index = 0; index < m.layers; ++index) {
+      const Layer &layer = m.layer[index];
+      rms_norm_model(hidden, rows, w, *layer.pre_norm, m.eps, &normalized);
+      std::vector<float> projected;
+      if (layer.projection->dtype == "F8_E4M3")
+        linear_fp8(normalized, rows, w, *layer.projection, 3 * w,
+                   layer.fp8_input_scale, layer.fp8_output_scale, &projected,
+                   threads);
+      else
+        linear_model(normalized, rows, w, *layer.projection, 3 * w, nullptr,
+                     &projected, threads);
+      if (layer.type == Mixer::kAttention) {
+        attention_model(m, projected, rows, layer, &state[index], &mixed);
+      } else {
+        const Tensor *inner = layer.inner_filter;
+        const Tensor *sf = layer.short_filter;
+        const Tensor *dir = layer.direct;
+        const Tensor *lp = layer.log_poles;
+        const Tensor *res = layer.residues;
+        hyena_model(
+            layer.type, projected, rows, w,
+            [sf](size_t i) { return sf->at(i); }, m.short_len,
+            [inner](size_t i) { return inner->at(i); }, m.hcs_groups, m.hcs_len,
+            m.hcm_groups, m.hcm_len, [dir](size_t i) { return dir->at(i); },
+            [lp](size_t i) { return lp->at(i); },
+            [res](size_t i) { return res->at(i); }, m.state, &state[index],
+            &mixed);
+      }
+      linear_model(mixed, rows, w, *layer.out_weight, w, layer.out_bias,
+                   &residual, threads);
+      for (size_t i = 0; i < residual.size(); ++i)
+        residual[i] += hidden[i];
+      rms_norm_model(residual, rows, w, *layer.post_norm, m.eps, &normalized);
+      linear_model(normalized, rows, w, *layer.l1, m.inner, nullptr, &first,
+                   threads);
+      linear_model(normalized, rows, w, *layer.l2, m.inner, nullptr, &second,
+                   threads);
+      gated.resize(first.size());
+      for (size_t i = 0; i < gated.size(); ++i) {
+        const float activated = index == 0 ? gelu_erf(first[i]) : first[i];
+        gated[i] = activated * second[i];
+      }
+      linear_model(gated, rows, m.inner, *layer.l3, w, nullptr, &hidden,
+                   threads);
+      for (size_t i = 0; i < hidden.size(); ++i)
+        hidden[i] += residual[i];
+      if (capture != nullptr && capture_layer == index)
+        std::copy(hidden.begin(), hidden.end(), capture + offset * w);
+    }
+    rms_norm_model(hidden, rows, w, *m.final_norm, m.eps, &normalized);
+    std::vector<float> chunk_logits;
+    linear_model(normalized, rows, w, *m.embedding, m.vocab, nullptr,
+                 &chunk_logits, threads);
+    std::copy(chunk_logits.begin(), chunk_logits.end(),
+              logits + offset * m.vocab);
+  }
+  return 0;
+}
+
+}  // extern "C"
