@@ -1,0 +1,70 @@
+// SPDX-License-Identifier: Apache-2.0
+// Shared device/host helpers for the gfx950 StripedHyena2 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "status.hpp"
+
+namespace evo::hip {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+// ---- BF16 helpers (raw 16-bit storage; round to nearest even).
+__host__ __device__ inline float bf16_to_f32(const uint16_t bits) {
+  return __builtin_bit_cast(float, static_cast<uint32_t>(bits) << 16U);
+}
+
+__host__ __device__ inline uint16_t f32_to_bf16(const float value) {
+  const uint32_t bits = __builtin_bit_cast(uint32_t, value);
+  if ((bits & 0x7fffffffU) > 0x7f800000U)
+    return static_cast<uint16_t>((bits >> 16U) | 0x40U);
+  return static_cast<uint16_t>((bits + 0x7fffU + ((bits >> 16U) & 1U)) >> 16U);
+}
+
+__host__ __device__ inline float round_bf16(const float value) {
+  return bf16_to_f32(f32_to_bf16(value));
+}
+
+// ---- Activation storage type of the inter-kernel tensors.
+enum class IoType : int { kF32 = 0, kBF16 = 1 };
+
+template <typename T> __device__ inline float load_act(const T *p, size_t i);
+template <> __device__ inline float load_act<float>(const float *p, size_t i) {
+  return p[i];
+}
+template <>
+__device__ inline float load_act<uint16_t>(const uint16_t *p, size_t i) {
+  return bf16_to_f32(p[i]);
+}
+template <typename T> __device__ inline void store_act(T *p, size_t i, float v);
+template <> __device__ inline void store_act<float>(float *p, size_t i, float v) {
+  p[i] = v;
+}
+template <>
+__device__ inline void store_act<uint16_t>(uint16_t *p, size_t i, float v) {
+  p[i] = f32_to_bf16(v);
+}
+
+inline Status hip_status(const hipError_t error, const char *what) {
+  if (error == hipSuccess)
+    return Status::Ok();
+  return {ErrorCode::kHip, std::string(what) + ": " + hipGetErrorString(error)};
+}
+
+inline Status launch_status(const char *kernel) {
+  return hip_status(hipGetLastError(), kernel);
+}
+
+inline unsigned ceil_div(const size_t a, const size_t b) {
+  return static_cast<unsigned>((a + b - 1) / b);
+}
+
+}  // namespace evo::hip

@@ -1,0 +1,126 @@
+// SPDX-License-Identifier: Apache-2.0
+// Embedding gather, RMSNorm and FIR-history maintenance.
+//
+// RMSNorm follows evo.cpp `src/cpu_reference.cpp:61-98` /
+// `src/cpu/model.cpp:316-334`: y = x / (sqrt(mean(x^2)) + eps) * scale, the
+// epsilon added after the square root. One 256-thread block per row; each
+// thread reads 16-byte vectors, the sum of squares is reduced with wave
+// shuffles and one LDS exchange (F32 throughout).
+#include "common.hpp"
+#include "ops.hpp"
+
+namespace evo::hip {
+namespace {
+
+__global__ void embed_kernel(const uint32_t *__restrict__ tokens, size_t rows,
+                             const uint16_t *__restrict__ table, size_t width,
+                             float *__restrict__ out) {
+  const size_t n = rows * width;
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
+       i < n; i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    const size_t row = i / width, col = i % width;
+    out[i] = bf16_to_f32(table[static_cast<size_t>(tokens[row]) * width + col]);
+  }
+}
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1)
+    v += __shfl_xor(v, offset, 64);
+  return v;
+}
+
+__global__ __launch_bounds__(256) void rms_norm_kernel(
+    const float *__restrict__ x, size_t width, const float *__restrict__ scale,
+    float eps, float *__restrict__ out) {
+  __shared__ float partial[4];
+  const size_t row = blockIdx.x;
+  const float *src = x + row * width;
+  float *dst = out + row * width;
+  float sum = 0.0F;
+  const bool vec = (width % 4) == 0;
+  if (vec) {
+    for (size_t c = threadIdx.x * 4; c < width; c += 256 * 4) {
+      const float4 v = *reinterpret_cast<const float4 *>(src + c);
+      sum += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    }
+  } else {
+    for (size_t c = threadIdx.x; c < width; c += 256)
+      sum += src[c] * src[c];
+  }
+  sum = wave_sum(sum);
+  if ((threadIdx.x & 63) == 0)
+    partial[threadIdx.x >> 6] = sum;
+  __syncthreads();
+  const float total = partial[0] + partial[1] + partial[2] + partial[3];
+  const float denominator = sqrtf(total / static_cast<float>(width)) + eps;
+  if (vec) {
+    for (size_t c = threadIdx.x * 4; c < width; c += 256 * 4) {
+      const float4 v = *reinterpret_cast<const float4 *>(src + c);
+      const float4 s = *reinterpret_cast<const float4 *>(scale + c);
+      *reinterpret_cast<float4 *>(dst + c) =
+          make_float4(v.x / denominator * s.x, v.y / denominator * s.y,
+                      v.z / denominator * s.z, v.w / denominator * s.w);
+    }
+  } else {
+    for (size_t c = threadIdx.x; c < width; c += 256)
+      dst[c] = src[c] / denominator * scale[c];
+  }
+}
+
+// history[h, c] <- row h of the last H rows of [history ; x]. Each thread owns
+// one channel and walks h upwards, so an old row is read before it is
+// overwritten (it only moves to a lower index).
+__global__ void update_history_kernel(const float *__restrict__ x, size_t rows,
+                                      size_t channels, float *history,
+                                      size_t history_rows) {
+  const size_t c = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
+  if (c >= channels)
+    return;
+  for (size_t h = 0; h < history_rows; ++h) {
+    const size_t source = h + rows;  // index into [history ; x]
+    history[h * channels + c] = source < history_rows
+                                    ? history[source * channels + c]
+                                    : x[(source - history_rows) * channels + c];
+  }
+}
+
+}  // namespace
+
+Status embed_tokens(const uint32_t *tokens, size_t rows, const uint16_t *table,
+                    size_t vocab, size_t width, float *out, hipStream_t stream) {
+  (void)vocab;  // token ids are validated on the host before upload
+  if (tokens == nullptr || table == nullptr || out == nullptr || rows == 0 ||
+      width == 0)
+    return {ErrorCode::kInvalidArgument, "embed_tokens: invalid arguments"};
+  const size_t n = rows * width;
+  const unsigned grid = static_cast<unsigned>(std::min<size_t>((n + 255) / 256, 16384));
+  hipLaunchKernelGGL(embed_kernel, dim3(grid), dim3(256), 0, stream, tokens, rows,
+                     table, width, out);
+  return launch_status("embed_kernel");
+}
+
+Status rms_norm(const float *x, size_t rows, size_t width, const float *scale,
+                float eps, float *out, hipStream_t stream) {
+  if (x == nullptr || scale == nullptr || out == nullptr || rows == 0 ||
+      width == 0 || rows > (1U << 31))
+    return {ErrorCode::kInvalidArgument, "rms_norm: invalid arguments"};
+  hipLaunchKernelGGL(rms_norm_kernel, dim3(static_cast<unsigned>(rows)), dim3(256),
+                     0, stream, x, width, scale, eps, out);
+  return launch_status("rms_norm_kernel");
+}
+
+Status update_history(const float *x, size_t rows, size_t channels,
+                      float *history, size_t history_rows, float *scratch,
+                      hipStream_t stream) {
+  (void)scratch;
+  if (history_rows == 0)
+    return Status::Ok();
+  if (x == nullptr || history == nullptr || rows == 0 || channels == 0)
+    return {ErrorCode::kInvalidArgument, "update_history: invalid arguments"};
+  hipLaunchKernelGGL(update_history_kernel, dim3(ceil_div(channels, 256)), dim3(256),
+                     0, stream, x, rows, channels, history, history_rows);
+  return launch_status("update_history_kernel");
+}
+
+}  // namespace evo::hip

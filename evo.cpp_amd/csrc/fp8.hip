@@ -1,0 +1,341 @@
+// SPDX-License-Identifier: Apache-2.0
+// Software-FP8 projection executor on gfx950.
+//
+// Quantiser: code = E4M3FN(float(bf16(x)) * scale), round to nearest even,
+// saturating finite overflow and infinities to +-448, NaN -> 0x7f|sign, sign
+// kept on values rounding to zero. This is the code set of evo.cpp
+// `src/fp8.cpp:26-58` (the reference searches the code table; here the code is
+// computed from the binade: subnormals as rint(m * 2^9), normals as
+// rint(m * 2^(3-e)) offset by the exponent field, which yields the same code
+// including tie-to-even on the code's low bit). Applied to BF16 activations
+// as in `src/cuda/ops.cu:250-262`.
+//
+// GEMM, three modes over E4M3 codes A [M,K] and W [N,K]:
+//  * exact: the integer QGMMA emulation of `src/cuda/ops.cu:277-441` -- per
+//    K=32 group the maximum exponent over the accumulator and all nonzero
+//    products, every term aligned to 13 fractional bits and truncated, one
+//    integer sum, E8M13 truncation of the normalised result;
+//  * mfma-k32 / mfma-k128: OCP-E4M3 MFMA (v_mfma_f32_32x32x16_fp8_fp8 or
+//    v_mfma_scale_f32_32x32x64_f8f6f4 with unit scales) computes each K chunk
+//    exactly-rounded in F32; the chunk is then promoted into the running
+//    accumulator, which is truncated to E8M13 after every promotion like the
+//    reference's. Per-term truncation inside a chunk is not reproduced, so
+//    results differ from exact mode by a few E8M13 ulps.
+// All modes finish with bf16(acc * output_scale).
+#include "common.hpp"
+#include "ops.hpp"
+
+namespace evo::hip {
+namespace {
+
+__host__ __device__ inline uint8_t encode_e4m3(const float value) {
+  const uint32_t bits = __builtin_bit_cast(uint32_t, value);
+  const uint8_t sign = (bits >> 24U) & 0x80U;
+  const uint32_t abs_bits = bits & 0x7fffffffU;
+  if (abs_bits > 0x7f800000U)
+    return sign | 0x7fU;
+  const float magnitude = __builtin_bit_cast(float, abs_bits);
+  if (magnitude >= 448.0F)
+    return sign | 0x7eU;
+  if (magnitude < 0.015625F) {  // below 2^-6: subnormal step 2^-9
+    return sign | static_cast<uint8_t>(rintf(magnitude * 512.0F));
+  }
+  const int exponent = static_cast<int>(abs_bits >> 23U) - 127;  // -6..8
+  const float scaled = ldexpf(magnitude, 3 - exponent);          // [8, 16)
+  const int q = static_cast<int>(rintf(scaled));                 // 8..16
+  return sign | static_cast<uint8_t>(((exponent + 7) << 3) + (q - 8));
+}
+
+__global__ void quantize_f32_kernel(const float *__restrict__ x, size_t n,
+                                    float scale, uint8_t *__restrict__ codes) {
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
+       i < n; i += static_cast<size_t>(gridDim.x) * blockDim.x)
+    codes[i] = encode_e4m3(round_bf16(x[i]) * scale);
+}
+
+__global__ void quantize_bf16_kernel(const uint16_t *__restrict__ x, size_t n,
+                                     float scale, uint8_t *__restrict__ codes) {
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
+       i < n; i += static_cast<size_t>(gridDim.x) * blockDim.x)
+    codes[i] = encode_e4m3(bf16_to_f32(x[i]) * scale);
+}
+
+// Packed integer form of a code: 4-bit significand (bits 0-4), exponent + 16
+// (bits 5-9), sign (bit 10); value = significand/8 * 2^exponent.
+__device__ inline uint16_t pack_code(const uint8_t code) {
+  const unsigned field = (code >> 3U) & 0x0fU;
+  const unsigned mantissa = code & 0x07U;
+  int exponent;
+  unsigned significand;
+  if (field == 0U) {
+    if (mantissa == 0U)
+      return 0U;
+    const int lead = 31 - __clz(mantissa);
+    exponent = lead - 9;
+    significand = mantissa << (3 - lead);
+  } else {
+    exponent = static_cast<int>(field) - 7;
+    significand = 8U + mantissa;
+  }
+  return static_cast<uint16_t>(significand | ((exponent + 16) << 5) |
+                               ((code & 0x80U) ? 0x400U : 0U));
+}
+
+__device__ inline float truncate_e8m13(const float v) {
+  return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v) & 0xfffffc00U);
+}
+
+__device__ inline int float_exponent(const float v) {
+  return static_cast<int>((__builtin_bit_cast(uint32_t, v) >> 23U) & 0xffU) - 127;
+}
+
+// Exact QGMMA: 16x16 outputs per 256-thread block, one output per thread.
+constexpr int kExactTile = 16;
+constexpr int kGroup = 32;
+
+__global__ __launch_bounds__(256) void qgmma_exact_kernel(
+    const uint8_t *__restrict__ a, const uint8_t *__restrict__ w,
+    float *__restrict__ out, int M, int N, int K, float output_scale) {
+  __shared__ uint16_t a_tile[kExactTile][kGroup];
+  __shared__ uint16_t w_tile[kGroup][kExactTile + 1];
+  const int t = threadIdx.x;
+  const int lr = t / kExactTile, lc = t % kExactTile;
+  const int row = blockIdx.y * kExactTile + lr;
+  const int col = blockIdx.x * kExactTile + lc;
+  float acc = 0.0F;
+  for (int k0 = 0; k0 < K; k0 += kGroup) {
+    for (int i = t; i < kExactTile * kGroup; i += 256) {
+      const int r = i / kGroup, k = i % kGroup;
+      const int gr = blockIdx.y * kExactTile + r;
+      const int gc = blockIdx.x * kExactTile + r;
+      a_tile[r][k] = gr < M ? pack_code(a[static_cast<size_t>(gr) * K + k0 + k]) : 0;
+      w_tile[k][r] = gc < N ? pack_code(w[static_cast<size_t>(gc) * K + k0 + k]) : 0;
+    }
+    __syncthreads();
+    int top = acc == 0.0F ? -1024 : float_exponent(acc);
+#pragma unroll
+    for (int k = 0; k < kGroup; ++k) {
+      const uint16_t l = a_tile[lr][k], r = w_tile[k][lc];
+      if ((l & 0x1fU) && (r & 0x1fU))
+        top = max(top, static_cast<int>((l >> 5) & 0x1fU) +
+                           static_cast<int>((r >> 5) & 0x1fU) - 32);
+    }
+    int32_t sum = 0;
+    if (acc != 0.0F) {
+      const uint32_t bits = __builtin_bit_cast(uint32_t, acc);
+      uint32_t significand = ((bits & 0x7fffffU) | 0x800000U) >> 10U;
+      const int shift = top - float_exponent(acc);
+      significand = shift > 31 ? 0U : (significand >> shift);
+      sum = (bits & 0x80000000U) ? -static_cast<int32_t>(significand)
+                                 : static_cast<int32_t>(significand);
+    }
+#pragma unroll
+    for (int k = 0; k < kGroup; ++k) {
+      const uint16_t l = a_tile[lr][k], r = w_tile[k][lc];
+      if ((l & 0x1fU) && (r & 0x1fU)) {
+        const int shift = top - (static_cast<int>((l >> 5) & 0x1fU) +
+                                 static_cast<int>((r >> 5) & 0x1fU) - 32);
+        if (shift <= 31) {
+          const uint32_t value = ((l & 0x1fU) * (r & 0x1fU) * 128U) >> shift;
+          sum += ((l ^ r) & 0x400U) ? -static_cast<int32_t>(value)
+                                    : static_cast<int32_t>(value);
+        }
+      }
+    }
+    acc = sum == 0 ? 0.0F : truncate_e8m13(ldexpf(static_cast<float>(sum), top - 13));
+    __syncthreads();
+  }
+  if (row < M && col < N)
+    out[static_cast<size_t>(row) * N + col] = round_bf16(acc * output_scale);
+}
+
+// MFMA path. Block 128x128 outputs, 4 waves of 64x64 (2x2 tiles 32x32),
+// K staged 128 bytes per step through LDS rows padded to 144 B.
+constexpr int kBM = 128, kBN = 128, kBK = 128, kStride = kBK + 16;
+
+template <int kChunk>
+__global__ __launch_bounds__(256) void fp8_mfma_kernel(
+    const uint8_t *__restrict__ a, const uint8_t *__restrict__ w,
+    float *__restrict__ out, int M, int N, int K, float output_scale) {
+  __shared__ __attribute__((aligned(16))) uint8_t a_s[kBM * kStride];
+  __shared__ __attribute__((aligned(16))) uint8_t w_s[kBN * kStride];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wave_m = wave >> 1, wave_n = wave & 1;
+  const int block_m = blockIdx.y * kBM, block_n = blockIdx.x * kBN;
+  // loader: 128 rows x 128 bytes per operand = 1024 uint4; 4 per thread.
+  uint4 a_reg[4], w_reg[4];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int idx = tid + v * 256;
+      const int r = idx >> 3, seg = (idx & 7) * 16;
+      const int ar = block_m + r, wr = block_n + r;
+      a_reg[v] = ar < M ? *reinterpret_cast<const uint4 *>(a + static_cast<size_t>(ar) * K + k0 + seg)
+                        : make_uint4(0, 0, 0, 0);
+      w_reg[v] = wr < N ? *reinterpret_cast<const uint4 *>(w + static_cast<size_t>(wr) * K + k0 + seg)
+                        : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto stash = [&]() {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int idx = tid + v * 256;
+      const int r = idx >> 3, seg = (idx & 7) * 16;
+      *reinterpret_cast<uint4 *>(a_s + r * kStride + seg) = a_reg[v];
+      *reinterpret_cast<uint4 *>(w_s + r * kStride + seg) = w_reg[v];
+    }
+  };
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        acc[i][j][e] = 0.0F;
+
+  fetch(0);
+  for (int k0 = 0; k0 < K; k0 += kBK) {
+    __syncthreads();
+    stash();
+    __syncthreads();
+    if (k0 + kBK < K)
+      fetch(k0 + kBK);
+#pragma unroll
+    for (int c0 = 0; c0 < kBK; c0 += kChunk) {
+      f32x16 part[2][2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            part[i][j][e] = 0.0F;
+      if constexpr (kChunk == 32) {
+#pragma unroll
+        for (int ks = 0; ks < 32; ks += 16) {
+          const int koff = c0 + ks + (lane >> 5) * 8;
+          long bv[2];
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            bv[j] = *reinterpret_cast<const long *>(
+                w_s + (wave_n * 64 + j * 32 + (lane & 31)) * kStride + koff);
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            const long av = *reinterpret_cast<const long *>(
+                a_s + (wave_m * 64 + i * 32 + (lane & 31)) * kStride + koff);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+              part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(av, bv[j], part[i][j], 0, 0, 0);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int ks = 0; ks < kChunk; ks += 64) {
+          const int koff = c0 + ks + (lane >> 5) * 32;
+          i32x8 bv[2];
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const uint8_t *p = w_s + (wave_n * 64 + j * 32 + (lane & 31)) * kStride + koff;
+            const uint4 lo = *reinterpret_cast<const uint4 *>(p);
+            const uint4 hi = *reinterpret_cast<const uint4 *>(p + 16);
+            bv[j] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
+                          (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+          }
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            const uint8_t *p = a_s + (wave_m * 64 + i * 32 + (lane & 31)) * kStride + koff;
+            const uint4 lo = *reinterpret_cast<const uint4 *>(p);
+            const uint4 hi = *reinterpret_cast<const uint4 *>(p + 16);
+            const i32x8 av{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
+                           (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+              part[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                  av, bv[j], part[i][j], 0, 0, 0, 127, 0, 127);
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            acc[i][j][e] = truncate_e8m13(acc[i][j][e] + part[i][j][e]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int row = block_m + wave_m * 64 + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+      if (row >= M)
+        continue;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int col = block_n + wave_n * 64 + j * 32 + (lane & 31);
+        if (col < N)
+          out[static_cast<size_t>(row) * N + col] = round_bf16(acc[i][j][e] * output_scale);
+      }
+    }
+}
+
+unsigned elementwise_grid(size_t n) {
+  const size_t blocks = (n + 255) / 256;
+  return static_cast<unsigned>(blocks < 16384 ? blocks : 16384);
+}
+
+}  // namespace
+
+uint8_t e4m3_encode_host(float value) { return encode_e4m3(value); }
+
+Status e4m3_quantize_f32(const float *x, size_t n, float scale, uint8_t *codes,
+                         hipStream_t stream) {
+  if (x == nullptr || codes == nullptr || n == 0 || !(scale > 0.0F) ||
+      !__builtin_isfinite(scale))
+    return {ErrorCode::kInvalidArgument, "e4m3_quantize: invalid arguments"};
+  hipLaunchKernelGGL(quantize_f32_kernel, dim3(elementwise_grid(n)), dim3(256), 0,
+                     stream, x, n, scale, codes);
+  return launch_status("quantize_f32_kernel");
+}
+
+Status e4m3_quantize_bf16(const uint16_t *x, size_t n, float scale,
+                          uint8_t *codes, hipStream_t stream) {
+  if (x == nullptr || codes == nullptr || n == 0 || !(scale > 0.0F) ||
+      !__builtin_isfinite(scale))
+    return {ErrorCode::kInvalidArgument, "e4m3_quantize: invalid arguments"};
+  hipLaunchKernelGGL(quantize_bf16_kernel, dim3(elementwise_grid(n)), dim3(256), 0,
+                     stream, x, n, scale, codes);
+  return launch_status("quantize_bf16_kernel");
+}
+
+Status fp8_linear(const uint8_t *in_codes, const uint8_t *w_codes, float *out,
+                  size_t M, size_t N, size_t K, float output_scale,
+                  Fp8Mode mode, hipStream_t stream) {
+  if (in_codes == nullptr || w_codes == nullptr || out == nullptr || M == 0 ||
+      N == 0 || K == 0 || K % 32 != 0 || !(output_scale > 0.0F) ||
+      !__builtin_isfinite(output_scale) || M > (1U << 30) || N > (1U << 30))
+    return {ErrorCode::kInvalidArgument,
+            "fp8_linear: invalid arguments (K must be a positive multiple of 32)"};
+  const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
+  if (mode == kFp8Exact) {
+    hipLaunchKernelGGL(qgmma_exact_kernel, dim3(ceil_div(N, kExactTile), ceil_div(M, kExactTile)),
+                       dim3(256), 0, stream, in_codes, w_codes, out, m, n, k, output_scale);
+    return launch_status("qgmma_exact_kernel");
+  }
+  if (K % kBK != 0)
+    return {ErrorCode::kInvalidArgument, "fp8_linear: MFMA modes need K % 128 == 0"};
+  const dim3 grid(ceil_div(N, kBN), ceil_div(M, kBM));
+  if (mode == kFp8MfmaK32)
+    hipLaunchKernelGGL(fp8_mfma_kernel<32>, grid, dim3(256), 0, stream, in_codes,
+                       w_codes, out, m, n, k, output_scale);
+  else if (mode == kFp8MfmaK128)
+    hipLaunchKernelGGL(fp8_mfma_kernel<128>, grid, dim3(256), 0, stream, in_codes,
+                       w_codes, out, m, n, k, output_scale);
+  else
+    return {ErrorCode::kInvalidArgument, "fp8_linear: unknown mode"};
+  return launch_status("fp8_mfma_kernel");
+}
+
+}  // namespace evo::hip

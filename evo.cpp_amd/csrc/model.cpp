@@ -1,0 +1,467 @@
+// SPDX-License-Identifier: Apache-2.0
+#include "model.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <limits>
+#include <set>
+
+namespace evo::hip {
+namespace {
+
+constexpr size_t kArenaRows = 8192;  // activation rows per prefill chunk
+
+Status hip_check(hipError_t error, const std::string &what) {
+  if (error == hipSuccess)
+    return Status::Ok();
+  return {ErrorCode::kHip, "hip: " + what + ": " + hipGetErrorString(error)};
+}
+
+Status format_error(const std::string &message) {
+  return {ErrorCode::kModelFormat, "model_format: " + message};
+}
+
+float bf16_host(const uint8_t *p) {
+  const uint32_t bits = static_cast<uint32_t>(p[0]) << 16U | static_cast<uint32_t>(p[1]) << 24U;
+  float v;
+  std::memcpy(&v, &bits, 4);
+  return v;
+}
+
+std::vector<float> to_f32(const TensorView &t) {
+  std::vector<float> out(t.elements());
+  for (size_t i = 0; i < out.size(); ++i) {
+    if (t.dtype == DType::kF32)
+      std::memcpy(&out[i], t.data + 4 * i, 4);
+    else
+      out[i] = bf16_host(t.data + 2 * i);
+  }
+  return out;
+}
+
+Status view(const Artifact &a, const std::string &name,
+            std::vector<uint64_t> shape, DType dtype, const TensorView **out,
+            bool accept_f32 = false, bool accept_fp8 = false) {
+  const TensorView *t = a.tensor(name);
+  if (t == nullptr)
+    return format_error("required tensor is missing: " + name);
+  if (t->shape != shape)
+    return format_error("tensor shape mismatch: " + name);
+  if (t->dtype != dtype && !(accept_f32 && t->dtype == DType::kF32) &&
+      !(accept_fp8 && t->dtype == DType::kE4M3))
+    return format_error("tensor dtype mismatch: " + name);
+  *out = t;
+  return Status::Ok();
+}
+
+Status upload_view(DeviceBuffer *buffer, const TensorView &t, const std::string &name) {
+  EVO_TRY(buffer->allocate(t.bytes, name.c_str()));
+  return buffer->upload(t.data, t.bytes, name.c_str());
+}
+
+Status upload_f32(DeviceBuffer *buffer, const std::vector<float> &values,
+                  const std::string &name) {
+  EVO_TRY(buffer->allocate(values.size() * 4, name.c_str()));
+  return buffer->upload(values.data(), values.size() * 4, name.c_str());
+}
+
+}  // namespace
+
+Status DeviceBuffer::allocate(size_t bytes, const char *what) {
+  reset();
+  if (bytes == 0)
+    return Status::Ok();
+  const hipError_t error = hipMalloc(&ptr_, bytes);
+  if (error != hipSuccess) {
+    ptr_ = nullptr;
+    return {ErrorCode::kHip, std::string("hip: allocate ") + what + " (" +
+                                 std::to_string(bytes) + " B): " + hipGetErrorString(error)};
+  }
+  bytes_ = bytes;
+  return Status::Ok();
+}
+
+Status DeviceBuffer::upload(const void *host, size_t bytes, const char *what) {
+  if (bytes > bytes_)
+    return {ErrorCode::kInternal, std::string("upload overflows ") + what};
+  return hip_check(hipMemcpy(ptr_, host, bytes, hipMemcpyHostToDevice),
+                   std::string("upload ") + what);
+}
+
+void DeviceBuffer::reset() {
+  if (ptr_ != nullptr)
+    (void)hipFree(ptr_);
+  ptr_ = nullptr;
+  bytes_ = 0;
+}
+
+// ---------------------------------------------------------------- Model load
+// Tensor set, shapes and dtypes: evo.cpp `src/cpu/model.cpp:2651-2874`.
+Status Model::load(const Artifact &a, int device, bool allow_synthetic) {
+  device_ = device;
+  EVO_TRY(hip_check(hipSetDevice(device), "select device"));
+  ModelConfig &c = config_;
+  EVO_TRY(a.meta_string("model.architecture", &c.architecture));
+  if (c.architecture == "StripedHyena2Test") {
+    bool synthetic = false;
+    EVO_TRY(a.meta_bool("fixture.synthetic", &synthetic));
+    if (!synthetic || !allow_synthetic)
+      return {ErrorCode::kUnsupported,
+              "unsupported: synthetic model fixtures require explicit test permission"};
+  } else if (c.architecture != "StripedHyena2") {
+    return {ErrorCode::kUnsupported, "unsupported: architecture is not StripedHyena2"};
+  }
+  if (!a.meta_string("model.id", &c.model_id).ok())
+    EVO_TRY(a.meta_string("model.name", &c.model_id));
+  const std::pair<const char *, size_t *> sizes[] = {
+      {"config.vocab_size", &c.vocab},
+      {"config.hidden_size", &c.width},
+      {"config.num_layers", &c.layers},
+      {"config.num_attention_heads", &c.heads},
+      {"config.state_size", &c.state},
+      {"config.inner_mlp_size", &c.inner},
+      {"config.short_filter_length", &c.short_len},
+      {"config.hcs_filter_length", &c.hcs_len},
+      {"config.hcm_filter_length", &c.hcm_len},
+      {"config.hcs_filter_groups", &c.hcs_groups},
+      {"config.hcm_filter_groups", &c.hcm_groups}};
+  for (const auto &item : sizes) {
+    uint64_t v = 0;
+    EVO_TRY(a.meta_u64(item.first, &v));
+    *item.second = static_cast<size_t>(v);
+  }
+  if (c.architecture == "StripedHyena2Test") {
+    c.max_seqlen = std::numeric_limits<size_t>::max();
+  } else {
+    uint64_t v = 0;
+    EVO_TRY(a.meta_u64("config.max_seqlen", &v));
+    c.max_seqlen = static_cast<size_t>(v);
+  }
+  double eps = 0, rope = 0;
+  EVO_TRY(a.meta_f64("config.eps", &eps));
+  EVO_TRY(a.meta_f64("config.rotary_emb_scaling_factor", &rope));
+  c.eps = static_cast<float>(eps);
+  c.rope_scale = static_cast<float>(rope);
+  if (a.has_meta("config.column_split"))
+    EVO_TRY(a.meta_bool("config.column_split", &c.column_split));
+  if (c.vocab == 0 || c.width == 0 || c.layers == 0 || c.heads == 0 ||
+      c.width % c.heads != 0 || c.head_dim() % 2 != 0 || c.state == 0 ||
+      c.state > 16 || c.inner == 0 || c.short_len < 2 || c.short_len > 8 ||
+      c.hcs_len < 2 || c.hcs_len > 8 || c.hcm_len < 2 || c.hcm_len > 128 ||
+      c.hcs_groups == 0 || c.hcm_groups == 0 || c.width % c.hcs_groups != 0 ||
+      c.width % c.hcm_groups != 0 || !std::isfinite(c.eps) || c.eps <= 0.0F ||
+      !std::isfinite(c.rope_scale) || c.rope_scale <= 0.0F || c.width % 32 != 0 ||
+      c.inner % 8 != 0)
+    return {ErrorCode::kUnsupported,
+            "unsupported: model dimensions are outside the HIP backend's envelope "
+            "(width % 32, inner % 8, state <= 16, short/HCS taps <= 8, HCM taps <= 128)"};
+  const size_t hd = c.head_dim();
+  if (hd != 16 && hd != 32 && hd != 64 && hd != 128)
+    return {ErrorCode::kUnsupported, "unsupported: head_dim must be 16, 32, 64 or 128"};
+  c.inner_padded = (c.inner + 31) / 32 * 32;
+
+  std::vector<uint64_t> hcs, hcm, hcl, attn;
+  EVO_TRY(a.meta_list("config.hcs_layer_idxs", &hcs));
+  EVO_TRY(a.meta_list("config.hcm_layer_idxs", &hcm));
+  EVO_TRY(a.meta_list("config.hcl_layer_idxs", &hcl));
+  EVO_TRY(a.meta_list("config.attn_layer_idxs", &attn));
+  layer.clear();
+  layer.resize(c.layers);
+  std::set<uint64_t> seen;
+  auto classify = [&](const std::vector<uint64_t> &list, Mixer type,
+                      const char *name) -> Status {
+    for (auto index : list) {
+      if (index >= c.layers || !seen.insert(index).second)
+        return format_error(std::string("invalid ") + name + " layer list");
+      layer[index].type = type;
+    }
+    return Status::Ok();
+  };
+  EVO_TRY(classify(hcs, Mixer::kHcs, "HCS"));
+  EVO_TRY(classify(hcm, Mixer::kHcm, "HCM"));
+  EVO_TRY(classify(hcl, Mixer::kHcl, "HCL"));
+  EVO_TRY(classify(attn, Mixer::kAttention, "attention"));
+  if (seen.size() != c.layers)
+    return format_error("mixer lists do not cover all blocks");
+
+  const size_t w = c.width;
+  const TensorView *t = nullptr;
+  EVO_TRY(view(a, "embedding_layer.weight", {c.vocab, w}, DType::kBF16, &t));
+  EVO_TRY(upload_view(&embedding, *t, "embedding_layer.weight"));
+  EVO_TRY(view(a, "norm.scale", {w}, DType::kF32, &t));
+  EVO_TRY(upload_view(&final_norm, *t, "norm.scale"));
+
+  for (size_t i = 0; i < c.layers; ++i) {
+    Layer &L = layer[i];
+    const std::string p = "blocks." + std::to_string(i);
+    EVO_TRY(view(a, p + ".pre_norm.scale", {w}, DType::kF32, &t));
+    EVO_TRY(upload_view(&L.pre_norm, *t, p + ".pre_norm.scale"));
+    EVO_TRY(view(a, p + ".post_norm.scale", {w}, DType::kF32, &t));
+    EVO_TRY(upload_view(&L.post_norm, *t, p + ".post_norm.scale"));
+    // Gated MLP: l1 and l2 interleaved in 32-row blocks so one GEMM produces
+    // both operands of every gated output in the same lane.
+    const TensorView *l1 = nullptr, *l2 = nullptr, *l3 = nullptr;
+    EVO_TRY(view(a, p + ".mlp.l1.weight", {c.inner, w}, DType::kBF16, &l1));
+    EVO_TRY(view(a, p + ".mlp.l2.weight", {c.inner, w}, DType::kBF16, &l2));
+    EVO_TRY(view(a, p + ".mlp.l3.weight", {w, c.inner}, DType::kBF16, &l3));
+    {
+      std::vector<uint16_t> packed(2 * c.inner_padded * w, 0);
+      for (size_t q = 0; q < c.inner_padded / 32; ++q)
+        for (size_t r = 0; r < 32; ++r) {
+          const size_t src = q * 32 + r;
+          if (src >= c.inner)
+            continue;
+          std::memcpy(&packed[(64 * q + r) * w], l1->data + src * w * 2, w * 2);
+          std::memcpy(&packed[(64 * q + 32 + r) * w], l2->data + src * w * 2, w * 2);
+        }
+      EVO_TRY(L.mlp_in.allocate(packed.size() * 2, "mlp l1/l2"));
+      EVO_TRY(L.mlp_in.upload(packed.data(), packed.size() * 2, "mlp l1/l2"));
+    }
+    EVO_TRY(upload_view(&L.mlp_out, *l3, p + ".mlp.l3.weight"));
+
+    if (L.type == Mixer::kAttention) {
+      EVO_TRY(view(a, p + ".inner_mha_cls.Wqkv.weight", {3 * w, w}, DType::kBF16, &t));
+      EVO_TRY(upload_view(&L.projection, *t, p + ".Wqkv"));
+      EVO_TRY(view(a, p + ".inner_mha_cls.out_proj.weight", {w, w}, DType::kBF16, &t));
+      EVO_TRY(upload_view(&L.out_weight, *t, p + ".out_proj.weight"));
+      EVO_TRY(view(a, p + ".inner_mha_cls.out_proj.bias", {w}, DType::kBF16, &t));
+      EVO_TRY(upload_view(&L.out_bias, *t, p + ".out_proj.bias"));
+      EVO_TRY(view(a, p + ".inner_mha_cls.rotary_emb.inv_freq", {hd / 2}, DType::kF32, &t));
+      EVO_TRY(upload_view(&L.inv_freq, *t, p + ".inv_freq"));
+      continue;
+    }
+    EVO_TRY(view(a, p + ".projections.weight", {3 * w, w}, DType::kBF16, &t, false, true));
+    L.fp8 = t->dtype == DType::kE4M3;
+    EVO_TRY(upload_view(&L.projection, *t, p + ".projections.weight"));
+    if (L.fp8) {
+      // [input_scale, output_scale] (`src/cuda/model.cu:226-248`).
+      const TensorView *s = nullptr;
+      EVO_TRY(view(a, p + ".projections.fp8_runtime_scales", {2}, DType::kF32, &s));
+      float scales[2];
+      std::memcpy(scales, s->data, 8);
+      if (!(std::isfinite(scales[0]) && scales[0] > 0 && std::isfinite(scales[1]) &&
+            scales[1] > 0))
+        return format_error(p + " contains invalid software-FP8 runtime scales");
+      L.fp8_input_scale = scales[0];
+      L.fp8_output_scale = scales[1];
+      if (w % 32 != 0)
+        return {ErrorCode::kUnsupported, "unsupported: FP8 projections need width % 32 == 0"};
+    }
+    EVO_TRY(view(a, p + ".out_filter_dense.weight", {w, w}, DType::kBF16, &t));
+    EVO_TRY(upload_view(&L.out_weight, *t, p + ".out_filter_dense.weight"));
+    EVO_TRY(view(a, p + ".out_filter_dense.bias", {w}, DType::kBF16, &t));
+    EVO_TRY(upload_view(&L.out_bias, *t, p + ".out_filter_dense.bias"));
+    EVO_TRY(view(a, p + ".filter.short_filter_weight", {3 * w, 1, c.short_len}, DType::kBF16, &t));
+    EVO_TRY(upload_view(&L.short_filter, *t, p + ".short_filter_weight"));
+    if (L.type == Mixer::kHcs) {
+      EVO_TRY(view(a, p + ".filter.h", {c.hcs_groups, 1, c.hcs_len}, DType::kBF16, &t));
+      EVO_TRY(upload_f32(&L.inner_filter, to_f32(*t), p + ".filter.h"));
+      continue;
+    }
+    EVO_TRY(view(a, p + ".filter.D", {w}, DType::kBF16, &t));
+    EVO_TRY(upload_f32(&L.direct, to_f32(*t), p + ".filter.D"));
+    if (L.type == Mixer::kHcm) {
+      EVO_TRY(view(a, p + ".filter.h", {c.hcm_groups, 1, c.hcm_len}, DType::kBF16, &t, true));
+      EVO_TRY(upload_f32(&L.inner_filter, to_f32(*t), p + ".filter.h"));
+    } else {
+      EVO_TRY(view(a, p + ".filter.log_poles", {w, c.state, 1}, DType::kF32, &t));
+      std::vector<float> poles = to_f32(*t);
+      // exp(log_pole) once, with the host libm expf the F32 reference uses
+      // per step (`src/cpu/model.cpp:589-590`).
+      for (auto &v : poles)
+        v = std::exp(v);
+      EVO_TRY(upload_f32(&L.poles, poles, p + ".poles"));
+      EVO_TRY(view(a, p + ".filter.residues", {w, c.state}, DType::kF32, &t));
+      EVO_TRY(upload_view(&L.residues, *t, p + ".filter.residues"));
+    }
+  }
+  return hip_check(hipDeviceSynchronize(), "model upload");
+}
+
+// ------------------------------------------------------------------ Context
+Context::~Context() {
+  if (host_logits_ != nullptr)
+    (void)hipHostFree(host_logits_);
+  if (stream_ != nullptr)
+    (void)hipStreamDestroy(stream_);
+}
+
+Status Context::initialize(std::shared_ptr<const Model> model, size_t capacity,
+                           const ContextOptions &options) {
+  model_ = std::move(model);
+  options_ = options;
+  const ModelConfig &c = model_->config();
+  if (capacity == 0 || capacity > c.max_seqlen)
+    return {ErrorCode::kInvalidArgument,
+            "invalid_argument: context requires a valid capacity"};
+  capacity_ = capacity;
+  arena_rows_ = std::min(capacity, kArenaRows);
+  // Test hook: a smaller activation arena forces multi-chunk prefill.
+  if (const char *rows = std::getenv("EVO_HIP_ARENA_ROWS")) {
+    const long value = std::atol(rows);
+    if (value > 0)
+      arena_rows_ = std::min(arena_rows_, static_cast<size_t>(value));
+  }
+  profile_ = options.split_activations ? "hip-f32" : "hip-bf16";
+  if (options.fp8_mode == kFp8Exact)
+    profile_ += "+fp8-exact";
+  EVO_TRY(hip_check(hipSetDevice(model_->device()), "select device"));
+  EVO_TRY(hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "create stream"));
+  const size_t R = arena_rows_, w = c.width;
+  EVO_TRY(tokens_.allocate(R * 4, "tokens"));
+  EVO_TRY(hidden_.allocate(R * w * 4, "hidden"));
+  EVO_TRY(residual_.allocate(R * w * 4, "residual"));
+  EVO_TRY(normed_.allocate(R * w * 4, "normed"));
+  EVO_TRY(projected_.allocate(R * 3 * w * 4, "projection"));
+  EVO_TRY(mixed_.allocate(R * w * 4, "mixer output"));
+  EVO_TRY(query_.allocate(R * w * 4, "query"));
+  EVO_TRY(gated_.allocate(R * c.inner * 4, "mlp gate"));
+  EVO_TRY(logits_.allocate(R * c.vocab * 4, "logits"));
+  EVO_TRY(codes_.allocate(R * w, "fp8 codes"));
+  workspace_bytes_ = hyena_workspace_bytes(kHyenaHcl, R, w, c.state);
+  EVO_TRY(workspace_.allocate(std::max<size_t>(workspace_bytes_, 256), "hyena workspace"));
+  EVO_TRY(hip_check(hipHostMalloc(reinterpret_cast<void **>(&host_logits_),
+                                  R * std::max(c.vocab, w) * 4, hipHostMallocDefault),
+                    "pinned logits"));
+  cache_.clear();
+  cache_.resize(c.layers);
+  for (size_t i = 0; i < c.layers; ++i) {
+    const Layer &L = model_->layer[i];
+    Cache &k = cache_[i];
+    if (L.type == Mixer::kAttention) {
+      EVO_TRY(k.keys.allocate(capacity * w * 4, "key cache"));
+      EVO_TRY(k.values.allocate(capacity * w * 4, "value cache"));
+      continue;
+    }
+    EVO_TRY(k.short_history.allocate((c.short_len - 1) * 3 * w * 4, "short FIR cache"));
+    if (L.type == Mixer::kHcs)
+      EVO_TRY(k.inner_history.allocate((c.hcs_len - 1) * w * 4, "HCS cache"));
+    else if (L.type == Mixer::kHcm)
+      EVO_TRY(k.inner_history.allocate((c.hcm_len - 1) * w * 4, "HCM cache"));
+    else
+      EVO_TRY(k.modal_state.allocate(w * c.state * 4, "HCL state"));
+  }
+  reset_caches();
+  return hip_check(hipStreamSynchronize(stream_), "context initialise");
+}
+
+void Context::reset_caches() {
+  for (auto &k : cache_)
+    for (DeviceBuffer *b : {&k.short_history, &k.inner_history, &k.modal_state})
+      if (b->bytes() != 0)
+        (void)hipMemsetAsync(b->as<void>(), 0, b->bytes(), stream_);
+  position_ = 0;
+  valid_ = false;
+}
+
+Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
+  const ModelConfig &c = model_->config();
+  const size_t w = c.width;
+  const bool split = options_.split_activations;
+  float *hidden = hidden_.as<float>(), *residual = residual_.as<float>(),
+        *normed = normed_.as<float>(), *projected = projected_.as<float>(),
+        *mixed = mixed_.as<float>();
+  for (size_t i = 0; i < c.layers; ++i) {
+    const Layer &L = model_->layer[i];
+    Cache &k = cache_[i];
+    EVO_TRY(rms_norm(hidden, rows, w, L.pre_norm.as<float>(), c.eps, normed, stream_));
+    if (L.fp8) {
+      EVO_TRY(e4m3_quantize_f32(normed, rows * w, L.fp8_input_scale, codes_.as<uint8_t>(), stream_));
+      const Fp8Mode mode = (w % 128 != 0) ? kFp8Exact : options_.fp8_mode;
+      EVO_TRY(fp8_linear(codes_.as<uint8_t>(), L.projection.as<uint8_t>(), projected, rows,
+                         3 * w, w, L.fp8_output_scale, mode, stream_));
+    } else {
+      EVO_TRY(gemm_bf16w(normed, L.projection.as<uint16_t>(), projected, rows, 3 * w, w,
+                         3 * w, kGemmStore, nullptr, nullptr, false, 0, split, stream_));
+    }
+    if (L.type == Mixer::kAttention) {
+      float *query = query_.as<float>();
+      EVO_TRY(qkv_rope(projected, rows, w, c.heads, c.column_split, L.inv_freq.as<float>(),
+                       c.rope_scale, position_, query, k.keys.as<float>(),
+                       k.values.as<float>(), stream_));
+      EVO_TRY(causal_attention(query, k.keys.as<float>(), k.values.as<float>(), rows,
+                               position_, c.heads, c.head_dim(), mixed, stream_));
+    } else {
+      HyenaWeights hw{};
+      hw.short_filter = L.short_filter.as<uint16_t>();
+      hw.short_len = c.short_len;
+      hw.inner_filter = L.inner_filter.as<float>();
+      hw.groups = L.type == Mixer::kHcs ? c.hcs_groups : c.hcm_groups;
+      hw.inner_len = L.type == Mixer::kHcs ? c.hcs_len : c.hcm_len;
+      hw.direct = L.direct.as<float>();
+      hw.poles = L.poles.as<float>();
+      hw.residues = L.residues.as<float>();
+      hw.state = c.state;
+      const int kind = L.type == Mixer::kHcs ? kHyenaHcs
+                       : L.type == Mixer::kHcm ? kHyenaHcm : kHyenaHcl;
+      EVO_TRY(hyena_forward<float>(kind, projected, rows, w, hw,
+                                   k.short_history.as<float>(),
+                                   k.inner_history.as<float>(),
+                                   k.modal_state.as<float>(), workspace_.as<void>(),
+                                   workspace_.bytes(), mixed, stream_));
+    }
+    // residual = (mixed . Wout^T + bias) + hidden   (`src/cpu/model.cpp:641-645`)
+    EVO_TRY(gemm_bf16w(mixed, L.out_weight.as<uint16_t>(), residual, rows, w, w, w,
+                       kGemmBiasResidual, L.out_bias.as<uint16_t>(), hidden, false, 0,
+                       split, stream_));
+    EVO_TRY(rms_norm(residual, rows, w, L.post_norm.as<float>(), c.eps, normed, stream_));
+    // gated = act(l1 x) * (l2 x), act = erf-GELU in block 0 only (`:650-667`)
+    EVO_TRY(gemm_bf16w(normed, L.mlp_in.as<uint16_t>(), gated_.as<float>(), rows,
+                       2 * c.inner_padded, w, c.inner, kGemmGated, nullptr, nullptr,
+                       i == 0, c.inner, split, stream_));
+    // hidden = gated . l3^T + residual
+    EVO_TRY(gemm_bf16w(gated_.as<float>(), L.mlp_out.as<uint16_t>(), hidden, rows, w,
+                       c.inner, w, kGemmResidual, nullptr, residual, false, 0, split,
+                       stream_));
+    if (capture != nullptr && capture_layer == i)
+      EVO_TRY(hip_check(hipMemcpyAsync(capture, hidden, rows * w * 4,
+                                       hipMemcpyDeviceToHost, stream_),
+                        "capture download"));
+  }
+  return Status::Ok();
+}
+
+Status Context::forward(const uint32_t *tokens, size_t rows, bool initial,
+                        float *logits, size_t capture_layer, float *capture) {
+  const ModelConfig &c = model_->config();
+  if (rows == 0 || rows > arena_rows_ || (logits == nullptr && capture == nullptr))
+    return {ErrorCode::kInvalidArgument, "invalid_argument: forward arguments are invalid"};
+  if (initial) {
+    reset_caches();
+  } else if (!valid_ || rows > capacity_ - position_) {
+    return {ErrorCode::kInvalidArgument,
+            "invalid_argument: continuation requires a valid prefill and free capacity"};
+  }
+  if (initial && rows > capacity_)
+    return {ErrorCode::kInvalidArgument, "invalid_argument: chunk exceeds capacity"};
+  for (size_t r = 0; r < rows; ++r)
+    if (tokens[r] >= c.vocab)
+      return {ErrorCode::kInvalidArgument, "invalid_argument: token exceeds model vocabulary"};
+  EVO_TRY(hip_check(hipSetDevice(model_->device()), "select device"));
+  EVO_TRY(hip_check(hipMemcpyAsync(tokens_.as<void>(), tokens, rows * 4,
+                                   hipMemcpyHostToDevice, stream_), "token upload"));
+  EVO_TRY(embed_tokens(tokens_.as<uint32_t>(), rows, model_->embedding.as<uint16_t>(),
+                       c.vocab, c.width, hidden_.as<float>(), stream_));
+  if (capture != nullptr && capture_layer >= c.layers)
+    return {ErrorCode::kInvalidArgument, "invalid_argument: embedding layer is invalid"};
+  EVO_TRY(run_layers(rows, capture_layer, capture));
+  if (logits != nullptr) {
+    EVO_TRY(rms_norm(hidden_.as<float>(), rows, c.width, model_->final_norm.as<float>(),
+                     c.eps, normed_.as<float>(), stream_));
+    EVO_TRY(gemm_bf16w(normed_.as<float>(), model_->embedding.as<uint16_t>(),
+                       logits_.as<float>(), rows, c.vocab, c.width, c.vocab, kGemmStore,
+                       nullptr, nullptr, false, 0, options_.split_activations, stream_));
+    EVO_TRY(hip_check(hipMemcpyAsync(host_logits_, logits_.as<void>(), rows * c.vocab * 4,
+                                     hipMemcpyDeviceToHost, stream_), "logits download"));
+  }
+  EVO_TRY(hip_check(hipStreamSynchronize(stream_), "prefill"));
+  if (logits != nullptr)
+    std::memcpy(logits, host_logits_, rows * c.vocab * 4);
+  position_ = initial ? rows : position_ + rows;
+  valid_ = true;
+  return Status::Ok();
+}
+
+}  // namespace evo::hip

@@ -1,0 +1,97 @@
+// SPDX-License-Identifier: Apache-2.0
+// Host launchers of the gfx950 kernels (device pointers, one HIP stream).
+// Each launcher validates shapes on the host before it launches, so no kernel
+// runs with a grid its indexing does not cover.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "status.hpp"
+
+namespace evo::hip {
+
+enum GemmEpilogue : int {
+  kGemmStore = 0,
+  kGemmBias = 1,
+  kGemmResidual = 2,
+  kGemmBiasResidual = 3,
+  kGemmGated = 4,
+};
+
+// C = A . W^T with A F32 [M,K], W BF16 [N,K]; see gemm.hip.
+Status gemm_bf16w(const float *A, const uint16_t *W, float *C, size_t M,
+                  size_t N, size_t K, size_t ldc, GemmEpilogue mode,
+                  const uint16_t *bias, const float *residual, bool gelu,
+                  size_t gated_width, bool split, hipStream_t stream);
+
+// ---- Software FP8 (fp8.hip).
+// codes[i] = E4M3FN_RNE_satfinite(float(bf16(x[i])) * scale).
+Status e4m3_quantize_f32(const float *x, size_t n, float scale, uint8_t *codes,
+                         hipStream_t stream);
+Status e4m3_quantize_bf16(const uint16_t *x, size_t n, float scale,
+                          uint8_t *codes, hipStream_t stream);
+enum Fp8Mode : int {
+  kFp8MfmaK32 = 0,   // E4M3 MFMA, promotion to the E8M13 accumulator every 32 K
+  kFp8MfmaK128 = 1,  // E4M3 MFMA, promotion every 128 K
+  kFp8Exact = 2,     // integer QGMMA emulation, bit-exact to the reference
+};
+// out[M,N] (F32 holding BF16 values) = bf16(QGMMA(in_codes, w_codes) * output_scale)
+// (+ optional F32 residual added after the BF16 rounding).
+Status fp8_linear(const uint8_t *in_codes, const uint8_t *w_codes, float *out,
+                  size_t M, size_t N, size_t K, float output_scale,
+                  Fp8Mode mode, hipStream_t stream);
+
+// ---- Elementwise / normalisation (elementwise.hip).
+Status embed_tokens(const uint32_t *tokens, size_t rows, const uint16_t *table,
+                    size_t vocab, size_t width, float *out, hipStream_t stream);
+Status rms_norm(const float *x, size_t rows, size_t width, const float *scale,
+                float eps, float *out, hipStream_t stream);
+// Copies the last `history` rows of the sequence [old_history ; x] into
+// history (F32 [history, channels]), keeping continuation caches.
+Status update_history(const float *x, size_t rows, size_t channels,
+                      float *history, size_t history_rows, float *scratch,
+                      hipStream_t stream);
+
+// ---- Hyena operator (hyena.hip). Projection P [L, 3W] interleaved triples
+// (x2, x1, v) per channel. Caches (may be null for a fresh sequence):
+// short_history F32 [short_len-1, 3W], inner_history F32 [inner_len-1, W],
+// modal_state F32 [W, S]. They are read as the state before row 0 and
+// rewritten to the state after row L-1.
+enum HyenaKind : int { kHyenaHcs = 0, kHyenaHcm = 1, kHyenaHcl = 2 };
+struct HyenaWeights {
+  const uint16_t *short_filter;  // BF16 [3W, short_len]
+  size_t short_len;
+  const float *inner_filter;     // F32 [groups, inner_len] (HCS/HCM)
+  size_t groups, inner_len;
+  const float *direct;           // F32 [W] (HCM/HCL)
+  const float *poles;            // F32 [W, S] = exp(log_poles) (HCL)
+  const float *residues;         // F32 [W, S] (HCL)
+  size_t state;
+};
+size_t hyena_workspace_bytes(int kind, size_t length, size_t width,
+                             size_t state);
+template <typename T>
+Status hyena_forward(int kind, const T *projection, size_t length,
+                     size_t width, const HyenaWeights &weights,
+                     float *short_history, float *inner_history,
+                     float *modal_state, void *workspace,
+                     size_t workspace_bytes, T *out, hipStream_t stream);
+
+// ---- Attention (attention.hip).
+// Splits the QKV projection [rows, 3W] into rotated Q and K and plain V,
+// appending K/V rows at position `prefix` of the caches [capacity, W].
+Status qkv_rope(const float *projected, size_t rows, size_t width, size_t heads,
+                bool column_split, const float *inv_freq, float rope_scale,
+                size_t prefix, float *q, float *k_cache, float *v_cache,
+                hipStream_t stream);
+// Causal attention of `rows` queries at positions prefix.. against keys
+// [0, prefix + rows). Layout [time, heads, head_dim] = [time, W].
+Status causal_attention(const float *q, const float *k_cache,
+                        const float *v_cache, size_t rows, size_t prefix,
+                        size_t heads, size_t head_dim, float *out,
+                        hipStream_t stream);
+
+}  // namespace evo::hip

@@ -1,0 +1,127 @@
+/* SPDX-License-Identifier: Apache-2.0
+ *
+ * Operator-level C ABI of libevo_hip.so: the gfx950 kernels of the
+ * StripedHyena2 prefill path on caller-owned device memory.
+ *
+ * All pointers are device pointers (hipMalloc'd or a torch tensor's
+ * data_ptr()); `stream` is a hipStream_t (NULL = the default stream). Calls
+ * are asynchronous on that stream and never allocate device memory: every
+ * temporary lives in a caller-provided workspace whose size the matching
+ * *_workspace_bytes query returns. Shapes are validated on the host before
+ * any launch; invalid arguments return EVO_STATUS_INVALID_ARGUMENT with the
+ * message in evo_last_error(). BF16 tensors are raw uint16 bit patterns.
+ *
+ * Each entry point names the reference interface it replaces.
+ */
+#ifndef EVO_HIP_OPS_H
+#define EVO_HIP_OPS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "evo/evo.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Storage type of activation tensors passed to the Hyena operator. */
+typedef enum evo_hip_dtype { EVO_HIP_F32 = 0, EVO_HIP_BF16 = 1 } evo_hip_dtype;
+typedef enum evo_hip_hyena_kind {
+  EVO_HIP_HYENA_HCS = 0,
+  EVO_HIP_HYENA_HCM = 1,
+  EVO_HIP_HYENA_HCL = 2
+} evo_hip_hyena_kind;
+
+/* Fused Hyena mixer of one block: short FIR (short_len taps, per column of
+ * the [L, 3W] projection with interleaved (x2, x1, v) triples), u = x1*v, the
+ * long filter (HCS grouped FIR / HCM grouped causal conv + D*u / HCL modal
+ * recurrence + D*u), times x2; output [L, W] in `dtype`.
+ * Replaces evo.cpp `bf16_fir_prefill_direct` + `bf16_hcs_prefill` /
+ * `bf16_hcm_prefill` / `bf16_hcl_prefill`
+ * (`include/evo/cuda/hyena.hpp:154-252`) and the CPU mixer
+ * (`src/cpu/model.cpp:546-605`).
+ *   short_filter  BF16 [3W, short_len]
+ *   inner_filter  F32 [groups, inner_len]          (HCS/HCM; else NULL)
+ *   direct        F32 [W]                          (HCM/HCL; else NULL)
+ *   poles         F32 [W, state] = exp(log_poles)  (HCL; else NULL)
+ *   residues      F32 [W, state]                   (HCL; else NULL)
+ *   short_history F32 [short_len-1, 3W], inner_history F32 [inner_len-1, W],
+ *   modal_state   F32 [W, state]: optional continuation caches (NULL = zero
+ *                 initial state, nothing kept); read as the state before row
+ *                 0 and overwritten with the state after row L-1. */
+EVO_API size_t evo_hip_hyena_workspace_bytes(evo_hip_hyena_kind kind,
+                                             size_t length, size_t width,
+                                             size_t state_size);
+EVO_API evo_status evo_hip_hyena_forward(
+    evo_hip_hyena_kind kind, evo_hip_dtype dtype, const void *projection,
+    size_t length, size_t width, const uint16_t *short_filter,
+    size_t short_len, const float *inner_filter, size_t groups,
+    size_t inner_len, const float *direct, const float *poles,
+    const float *residues, size_t state_size, float *short_history,
+    float *inner_history, float *modal_state, void *workspace,
+    size_t workspace_bytes, void *output, void *stream);
+
+/* codes[i] = E4M3FN(float(bf16(x[i])) * scale), RNE, satfinite.
+ * Replaces `software_e4m3_quantize_bf16_codes` (`include/evo/cuda/ops.hpp:92-96`). */
+EVO_API evo_status evo_hip_e4m3_quantize(evo_hip_dtype dtype, const void *x,
+                                         size_t count, float scale,
+                                         uint8_t *codes, void *stream);
+
+/* Software-FP8 projection out[M,N] = bf16(QGMMA(in_codes[M,K], w_codes[N,K])
+ * * output_scale), stored as F32. mode 0 = E4M3 MFMA with promotion every 32
+ * K, 1 = every 128 K, 2 = bit-exact integer QGMMA emulation.
+ * Replaces `software_e4m3_h100_linear` (`include/evo/cuda/ops.hpp:104-114`). */
+EVO_API evo_status evo_hip_fp8_linear(const uint8_t *in_codes,
+                                      const uint8_t *w_codes, float *out,
+                                      size_t m, size_t n, size_t k,
+                                      float output_scale, int mode,
+                                      void *stream);
+
+/* out[M,N] = x[M,K] . w[N,K]^T (+ bf16 bias[N]) (+ residual[M,N]), F32 x and
+ * out, BF16 w. split != 0 uses two BF16 MFMA passes per F32 activation.
+ * Replaces `bf16_linear` (`include/evo/cuda/ops.hpp:61-70`) and the CPU
+ * `linear` (`src/cpu/model.cpp:284-314`). */
+EVO_API evo_status evo_hip_linear(const float *x, const uint16_t *w,
+                                  const uint16_t *bias, const float *residual,
+                                  size_t m, size_t n, size_t k, int split,
+                                  float *out, void *stream);
+
+/* Gated MLP out[M,F] = l3(act(l1 x) * l2 x) with act = erf-GELU when gelu != 0.
+ * w12 is the interleaved [2*Fp, K] l1/l2 weight (32-row blocks, Fp = F
+ * rounded up to 32) built by evo_hip_pack_mlp; inner [M, F] is workspace.
+ * Replaces `bf16_mlp` (`include/evo/cuda/ops.hpp:133-138`). */
+EVO_API evo_status evo_hip_pack_mlp(const uint16_t *l1, const uint16_t *l2,
+                                    size_t inner, size_t width, uint16_t *w12,
+                                    void *stream);
+EVO_API evo_status evo_hip_gated_mlp(const float *x, const uint16_t *w12,
+                                     const uint16_t *l3, size_t m, size_t width,
+                                     size_t inner, int gelu, int split,
+                                     float *inner_workspace,
+                                     const float *residual, float *out,
+                                     void *stream);
+
+/* RMSNorm y = x / (sqrt(mean(x^2)) + eps) * scale over rows of width.
+ * Replaces `bf16_rms_norm` (`include/evo/cuda/ops.hpp:117-120`). */
+EVO_API evo_status evo_hip_rms_norm(const float *x, size_t rows, size_t width,
+                                    const float *scale, float eps, float *out,
+                                    void *stream);
+
+/* Attention block body: split Wqkv output [rows, 3W], RoPE, append to K/V
+ * caches [capacity, W] at `prefix`, causal softmax attention into out
+ * [rows, W]; query is [rows, W] workspace.
+ * Replaces `bf16_split_qkv` + `bf16_apply_rope` + `bf16_kv_append` +
+ * `bf16_online_causal_attention` (`include/evo/cuda/attention.hpp:100-133`). */
+EVO_API evo_status evo_hip_attention(const float *projected, size_t rows,
+                                     size_t width, size_t heads,
+                                     int column_split, const float *inv_freq,
+                                     float rope_scale, size_t prefix,
+                                     float *query, float *key_cache,
+                                     float *value_cache, float *out,
+                                     void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

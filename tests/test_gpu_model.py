@@ -1,0 +1,136 @@
+"""End-to-end StripedHyena2 prefill through the evo C ABI (libevo_hip.so,
+backend HIP) against the CPU oracle on identical seeded random-init
+artifacts, and against logits the reference's own CPU build produced
+(tests/golden/*.npz, written by tests/golden/make_golden.py).
+
+Tolerance (stated once, used below): logits and captured block outputs
+satisfy max|hip - ref| <= 1e-3 * max|ref| ("hip-f32" profile), top-1
+agreement 100 %. FP8-projection models compare with the oracle's
+FP8 semantics (codes bit-exact, QGMMA accumulation) at 1e-2 * max|ref|,
+because an E8M13 ulp difference can flip a downstream E4M3 code.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from evo_hip import artifact as A
+from evo_hip import capi
+
+pytestmark = pytest.mark.gpu
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB = os.path.join(ROOT, "evo.cpp_amd", "lib", "libevo_hip.so")
+TOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def hip():
+    return capi.EvoLibrary(LIB)
+
+
+def relmax(a, b):
+    return float(np.abs(a.astype(np.float64) - b).max() / np.abs(b).max())
+
+
+def run_hip(hip, path, tokens, flags=0, context=None, arena=None):
+    if arena:
+        os.environ["EVO_HIP_ARENA_ROWS"] = str(arena)
+    try:
+        model = hip.load(path, capi.BACKEND_HIP)
+        params = hip.lib.evo_context_default_params()
+        params.context_size = context or len(tokens)
+        params.flags = flags
+        import ctypes
+        handle = ctypes.c_void_p()
+        hip.check(hip.lib.evo_context_create(model.handle, ctypes.byref(params),
+                                             ctypes.byref(handle)))
+        ctx = capi.Context(model, handle)
+        logits = ctx.prefill(tokens.astype(np.uint8).tobytes())
+        assert ctx.position == len(tokens)
+        return logits, ctx.profile
+    finally:
+        os.environ.pop("EVO_HIP_ARENA_ROWS", None)
+
+
+def make(tmp_path, shape, seed, **kw):
+    path = str(tmp_path / f"model_{seed}.safetensors")
+    A.random_artifact(shape, seed=seed, **kw).write(path)
+    return path
+
+
+@pytest.mark.parametrize("length,arena", [(100, None), (300, 64), (37, 16)])
+def test_tiny_model_logits(hip, tmp_path, length, arena):
+    shape = A.tiny_shape(width=64, layers=8, heads=4, inner=96, groups=16, attn=(3,))
+    path = make(tmp_path, shape, seed=11)
+    tokens = A.acgt_tokens(length, seed=length)
+    expected = O.OracleModel(path).prefill(tokens)
+    actual, profile = run_hip(hip, path, tokens, arena=arena)
+    assert profile == "hip-f32"
+    assert relmax(actual, expected) <= TOL
+    assert np.array_equal(actual.argmax(1), expected.argmax(1))
+
+
+def test_tiny_model_bf16_profile(hip, tmp_path):
+    shape = A.tiny_shape(width=64, layers=8, heads=4, inner=96, groups=16, attn=(3,))
+    path = make(tmp_path, shape, seed=12)
+    tokens = A.acgt_tokens(120, seed=3)
+    expected = O.OracleModel(path).prefill(tokens)
+    actual, profile = run_hip(hip, path, tokens, flags=1 << 8)
+    assert profile == "hip-bf16"
+    assert relmax(actual, expected) <= 3e-2  # BF16 GEMM activations
+
+
+def fp8_model(tmp_path):
+    shape = A.tiny_shape(width=128, layers=7, heads=4, inner=160, groups=16, attn=(3,))
+    hyena = [i for i in range(shape.layers) if i not in shape.attn]
+    path = make(tmp_path, shape, seed=21, fp8_layers=hyena)
+    tokens = A.acgt_tokens(150, seed=4)
+    return path, tokens, O.OracleModel(path).prefill(tokens)
+
+
+def test_fp8_projection_model_exact(hip, tmp_path):
+    """Integer QGMMA path: codes and per-GEMM results bit-exact, so the model
+    differs from the oracle only by the F32 kernels' rounding."""
+    path, tokens, expected = fp8_model(tmp_path)
+    actual, profile = run_hip(hip, path, tokens, flags=1 << 9)
+    assert profile == "hip-f32+fp8-exact"
+    assert relmax(actual, expected) <= 1e-2
+    assert np.mean(actual.argmax(1) == expected.argmax(1)) >= 0.99
+
+
+def test_fp8_projection_model_mfma(hip, tmp_path):
+    """E4M3 MFMA path (approximate profile): one-ulp BF16 differences of the
+    projection flip downstream E4M3 codes, so the envelope is the reference's
+    approximate-profile style: logits cosine >= 0.999, top-1 >= 95 %."""
+    path, tokens, expected = fp8_model(tmp_path)
+    actual, profile = run_hip(hip, path, tokens)
+    cosine = float((actual.ravel() @ expected.ravel()) /
+                   (np.linalg.norm(actual) * np.linalg.norm(expected)))
+    print(f"fp8 mfma model: relmax {relmax(actual, expected):.3g} cosine {cosine:.6f}")
+    assert cosine >= 0.999
+    assert np.mean(actual.argmax(1) == expected.argmax(1)) >= 0.95
+
+
+def test_golden_reference_logits(hip, tmp_path):
+    """Logits produced by evo.cpp's own CPU library on this artifact."""
+    golden = np.load(os.path.join(ROOT, "tests", "golden", "tiny_reference_logits.npz"))
+    shape = A.tiny_shape(**{k: int(golden[k]) for k in ("width", "layers", "heads", "inner",
+                                                         "groups")}, attn=(3,))
+    path = make(tmp_path, shape, seed=int(golden["seed"]))
+    tokens = golden["tokens"]
+    actual, _ = run_hip(hip, path, tokens)
+    assert relmax(actual, golden["logits"]) <= TOL
+    assert np.array_equal(actual.argmax(1), golden["logits"].argmax(1))
+
+
+def test_evo2_1b_shape_config1(hip, tmp_path):
+    """1B-shaped SH2 (25 blocks, W 1920, 15 heads, FFN 5120),
+    128 ACGT tokens, seeded random-init weights."""
+    shape = A.evo2_1b_shape()
+    path = make(tmp_path, shape, seed=1, init="unit")
+    tokens = A.acgt_tokens(128, seed=1)
+    expected = O.OracleModel(path).prefill(tokens, threads=16)
+    actual, _ = run_hip(hip, path, tokens)
+    assert relmax(actual, expected) <= TOL
+    assert np.array_equal(actual.argmax(1), expected.argmax(1))

@@ -1,0 +1,312 @@
+"""GPU parity of each gfx950 kernel, called through the operator C ABI
+(include/evo/hip_ops.h), against the CPU oracle on identical seeded inputs.
+
+Tolerances are stated per test: bit-exact for FP8 codes and the exact QGMMA
+mode; relative (to the output scale) for floating-point kernels.
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from evo_hip import native as N
+from evo_hip.artifact import bf16_bits, bf16_to_f32
+from gpu_util import dev, empty, host, p, stream, zeros
+
+pytestmark = pytest.mark.gpu
+
+
+def rng(seed):
+    return np.random.Generator(np.random.PCG64(seed))
+
+
+def rel_err(actual, expected):
+    scale = max(1e-30, float(np.abs(expected).max()))
+    return float(np.abs(actual.astype(np.float64) - expected).max()) / scale
+
+
+# ------------------------------------------------------------------ FP8
+FP8_VALUES = [-448.0, -432.0, -416.0, -1.25, -1.1875, -1.125, -1.0625, -1.0, -0.5,
+              -0.015625, -0.00390625, -0.001953125, -0.0009765625, -0.0, 0.0,
+              0.0009765625, 0.001953125, 0.0029296875, 0.00390625, 0.015625, 0.5,
+              1.0, 1.0625, 1.125, 1.1875, 1.25, 416.0, 432.0, 448.0]
+FP8_CODES = [0xfe, 0xfe, 0xfd, 0xba, 0xba, 0xb9, 0xb8, 0xb8, 0xb0, 0x88, 0x82, 0x81,
+             0x80, 0x80, 0x00, 0x00, 0x01, 0x02, 0x02, 0x08, 0x30, 0x38, 0x38, 0x39,
+             0x3a, 0x3a, 0x7d, 0x7e, 0x7e]
+
+
+def quantize_gpu(x: np.ndarray, scale: float, dtype=N.DTYPE_F32):
+    d = dev(x)
+    codes = empty(x.shape, np.uint8)
+    N.call("evo_hip_e4m3_quantize", dtype, p(d), x.size, scale, p(codes), stream())
+    return host(codes)
+
+
+def test_e4m3_reference_vectors():
+    """The 29 PyTorch code vectors of evo.cpp tests/test_cuda_ops.cu:371-431."""
+    bits = bf16_bits(np.array(FP8_VALUES, np.float32))
+    assert list(quantize_gpu(bits, 1.0, N.DTYPE_BF16)) == FP8_CODES
+    assert list(quantize_gpu(np.array(FP8_VALUES, np.float32), 1.0)) == FP8_CODES
+
+
+@pytest.mark.parametrize("scale", [1.0, 5.75, 3.25, 56.0, 0.03125, 448.0 / 6.1])
+def test_e4m3_exhaustive_bf16(oracle, scale):
+    """Every BF16 bit pattern (incl. inf/NaN/subnormals), bit-exact codes."""
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    expected = np.zeros(65536, np.uint8)
+    oracle.oracle_e4m3_quantize_bf16(O.ptr(bits), bits.size, scale, O.ptr(expected))
+    assert np.array_equal(quantize_gpu(bits, scale, N.DTYPE_BF16), expected)
+
+
+def test_e4m3_f32_rounds_through_bf16(oracle):
+    x = rng(1).standard_normal(1 << 16).astype(np.float32) * 3
+    assert np.array_equal(quantize_gpu(x, 56.0), O.quantize_f32(x, 56.0))
+
+
+def fp8_case(seed, m, k, n, in_scale=5.75, w_scale=3.25):
+    r = rng(seed)
+    a = bf16_to_f32(bf16_bits(r.standard_normal((m, k)).astype(np.float32) * 2))
+    w = bf16_to_f32(bf16_bits(r.standard_normal((n, k)).astype(np.float32) * 0.05))
+    return O.quantize_f32(a, in_scale), O.quantize_f32(w, w_scale)
+
+
+def fp8_gpu(a_codes, w_codes, out_scale, mode):
+    m, k = a_codes.shape
+    n = w_codes.shape[0]
+    out = empty((m, n))
+    N.call("evo_hip_fp8_linear", p(dev(a_codes)), p(dev(w_codes)), p(out), m, n, k,
+           out_scale, mode, stream())
+    return host(out)
+
+
+@pytest.mark.parametrize("m,k,n", [(3, 64, 5), (1, 64, 5), (130, 256, 96), (64, 4096, 40)])
+def test_qgmma_exact_bit_exact(m, k, n):
+    """Reference case shape rows 3, K 64, N 5, scales 5.75/3.25/0.03125
+    (tests/test_cuda_ops.cu:433-503) and larger ragged shapes."""
+    a, w = fp8_case(7 + m, m, k, n)
+    expected = O.qgmma(a, w, 0.03125)
+    actual = fp8_gpu(a, w, 0.03125, N.FP8_EXACT)
+    assert np.array_equal(actual.view(np.uint32), expected.view(np.uint32))
+
+
+@pytest.mark.parametrize("mode", [N.FP8_MFMA_K32, N.FP8_MFMA_K128])
+@pytest.mark.parametrize("m,k,n", [(128, 128, 128), (200, 512, 300), (1024, 4096, 256)])
+def test_fp8_mfma_close_to_qgmma(mode, m, k, n):
+    """MFMA chunks are F32-exact sums; they differ from QGMMA only by its
+    per-term truncation (a few E8M13 ulps, 2^-13 relative), which can move the
+    final BF16 rounding by one BF16 ulp: bound per element 2^-7 |ref| plus
+    2^-12 of the output scale, and at most 10 % of the elements may differ."""
+    a, w = fp8_case(11 + m, m, k, n)
+    expected = O.qgmma(a, w, 0.03125)
+    actual = fp8_gpu(a, w, 0.03125, mode)
+    bound = 2.0 ** -7 * np.abs(expected) + 2.0 ** -12 * np.abs(expected).max()
+    assert np.all(np.abs(actual - expected) <= bound)
+    assert np.mean(actual != expected) < 0.10
+
+
+def test_fp8_mfma_exact_on_representable_sums():
+    """Codes restricted to +-{1, 1.5, 2}: every QGMMA term and partial sum is
+    exact, so all three modes must agree bit for bit."""
+    r = rng(5)
+    choices = np.array([0x38, 0x3c, 0x40, 0xb8, 0xbc, 0xc0], np.uint8)
+    a = choices[r.integers(0, 6, (64, 256))]
+    w = choices[r.integers(0, 6, (96, 256))]
+    exact = fp8_gpu(a, w, 1.0, N.FP8_EXACT)
+    for mode in (N.FP8_MFMA_K32, N.FP8_MFMA_K128):
+        assert np.array_equal(fp8_gpu(a, w, 1.0, mode), exact)
+    dense = O.lib()  # closed form: plain dot of the decoded values
+    dec = np.vectorize(lambda c: dense.oracle_e4m3_decode(int(c)))
+    ref = dec(a).astype(np.float64) @ dec(w).astype(np.float64).T
+    # the reference rounds the promoted accumulator to BF16 on output
+    assert np.array_equal(exact, bf16_to_f32(bf16_bits(ref.astype(np.float32))))
+
+
+# ---------------------------------------------------------------- GEMM
+@pytest.mark.parametrize("m,n,k", [(1, 40, 64), (130, 200, 72), (256, 384, 1024)])
+@pytest.mark.parametrize("bias,residual", [(False, False), (True, True), (False, True)])
+def test_linear_split_matches_oracle(m, n, k, bias, residual):
+    r = rng(m + n + k)
+    x = r.standard_normal((m, k)).astype(np.float32)
+    w = bf16_bits(r.standard_normal((n, k)).astype(np.float32) / np.sqrt(k))
+    b = bf16_bits(r.standard_normal(n).astype(np.float32) * 0.1) if bias else None
+    res = r.standard_normal((m, n)).astype(np.float32) if residual else None
+    expected = O.linear_bf16w(x, w, b)
+    if residual:
+        expected = expected + res
+    out = empty((m, n))
+    N.call("evo_hip_linear", p(dev(x)), p(dev(w)), p(dev(b) if bias else None),
+           p(dev(res) if residual else None), m, n, k, 1, p(out), stream())
+    # split-BF16 activations: ~2^-17 relative per product, F32 accumulation
+    assert rel_err(host(out), expected) < 2e-5
+
+
+def test_linear_bf16_profile_is_bf16_accurate():
+    r = rng(3)
+    x = r.standard_normal((96, 512)).astype(np.float32)
+    w = bf16_bits(r.standard_normal((160, 512)).astype(np.float32) / 22.6)
+    out = empty((96, 160))
+    N.call("evo_hip_linear", p(dev(x)), p(dev(w)), None, None, 96, 160, 512, 0,
+           p(out), stream())
+    expected = O.linear_bf16w(bf16_to_f32(bf16_bits(x)), w)
+    assert rel_err(host(out), expected) < 2e-5
+
+
+@pytest.mark.parametrize("gelu", [1, 0])
+def test_gated_mlp(gelu):
+    from scipy.special import erf
+    r = rng(17 + gelu)
+    m, width, inner = 70, 96, 80  # inner not a multiple of 32: padded block
+    x = r.standard_normal((m, width)).astype(np.float32)
+    l1 = bf16_bits(r.standard_normal((inner, width)).astype(np.float32) / 10)
+    l2 = bf16_bits(r.standard_normal((inner, width)).astype(np.float32) / 10)
+    l3 = bf16_bits(r.standard_normal((width, inner)).astype(np.float32) / 9)
+    res = r.standard_normal((m, width)).astype(np.float32)
+    padded = (inner + 31) // 32 * 32
+    w12 = zeros((2 * padded, width), np.uint16)
+    N.call("evo_hip_pack_mlp", p(dev(l1)), p(dev(l2)), inner, width, p(w12), stream())
+    scratch, out = empty((m, inner)), empty((m, width))
+    N.call("evo_hip_gated_mlp", p(dev(x)), p(w12), p(dev(l3)), m, width, inner, gelu, 1,
+           p(scratch), p(dev(res)), p(out), stream())
+    first = O.linear_bf16w(x, l1).astype(np.float64)
+    second = O.linear_bf16w(x, l2).astype(np.float64)
+    act = 0.5 * first * (1 + erf(first / np.sqrt(2))) if gelu else first
+    expected = O.linear_bf16w((act * second).astype(np.float32), l3) + res
+    assert rel_err(host(out), expected) < 1e-4
+
+
+def test_rms_norm(oracle):
+    r = rng(9)
+    for rows, width in [(3, 257), (64, 4096), (5, 1920)]:
+        x = r.standard_normal((rows, width)).astype(np.float32) * 3
+        scale = (1 + 0.1 * r.standard_normal(width)).astype(np.float32)
+        expected = np.zeros_like(x)
+        oracle.oracle_rms_norm(O.ptr(x), rows, width, O.ptr(scale), 1e-6, O.ptr(expected))
+        out = empty((rows, width))
+        N.call("evo_hip_rms_norm", p(dev(x)), rows, width, p(dev(scale)), 1e-6, p(out),
+               stream())
+        assert rel_err(host(out), expected) < 1e-5
+
+
+# --------------------------------------------------------------- Hyena
+def hyena_case(seed, kind, length, width, groups=16, inner_len=7, state=16):
+    r = rng(seed)
+    proj = r.standard_normal((length, 3 * width)).astype(np.float32)
+    short = bf16_bits(r.standard_normal((3 * width, 3)).astype(np.float32) * 0.5)
+    case = dict(projection=proj, short=short, width=width)
+    if kind in (N.HYENA_HCS, N.HYENA_HCM):
+        case["inner"] = bf16_to_f32(bf16_bits(
+            r.standard_normal((groups, inner_len)).astype(np.float32) / np.sqrt(inner_len)))
+        case["groups"], case["inner_len"] = groups, inner_len
+    if kind in (N.HYENA_HCM, N.HYENA_HCL):
+        case["direct"] = bf16_to_f32(bf16_bits(r.standard_normal(width).astype(np.float32) * 0.5))
+    if kind == N.HYENA_HCL:
+        case["log_poles"] = np.log(r.uniform(0.5, 0.99, (width, state))).astype(np.float32)
+        case["residues"] = (r.standard_normal((width, state)) * 0.1).astype(np.float32)
+        case["state"] = state
+    return case
+
+
+def hyena_oracle(kind, case, projection=None):
+    return O.hyena_mixer(kind, case["projection"] if projection is None else projection,
+                         case["width"], bf16_to_f32(case["short"]), case.get("inner"),
+                         case.get("groups", 1), case.get("inner_len", 2),
+                         case.get("direct"), case.get("log_poles"), case.get("residues"),
+                         case.get("state", 0))
+
+
+def hyena_gpu(kind, case, dtype=N.DTYPE_F32, rows=None, caches=None, projection=None):
+    proj = case["projection"] if projection is None else projection
+    length = proj.shape[0] if rows is None else rows
+    width = case["width"]
+    state = case.get("state", 0)
+    poles = np.exp(case["log_poles"]).astype(np.float32) if "log_poles" in case else None
+    ws_bytes = N.call("evo_hip_hyena_workspace_bytes", kind, length, width, state)
+    ws = empty((max(ws_bytes, 256),), np.uint8)
+    if dtype == N.DTYPE_BF16:
+        proj_d = dev(bf16_bits(proj))
+        out = empty((length, width), np.uint16)
+    else:
+        proj_d = dev(proj)
+        out = empty((length, width))
+    caches = caches or {}
+    N.call("evo_hip_hyena_forward", kind, dtype, p(proj_d), length, width,
+           p(dev(case["short"])), 3, p(dev(case["inner"]) if "inner" in case else None),
+           case.get("groups", 1), case.get("inner_len", 0),
+           p(dev(case["direct"]) if "direct" in case else None),
+           p(dev(poles) if poles is not None else None),
+           p(dev(case["residues"]) if "residues" in case else None), state,
+           p(caches.get("short")), p(caches.get("inner")), p(caches.get("modal")),
+           p(ws), ws_bytes, p(out), stream())
+    result = host(out)
+    return bf16_to_f32(result.view(np.uint16)) if dtype == N.DTYPE_BF16 else result
+
+
+KINDS = [(N.HYENA_HCS, 7), (N.HYENA_HCM, 128), (N.HYENA_HCL, 0)]
+
+
+@pytest.mark.parametrize("kind,inner_len", KINDS)
+@pytest.mark.parametrize("length,width", [(1, 64), (300, 96), (1000, 128)])
+def test_hyena_f32_matches_oracle(kind, inner_len, length, width):
+    case = hyena_case(length + width + kind, kind, length, width, groups=16,
+                      inner_len=inner_len or 7)
+    expected = hyena_oracle(kind, case)
+    assert rel_err(hyena_gpu(kind, case), expected) < 1e-5
+
+
+@pytest.mark.parametrize("kind,inner_len", KINDS)
+def test_hyena_bf16_io(kind, inner_len):
+    """BF16 projection in, BF16 output: compare with the oracle on the same
+    BF16-rounded projection; the only extra error is the output rounding."""
+    case = hyena_case(77 + kind, kind, 777, 128, inner_len=inner_len or 7)
+    proj = bf16_to_f32(bf16_bits(case["projection"]))
+    expected = hyena_oracle(kind, case, projection=proj)
+    actual = hyena_gpu(kind, case, dtype=N.DTYPE_BF16)
+    assert np.abs(actual - expected).max() <= 2.0 ** -8 * np.abs(expected).max()
+
+
+@pytest.mark.parametrize("kind,inner_len", KINDS)
+@pytest.mark.parametrize("split", [1, 5, 130, 299])
+def test_hyena_continuation_equals_one_pass(kind, inner_len, split):
+    """Two calls sharing the FIR histories / modal state equal one call."""
+    case = hyena_case(5 + kind, kind, 300, 64, inner_len=inner_len or 7)
+    width = 64
+    whole = hyena_gpu(kind, case)
+    hist = inner_len - 1 if inner_len else 0
+    caches = {"short": zeros((2, 3 * width)),
+              "inner": zeros((max(hist, 1), width)) if hist else None,
+              "modal": zeros((width, 16)) if kind == N.HYENA_HCL else None}
+    first = hyena_gpu(kind, case, projection=case["projection"][:split], caches=caches)
+    second = hyena_gpu(kind, case, projection=case["projection"][split:], caches=caches)
+    joined = np.concatenate([first, second])
+    assert rel_err(joined, whole) < 1e-5
+
+
+# ----------------------------------------------------------- attention
+@pytest.mark.parametrize("rows,heads,head_dim,prefix", [(70, 4, 16, 0), (130, 2, 128, 0),
+                                                        (64, 3, 64, 33)])
+def test_attention_matches_oracle(oracle, rows, heads, head_dim, prefix):
+    r = rng(rows + heads)
+    width = heads * head_dim
+    total = prefix + rows
+    # projections of all `total` positions; the first `prefix` rows are
+    # appended to the cache by a first call.
+    proj = r.standard_normal((total, 3 * width)).astype(np.float32)
+    inv_freq = (1.0 / 10000 ** (np.arange(0, head_dim, 2) / head_dim)).astype(np.float32)
+    # oracle: column_split head-major layout [h][q,k,v][d]
+    qkv = proj.reshape(total, heads, 3, head_dim)
+    q = np.ascontiguousarray(qkv[:, :, 0]).reshape(total * heads * head_dim)
+    k = np.ascontiguousarray(qkv[:, :, 1]).reshape(total * heads * head_dim)
+    v = np.ascontiguousarray(qkv[:, :, 2]).reshape(total * heads * head_dim)
+    O.check(oracle.oracle_apply_rope(O.ptr(q), O.ptr(k), total, heads, head_dim,
+                                     O.ptr(inv_freq), 0, 8.0))
+    expected = np.zeros_like(q)
+    O.check(oracle.oracle_causal_attention(O.ptr(q), O.ptr(k), O.ptr(v), total, heads,
+                                           head_dim, O.ptr(expected)))
+    expected = expected.reshape(total, width)[prefix:]
+    kc, vc = zeros((total, width)), zeros((total, width))
+    query, out = empty((total, width)), empty((total, width))
+    if prefix:
+        N.call("evo_hip_attention", p(dev(proj[:prefix])), prefix, width, heads, 1,
+               p(dev(inv_freq)), 8.0, 0, p(query), p(kc), p(vc), p(out), stream())
+    N.call("evo_hip_attention", p(dev(proj[prefix:])), rows, width, heads, 1,
+           p(dev(inv_freq)), 8.0, prefix, p(query), p(kc), p(vc), p(out), stream())
+    assert rel_err(host(out)[:rows], expected) < 1e-5
