@@ -1,0 +1,255 @@
+"""Prefill benchmark of the MI355X StripedHyena2 library.
+
+Workload: Evo-2-7B-shaped model (32 blocks, width 4096, 32 heads, FFN 11264,
+byte vocab 512; hyena short/medium-128/long striping with attention at blocks
+3, 10, 17, 24, 31), seeded random-init weights (BF16 linears, Hyena input
+projections converted to software E4M3 at load), batch-1 prefill of 8192
+uniform ACGT tokens. One "step" = one full prefill with tokens and logits
+resident in HBM (evo_hip_context_prefill_resident).
+
+Also measured live (HIP events on the launching stream, algorithmic work
+only): the dominant kernel (MLP l1/l2 GEMM, M=8192 N=2x11264 K=4096), the
+fused Hyena long-conv operator (config 2, BF16 I/O, L=8192 W=4096) and the
+FP8 projection GEMM (config 3, M=1024 K=4096 N=12288); and, on the host
+cores, evo.cpp's own CPU library (oracle/_ref) on a bounded 16-token sample
+of the same artifact.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--tokens L]
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "evo.cpp_amd"))
+
+from evo_hip import artifact as A  # noqa: E402
+from evo_hip import capi, native  # noqa: E402
+
+METRIC = "prefill tok/s at 1 GPU, 7B-shape @1k/8k tok; % HBM BW and % FP8 MFMA peak"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+FP8_PEAK_TFLOPS = 5000.0
+LIB = os.path.join(ROOT, "evo.cpp_amd", "lib", "libevo_hip.so")
+REF_LIB = os.path.join(ROOT, "oracle", "_ref", "libevo_ref.so")
+
+
+def log(message):
+    print(f"[bench] {message}", file=sys.stderr, flush=True)
+
+
+def artifact_path(directory):
+    shape = A.evo2_7b_shape()
+    art = A.random_artifact(shape, seed=0, init="survey")
+    path = os.path.join(directory, "evo2_7b_shape_seed0_survey.safetensors")
+    expected = sum(s.nbytes for s in art.specs)
+    if not (os.path.exists(path) and os.path.getsize(path) > expected):
+        os.makedirs(directory, exist_ok=True)
+        log(f"writing 7B-shaped artifact ({expected / 1e9:.1f} GB) to {path}")
+        start = time.time()
+        art.write(path + ".tmp")
+        os.replace(path + ".tmp", path)
+        log(f"artifact written in {time.time() - start:.0f} s")
+    return path, shape
+
+
+def event_time(fn, repeats):
+    """Average launch duration of fn() on torch's current stream (ms)."""
+    import torch
+    fn()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(repeats):
+        fn()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / repeats
+
+
+def kernel_rooflines(split):
+    import torch
+    stream = torch.cuda.current_stream().cuda_stream
+    g = torch.Generator(device="cuda").manual_seed(0)
+    out = {}
+    # dominant kernel: gated MLP l1/l2 GEMM of one block at L=8192
+    m, n, k = 8192, 2 * 11264, 4096
+    x = torch.randn(m, k, device="cuda", generator=g)
+    w = (torch.randn(n, k, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    y = torch.empty(m, n, device="cuda")
+    ms = event_time(lambda: native.call("evo_hip_linear", x.data_ptr(), w.data_ptr(), None,
+                                        None, m, n, k, 1 if split else 0, y.data_ptr(),
+                                        stream), 5)
+    flops = 2.0 * m * n * k
+    out["gemm"] = dict(kernel="gemm_bf16w_kernel<%s>" % ("true" if split else "false"),
+                       ms=ms, flops=flops, tflops=flops / ms / 1e9)
+    del x, w, y
+    # config 2: fused Hyena HCL operator, BF16 [8192, 12288] in, [8192, 4096] out
+    length, width, state = 8192, 4096, 16
+    proj = torch.randn(length, 3 * width, device="cuda", generator=g).to(torch.bfloat16)
+    short = (torch.randn(3 * width, 3, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    poles = torch.rand(width, state, device="cuda", generator=g) * 0.49 + 0.5
+    residues = torch.randn(width, state, device="cuda", generator=g) * 0.02
+    direct = torch.randn(width, device="cuda", generator=g) * 0.02
+    ws_bytes = native.call("evo_hip_hyena_workspace_bytes", 2, length, width, state)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    yb = torch.empty(length, width, dtype=torch.bfloat16, device="cuda")
+    ms = event_time(lambda: native.call(
+        "evo_hip_hyena_forward", 2, 1, proj.data_ptr(), length, width, short.data_ptr(), 3,
+        None, 1, 0, direct.data_ptr(), poles.data_ptr(), residues.data_ptr(), state, None,
+        None, None, ws.data_ptr(), ws_bytes, yb.data_ptr(), stream), 10)
+    hbm_bytes = length * 3 * width * 2 + length * width * 2
+    out["hyena"] = dict(kernel="hcl operator (chunk_state + carry + output)", ms=ms,
+                        bytes=hbm_bytes, gbs=hbm_bytes / ms / 1e6)
+    del proj, yb, ws
+    # config 3: FP8 projection GEMM M=1024 K=4096 N=12288 (promotion every 32 K)
+    m, k, n = 1024, 4096, 12288
+    a8 = torch.randint(0, 0x7e, (m, k), dtype=torch.uint8, device="cuda", generator=g)
+    w8 = torch.randint(0, 0x7e, (n, k), dtype=torch.uint8, device="cuda", generator=g)
+    y8 = torch.empty(m, n, device="cuda")
+    for mode, name in ((0, "fp8_k32"), (1, "fp8_k128")):
+        ms = event_time(lambda: native.call("evo_hip_fp8_linear", a8.data_ptr(),
+                                            w8.data_ptr(), y8.data_ptr(), m, n, k, 1e-3,
+                                            mode, stream), 10)
+        flops = 2.0 * m * n * k
+        out[name] = dict(kernel=f"fp8_mfma_kernel<{32 if mode == 0 else 128}>", ms=ms,
+                         flops=flops, tflops=flops / ms / 1e9)
+    return out
+
+
+def cpu_baseline(path, sample_tokens):
+    """evo.cpp's CPU F32 prefill (single-threaded by construction) on a
+    bounded sample of the same artifact, through its own C ABI."""
+    if os.path.exists(REF_LIB):
+        library, kind, backend = capi.EvoLibrary(REF_LIB), "reference", capi.BACKEND_CPU
+    else:
+        return None
+    tokens = A.acgt_tokens(sample_tokens, seed=1).astype(np.uint8).tobytes()
+    model = library.load(path, backend)
+    context = model.context(sample_tokens)
+    start = time.time()
+    context.prefill(tokens)
+    seconds = time.time() - start
+    return {"value": sample_tokens / seconds, "unit": "tok/s", "cores": 1, "kind": kind,
+            "sample": f"{sample_tokens}-token prefill of the same 7B-shaped artifact "
+                      f"(BF16 projections; reference cpu-f32 path, {seconds:.1f} s; "
+                      f"host has {os.cpu_count()} cores)"}
+
+
+def main():
+    parser = argparse.ArgumentParser()
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=10)
+    parser.add_argument("--warmup", type=int, default=2)
+    parser.add_argument("--tokens", type=int, default=8192)
+    parser.add_argument("--profile", choices=["f32", "bf16"], default="f32")
+    parser.add_argument("--artifact-dir", default="/tmp/evo_bench")
+    parser.add_argument("--cpu-sample", type=int, default=16)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-kernels", action="store_true")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus} is not supported: this build runs on one "
+              "MI355X; the multi-GPU layout is described in DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    path, shape = artifact_path(args.artifact_dir)
+    hip = capi.EvoLibrary(LIB)
+    native.load()
+    log("loading model (FP8 Hyena projections at load)")
+    model = hip.load(path, capi.BACKEND_HIP, flags=1 << 8)
+    params = hip.lib.evo_context_default_params()
+    params.context_size = max(args.tokens, 1024)
+    params.flags = 0 if args.profile == "f32" else (1 << 8)
+    handle = ctypes.c_void_p()
+    hip.check(hip.lib.evo_context_create(model.handle, ctypes.byref(params),
+                                         ctypes.byref(handle)))
+    context = capi.Context(model, handle)
+    lib = native.load()
+    lib.evo_hip_context_prefill_resident.argtypes = [ctypes.c_void_p, ctypes.c_void_p,
+                                                      ctypes.c_size_t, ctypes.c_void_p]
+
+    def resident_rate(length, steps, warmup):
+        tokens = torch.from_numpy(A.acgt_tokens(length, seed=2).astype(np.int32)).cuda()
+        logits = torch.empty(length, shape.vocab, device="cuda")
+
+        def step():
+            status = lib.evo_hip_context_prefill_resident(handle, tokens.data_ptr(), length,
+                                                         logits.data_ptr())
+            if status != 0:
+                raise RuntimeError(lib.evo_last_error().decode())
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        start = time.perf_counter()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        seconds = time.perf_counter() - start
+        return length * steps / seconds, 1e3 * seconds / steps
+
+    log(f"timing {args.steps} prefills of {args.tokens} tokens")
+    value, ms_per_step = resident_rate(args.tokens, args.steps, args.warmup)
+    rate_1k, ms_1k = resident_rate(1024, max(args.steps, 5), 2)
+    # C-ABI rate with host logits (PCIe-inclusive; not the headline value)
+    seq = A.acgt_tokens(args.tokens, seed=2).astype(np.uint8).tobytes()
+    ctx2 = model.context(args.tokens)
+    start = time.perf_counter()
+    ctx2.prefill(seq)
+    cabi_rate = args.tokens / (time.perf_counter() - start)
+    ctx2.close()
+
+    result = {
+        "metric": METRIC, "value": round(value, 1), "unit": "tok/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp8-e4m3 projections + f32 (split-bf16 MFMA)" if args.profile == "f32"
+                 else "fp8-e4m3 projections + bf16 MFMA",
+        "data": "synthetic (seeded random-init weights, uniform ACGT tokens)",
+        "config": {"workload": f"evo2-7b-shape prefill L={args.tokens}, batch 1, "
+                               "fp8 hyena projections (BASELINE config 4)",
+                   "tokens": args.tokens, "layers": shape.layers, "width": shape.width,
+                   "heads": shape.heads, "ffn": shape.inner,
+                   "profile": context.profile, "tok_s_1k": round(rate_1k, 1),
+                   "ms_per_step_1k": round(ms_1k, 3),
+                   "c_abi_host_logits_tok_s": round(cabi_rate, 1)},
+    }
+    if not args.no_kernels:
+        log("kernel rooflines")
+        kernels = kernel_rooflines(args.profile == "f32")
+        g = kernels["gemm"]
+        result["roofline"] = {"bound": "mfma", "kernel": g["kernel"],
+                              "achieved": round(g["tflops"], 1), "peak": BF16_PEAK_TFLOPS,
+                              "unit": "TFLOP/s", "frac": round(g["tflops"] / BF16_PEAK_TFLOPS, 4),
+                              "traffic": None, "ms": round(g["ms"], 4),
+                              "per_launch": "2*8192*22528*4096 flop (MLP l1/l2 of one block)"}
+        h = kernels["hyena"]
+        result["hyena_roofline"] = {"bound": "hbm", "kernel": h["kernel"],
+                                    "achieved": round(h["gbs"], 1), "peak": HBM_PEAK_GBS,
+                                    "unit": "GB/s", "frac": round(h["gbs"] / HBM_PEAK_GBS, 4),
+                                    "ms": round(h["ms"], 4),
+                                    "per_launch": "268435456 B (read [8192,12288] + write [8192,4096] BF16)"}
+        for name in ("fp8_k32", "fp8_k128"):
+            f = kernels[name]
+            result[name + "_roofline"] = {"bound": "mfma", "kernel": f["kernel"],
+                                          "achieved": round(f["tflops"], 1),
+                                          "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                          "frac": round(f["tflops"] / FP8_PEAK_TFLOPS, 4),
+                                          "ms": round(f["ms"], 4)}
+    context.close()
+    model.close()
+    torch.cuda.empty_cache()
+    if not args.no_cpu_baseline:
+        log(f"CPU baseline: reference library, {args.cpu_sample}-token sample")
+        result["cpu_baseline"] = cpu_baseline(path, args.cpu_sample)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

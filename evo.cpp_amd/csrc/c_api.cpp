@@ -211,7 +211,9 @@ evo_status evo_model_load(const char *path, const evo_model_params *params,
     if (options.backend != EVO_BACKEND_AUTO && options.backend != EVO_BACKEND_HIP)
       return publish(EVO_STATUS_UNSUPPORTED,
                      "unsupported: this evo library implements the HIP backend only");
-    if ((options.flags & ~static_cast<uint32_t>(EVO_MODEL_FLAG_TEST_ONLY_ALLOW_SYNTHETIC)) != 0 ||
+    const uint32_t known_flags = EVO_MODEL_FLAG_TEST_ONLY_ALLOW_SYNTHETIC |
+                                 EVO_MODEL_FLAG_HIP_FP8_PROJECTIONS;
+    if ((options.flags & ~known_flags) != 0 ||
         options.device_count > 1 || (options.device_count != 0 && options.devices == nullptr))
       return publish(EVO_STATUS_INVALID_ARGUMENT,
                      "invalid_argument: invalid model flags/device list (one device)");
@@ -233,7 +235,8 @@ evo_status evo_model_load(const char *path, const evo_model_params *params,
                      "unsupported: artifact architecture/profile/ABI is not registered");
     state->weights = std::make_shared<evo::hip::Model>();
     status = state->weights->load(state->artifact, state->device,
-                                  (options.flags & EVO_MODEL_FLAG_TEST_ONLY_ALLOW_SYNTHETIC) != 0);
+                                  (options.flags & EVO_MODEL_FLAG_TEST_ONLY_ALLOW_SYNTHETIC) != 0,
+                                  (options.flags & EVO_MODEL_FLAG_HIP_FP8_PROJECTIONS) != 0);
     if (!status.ok())
       return publish(status);
     state->model_id = state->weights->config().model_id;
@@ -526,6 +529,27 @@ evo_status evo_sampler_sample(evo_sampler *sampler, const float *logits, size_t 
 }
 
 // ------------------------------------------------------------ operator ABI
+evo_status evo_hip_context_prefill_resident(evo_context *context, const uint32_t *tokens,
+                                            size_t count, float *logits) {
+  return protect([&]() -> evo_status {
+    if (context == nullptr || !context->hip)
+      return publish(EVO_STATUS_INVALID_ARGUMENT, "invalid_argument: context is null");
+    if (context->failed)
+      return publish(EVO_STATUS_INVALID_ARGUMENT,
+                     "invalid_argument: context is invalid after a prior failure");
+    context->failed = true;
+    const auto status = context->hip->prefill_resident(tokens, count, logits);
+    if (!status.ok())
+      return publish(status);
+    context->failed = false;
+    return publish(evo::Status::Ok());
+  });
+}
+
+void *evo_hip_context_stream(const evo_context *context) {
+  return context == nullptr || !context->hip ? nullptr : context->hip->stream();
+}
+
 size_t evo_hip_hyena_workspace_bytes(evo_hip_hyena_kind kind, size_t length, size_t width,
                                      size_t state_size) {
   return evo::hip::hyena_workspace_bytes(static_cast<int>(kind), length, width, state_size);

@@ -12,14 +12,22 @@
 namespace evo::hip {
 namespace {
 
+// Token ids outside the vocabulary produce zero rows and raise *invalid.
 __global__ void embed_kernel(const uint32_t *__restrict__ tokens, size_t rows,
-                             const uint16_t *__restrict__ table, size_t width,
-                             float *__restrict__ out) {
+                             const uint16_t *__restrict__ table, size_t vocab,
+                             size_t width, float *__restrict__ out,
+                             int *__restrict__ invalid) {
   const size_t n = rows * width;
   for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
        i < n; i += static_cast<size_t>(gridDim.x) * blockDim.x) {
     const size_t row = i / width, col = i % width;
-    out[i] = bf16_to_f32(table[static_cast<size_t>(tokens[row]) * width + col]);
+    const uint32_t token = tokens[row];
+    if (token >= vocab) {
+      out[i] = 0.0F;
+      *invalid = 1;
+      continue;
+    }
+    out[i] = bf16_to_f32(table[static_cast<size_t>(token) * width + col]);
   }
 }
 
@@ -88,15 +96,15 @@ __global__ void update_history_kernel(const float *__restrict__ x, size_t rows,
 }  // namespace
 
 Status embed_tokens(const uint32_t *tokens, size_t rows, const uint16_t *table,
-                    size_t vocab, size_t width, float *out, hipStream_t stream) {
-  (void)vocab;  // token ids are validated on the host before upload
-  if (tokens == nullptr || table == nullptr || out == nullptr || rows == 0 ||
-      width == 0)
+                    size_t vocab, size_t width, float *out, int *invalid,
+                    hipStream_t stream) {
+  if (tokens == nullptr || table == nullptr || out == nullptr || invalid == nullptr ||
+      rows == 0 || width == 0)
     return {ErrorCode::kInvalidArgument, "embed_tokens: invalid arguments"};
   const size_t n = rows * width;
   const unsigned grid = static_cast<unsigned>(std::min<size_t>((n + 255) / 256, 16384));
   hipLaunchKernelGGL(embed_kernel, dim3(grid), dim3(256), 0, stream, tokens, rows,
-                     table, width, out);
+                     table, vocab, width, out, invalid);
   return launch_status("embed_kernel");
 }
 

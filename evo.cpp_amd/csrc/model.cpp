@@ -12,6 +12,7 @@ namespace evo::hip {
 namespace {
 
 constexpr size_t kArenaRows = 8192;  // activation rows per prefill chunk
+constexpr float kFp8InputAmax = 8.0F;  // activation amax of load-time FP8 conversion
 
 Status hip_check(hipError_t error, const std::string &what) {
   if (error == hipSuccess)
@@ -99,7 +100,8 @@ void DeviceBuffer::reset() {
 
 // ---------------------------------------------------------------- Model load
 // Tensor set, shapes and dtypes: evo.cpp `src/cpu/model.cpp:2651-2874`.
-Status Model::load(const Artifact &a, int device, bool allow_synthetic) {
+Status Model::load(const Artifact &a, int device, bool allow_synthetic,
+                   bool fp8_projections) {
   device_ = device;
   EVO_TRY(hip_check(hipSetDevice(device), "select device"));
   ModelConfig &c = config_;
@@ -234,8 +236,38 @@ Status Model::load(const Artifact &a, int device, bool allow_synthetic) {
     }
     EVO_TRY(view(a, p + ".projections.weight", {3 * w, w}, DType::kBF16, &t, false, true));
     L.fp8 = t->dtype == DType::kE4M3;
-    EVO_TRY(upload_view(&L.projection, *t, p + ".projections.weight"));
-    if (L.fp8) {
+    if (!L.fp8 && fp8_projections) {
+      // Load-time software-FP8 conversion of a BF16 projection, the
+      // converter's per-tensor rule (`tools/evo/checkpoint.py:393-396`):
+      // weight_scale = 448 / amax(W), codes = E4M3(W * weight_scale),
+      // output_scale = 1 / (input_scale * weight_scale). The activation scale
+      // is the fixed TE-style 448 / kFp8InputAmax.
+      const auto *bits = reinterpret_cast<const uint16_t *>(t->data);
+      uint16_t top = 0;
+      for (uint64_t e = 0; e < t->elements(); ++e) {
+        const uint16_t magnitude = bits[e] & 0x7fffU;
+        if (magnitude <= 0x7f80U)  // finite or inf; NaN patterns are skipped
+          top = std::max(top, magnitude);
+      }
+      const uint32_t wide = static_cast<uint32_t>(top) << 16U;
+      float amax;
+      std::memcpy(&amax, &wide, 4);
+      if (!(amax > 0.0F) || !std::isfinite(amax))
+        return format_error(p + ".projections.weight has no finite nonzero amax");
+      const float weight_scale = 448.0F / amax;
+      DeviceBuffer staging;
+      EVO_TRY(upload_view(&staging, *t, p + ".projections.weight"));
+      EVO_TRY(L.projection.allocate(t->elements(), "fp8 projection"));
+      EVO_TRY(e4m3_quantize_bf16(staging.as<uint16_t>(), t->elements(), weight_scale,
+                                 L.projection.as<uint8_t>(), nullptr));
+      EVO_TRY(hip_check(hipDeviceSynchronize(), "fp8 projection conversion"));
+      L.fp8 = true;
+      L.fp8_input_scale = 448.0F / kFp8InputAmax;
+      L.fp8_output_scale = 1.0F / (L.fp8_input_scale * weight_scale);
+    } else {
+      EVO_TRY(upload_view(&L.projection, *t, p + ".projections.weight"));
+    }
+    if (L.fp8 && t->dtype == DType::kE4M3) {
       // [input_scale, output_scale] (`src/cuda/model.cu:226-248`).
       const TensorView *s = nullptr;
       EVO_TRY(view(a, p + ".projections.fp8_runtime_scales", {2}, DType::kF32, &s));
@@ -246,9 +278,9 @@ Status Model::load(const Artifact &a, int device, bool allow_synthetic) {
         return format_error(p + " contains invalid software-FP8 runtime scales");
       L.fp8_input_scale = scales[0];
       L.fp8_output_scale = scales[1];
-      if (w % 32 != 0)
-        return {ErrorCode::kUnsupported, "unsupported: FP8 projections need width % 32 == 0"};
     }
+    if (L.fp8 && w % 32 != 0)
+      return {ErrorCode::kUnsupported, "unsupported: FP8 projections need width % 32 == 0"};
     EVO_TRY(view(a, p + ".out_filter_dense.weight", {w, w}, DType::kBF16, &t));
     EVO_TRY(upload_view(&L.out_weight, *t, p + ".out_filter_dense.weight"));
     EVO_TRY(view(a, p + ".out_filter_dense.bias", {w}, DType::kBF16, &t));
@@ -284,6 +316,8 @@ Status Model::load(const Artifact &a, int device, bool allow_synthetic) {
 Context::~Context() {
   if (host_logits_ != nullptr)
     (void)hipHostFree(host_logits_);
+  if (host_flag_ != nullptr)
+    (void)hipHostFree(host_flag_);
   if (stream_ != nullptr)
     (void)hipStreamDestroy(stream_);
 }
@@ -320,6 +354,10 @@ Status Context::initialize(std::shared_ptr<const Model> model, size_t capacity,
   EVO_TRY(gated_.allocate(R * c.inner * 4, "mlp gate"));
   EVO_TRY(logits_.allocate(R * c.vocab * 4, "logits"));
   EVO_TRY(codes_.allocate(R * w, "fp8 codes"));
+  EVO_TRY(flag_.allocate(sizeof(int), "token check flag"));
+  EVO_TRY(hip_check(hipMemsetAsync(flag_.as<void>(), 0, sizeof(int), stream_), "flag reset"));
+  EVO_TRY(hip_check(hipHostMalloc(reinterpret_cast<void **>(&host_flag_), sizeof(int),
+                                  hipHostMallocDefault), "pinned flag"));
   workspace_bytes_ = hyena_workspace_bytes(kHyenaHcl, R, w, c.state);
   EVO_TRY(workspace_.allocate(std::max<size_t>(workspace_bytes_, 256), "hyena workspace"));
   EVO_TRY(hip_check(hipHostMalloc(reinterpret_cast<void **>(&host_logits_),
@@ -423,45 +461,90 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
   return Status::Ok();
 }
 
-Status Context::forward(const uint32_t *tokens, size_t rows, bool initial,
-                        float *logits, size_t capture_layer, float *capture) {
+Status Context::enqueue(const uint32_t *device_tokens, size_t rows, bool initial,
+                        float *device_logits, size_t capture_layer, float *capture) {
   const ModelConfig &c = model_->config();
-  if (rows == 0 || rows > arena_rows_ || (logits == nullptr && capture == nullptr))
+  if (rows == 0 || rows > arena_rows_ || (device_logits == nullptr && capture == nullptr))
     return {ErrorCode::kInvalidArgument, "invalid_argument: forward arguments are invalid"};
   if (initial) {
+    if (rows > capacity_)
+      return {ErrorCode::kInvalidArgument, "invalid_argument: chunk exceeds capacity"};
     reset_caches();
   } else if (!valid_ || rows > capacity_ - position_) {
     return {ErrorCode::kInvalidArgument,
             "invalid_argument: continuation requires a valid prefill and free capacity"};
   }
-  if (initial && rows > capacity_)
-    return {ErrorCode::kInvalidArgument, "invalid_argument: chunk exceeds capacity"};
+  if (capture != nullptr && capture_layer >= c.layers)
+    return {ErrorCode::kInvalidArgument, "invalid_argument: embedding layer is invalid"};
+  // From here on the caches advance: the context stays invalid until the
+  // caller has synchronised and confirmed success (commit()).
+  valid_ = false;
+  EVO_TRY(embed_tokens(device_tokens, rows, model_->embedding.as<uint16_t>(), c.vocab,
+                       c.width, hidden_.as<float>(), flag_.as<int>(), stream_));
+  EVO_TRY(run_layers(rows, capture_layer, capture));
+  if (device_logits != nullptr) {
+    EVO_TRY(rms_norm(hidden_.as<float>(), rows, c.width, model_->final_norm.as<float>(),
+                     c.eps, normed_.as<float>(), stream_));
+    EVO_TRY(gemm_bf16w(normed_.as<float>(), model_->embedding.as<uint16_t>(), device_logits,
+                       rows, c.vocab, c.width, c.vocab, kGemmStore, nullptr, nullptr, false,
+                       0, options_.split_activations, stream_));
+  }
+  position_ = initial ? rows : position_ + rows;
+  return Status::Ok();
+}
+
+Status Context::finish() {
+  EVO_TRY(hip_check(hipMemcpyAsync(host_flag_, flag_.as<void>(), sizeof(int),
+                                   hipMemcpyDeviceToHost, stream_), "flag download"));
+  EVO_TRY(hip_check(hipStreamSynchronize(stream_), "prefill"));
+  if (*host_flag_ != 0)
+    return {ErrorCode::kInvalidArgument, "invalid_argument: token exceeds model vocabulary"};
+  valid_ = true;
+  return Status::Ok();
+}
+
+Status Context::forward(const uint32_t *tokens, size_t rows, bool initial,
+                        float *logits, size_t capture_layer, float *capture) {
+  const ModelConfig &c = model_->config();
+  if (tokens == nullptr || rows == 0 || rows > arena_rows_)
+    return {ErrorCode::kInvalidArgument, "invalid_argument: forward arguments are invalid"};
   for (size_t r = 0; r < rows; ++r)
     if (tokens[r] >= c.vocab)
       return {ErrorCode::kInvalidArgument, "invalid_argument: token exceeds model vocabulary"};
   EVO_TRY(hip_check(hipSetDevice(model_->device()), "select device"));
+  EVO_TRY(hip_check(hipMemsetAsync(flag_.as<void>(), 0, sizeof(int), stream_), "flag reset"));
   EVO_TRY(hip_check(hipMemcpyAsync(tokens_.as<void>(), tokens, rows * 4,
                                    hipMemcpyHostToDevice, stream_), "token upload"));
-  EVO_TRY(embed_tokens(tokens_.as<uint32_t>(), rows, model_->embedding.as<uint16_t>(),
-                       c.vocab, c.width, hidden_.as<float>(), stream_));
-  if (capture != nullptr && capture_layer >= c.layers)
-    return {ErrorCode::kInvalidArgument, "invalid_argument: embedding layer is invalid"};
-  EVO_TRY(run_layers(rows, capture_layer, capture));
-  if (logits != nullptr) {
-    EVO_TRY(rms_norm(hidden_.as<float>(), rows, c.width, model_->final_norm.as<float>(),
-                     c.eps, normed_.as<float>(), stream_));
-    EVO_TRY(gemm_bf16w(normed_.as<float>(), model_->embedding.as<uint16_t>(),
-                       logits_.as<float>(), rows, c.vocab, c.width, c.vocab, kGemmStore,
-                       nullptr, nullptr, false, 0, options_.split_activations, stream_));
+  EVO_TRY(enqueue(tokens_.as<uint32_t>(), rows, initial,
+                  logits != nullptr ? logits_.as<float>() : nullptr, capture_layer, capture));
+  if (logits != nullptr)
     EVO_TRY(hip_check(hipMemcpyAsync(host_logits_, logits_.as<void>(), rows * c.vocab * 4,
                                      hipMemcpyDeviceToHost, stream_), "logits download"));
-  }
-  EVO_TRY(hip_check(hipStreamSynchronize(stream_), "prefill"));
+  EVO_TRY(finish());
   if (logits != nullptr)
     std::memcpy(logits, host_logits_, rows * c.vocab * 4);
-  position_ = initial ? rows : position_ + rows;
-  valid_ = true;
   return Status::Ok();
+}
+
+Status Context::prefill_resident(const uint32_t *device_tokens, size_t count,
+                                 float *device_logits) {
+  const ModelConfig &c = model_->config();
+  if (device_tokens == nullptr || device_logits == nullptr || count == 0)
+    return {ErrorCode::kInvalidArgument, "invalid_argument: resident prefill arguments"};
+  if (count > capacity_)
+    return {ErrorCode::kInvalidArgument,
+            "invalid_argument: sequence exceeds context capacity"};
+  EVO_TRY(hip_check(hipSetDevice(model_->device()), "select device"));
+  EVO_TRY(hip_check(hipMemsetAsync(flag_.as<void>(), 0, sizeof(int), stream_), "flag reset"));
+  for (size_t offset = 0; offset < count; offset += arena_rows_) {
+    const size_t rows = std::min(arena_rows_, count - offset);
+    EVO_TRY(enqueue(device_tokens + offset, rows, offset == 0,
+                    device_logits + offset * c.vocab, std::numeric_limits<size_t>::max(),
+                    nullptr));
+    if (offset + rows < count)
+      valid_ = true;  // later chunks of this call continue from it
+  }
+  return finish();
 }
 
 }  // namespace evo::hip

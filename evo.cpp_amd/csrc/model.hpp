@@ -83,7 +83,10 @@ struct ModelConfig {
 
 class Model {
 public:
-  Status load(const Artifact &artifact, int device, bool allow_synthetic);
+  // fp8_projections converts BF16 Hyena input projections to software E4M3
+  // at load (artifacts that already store F8_E4M3 keep their own scales).
+  Status load(const Artifact &artifact, int device, bool allow_synthetic,
+              bool fp8_projections);
   const ModelConfig &config() const { return config_; }
   int device() const { return device_; }
 
@@ -112,6 +115,11 @@ public:
   // state after block capture_layer) receive the outputs.
   Status forward(const uint32_t *tokens, size_t rows, bool initial,
                  float *logits, size_t capture_layer, float *capture);
+  // Whole-sequence prefill with tokens and logits ([count, vocab] F32) in
+  // device memory: chunks are enqueued back to back on the context stream,
+  // one synchronisation at the end, no host transfer of activations.
+  Status prefill_resident(const uint32_t *device_tokens, size_t count,
+                          float *device_logits);
   size_t position() const { return position_; }
   size_t activation_capacity() const { return arena_rows_; }
   size_t capacity() const { return capacity_; }
@@ -120,6 +128,9 @@ public:
   hipStream_t stream() const { return stream_; }
 
 private:
+  Status enqueue(const uint32_t *device_tokens, size_t rows, bool initial,
+                 float *device_logits, size_t capture_layer, float *capture);
+  Status finish();
   Status run_layers(size_t rows, size_t capture_layer, float *capture);
   void reset_caches();
 
@@ -130,13 +141,14 @@ private:
   size_t capacity_{0}, arena_rows_{0}, position_{0};
   bool valid_{false};
   DeviceBuffer tokens_, hidden_, residual_, normed_, projected_, mixed_, query_,
-      gated_, logits_, codes_, workspace_;
+      gated_, logits_, codes_, workspace_, flag_;
   size_t workspace_bytes_{0};
   struct Cache {
     DeviceBuffer short_history, inner_history, modal_state, keys, values;
   };
   std::vector<Cache> cache_;
   float *host_logits_{nullptr};
+  int *host_flag_{nullptr};
 };
 
 }  // namespace evo::hip

@@ -46,7 +46,8 @@ Status fp8_linear(const uint8_t *in_codes, const uint8_t *w_codes, float *out,
 
 // ---- Elementwise / normalisation (elementwise.hip).
 Status embed_tokens(const uint32_t *tokens, size_t rows, const uint16_t *table,
-                    size_t vocab, size_t width, float *out, hipStream_t stream);
+                    size_t vocab, size_t width, float *out, int *invalid,
+                    hipStream_t stream);
 Status rms_norm(const float *x, size_t rows, size_t width, const float *scale,
                 float eps, float *out, hipStream_t stream);
 // Copies the last `history` rows of the sequence [old_history ; x] into

@@ -158,8 +158,8 @@ class TensorSpec:
 
 @dataclass
 class Artifact:
-    """A seeded artifact description. Tensors are produced in declaration
-    order from one PCG64 stream, so the bytes depend only on (shape, seed,
+    """A seeded artifact description. Tensor i is drawn from its own PCG64
+    stream seeded with (seed, i), so the bytes depend only on (shape, seed,
     init, fp8 layers); ``write`` streams them to disk one tensor at a time."""
 
     shape: ModelShape
@@ -170,13 +170,30 @@ class Artifact:
             make: Callable[[np.random.Generator], np.ndarray]) -> None:
         self.specs.append(TensorSpec(name, dtype, [int(d) for d in shape], make))
 
-    def _stream(self):
-        rng = np.random.Generator(np.random.PCG64(self.seed))
-        for spec in self.specs:
-            array = np.ascontiguousarray(spec.make(rng))
-            if list(array.shape) != spec.shape or array.nbytes != spec.nbytes:
-                raise AssertionError(f"generator mismatch for {spec.name}")
-            yield spec, array
+    def _make(self, index: int) -> np.ndarray:
+        spec = self.specs[index]
+        rng = np.random.Generator(np.random.PCG64(
+            np.random.SeedSequence([self.seed, index])))
+        array = np.ascontiguousarray(spec.make(rng))
+        if list(array.shape) != spec.shape or array.nbytes != spec.nbytes:
+            raise AssertionError(f"generator mismatch for {spec.name}")
+        return array
+
+    def _stream(self, workers: int = 8):
+        """Yield (spec, array) in order; tensors are generated ahead on a
+        thread pool (each has its own PCG64 stream, so order and thread count
+        do not change the bytes)."""
+        from concurrent.futures import ThreadPoolExecutor
+        with ThreadPoolExecutor(max_workers=workers) as pool:
+            pending = {}
+            for index in range(min(workers, len(self.specs))):
+                pending[index] = pool.submit(self._make, index)
+            for index, spec in enumerate(self.specs):
+                array = pending.pop(index).result()
+                ahead = index + workers
+                if ahead < len(self.specs):
+                    pending[ahead] = pool.submit(self._make, ahead)
+                yield spec, array
 
     def tensors(self) -> Dict[str, np.ndarray]:
         """Materialise every tensor (small models only)."""
@@ -280,20 +297,26 @@ def random_artifact(shape: ModelShape, seed: int = 0, init: str = "unit",
                     lambda rng: inv_freq.copy())
         else:
             if index in fp8:
-                state = {}
+                # the codes and their scale tensor are derived from the same
+                # weight draw (seeded by the codes tensor's position)
                 weight_maker = normal((3 * w, w), 1.0 / math.sqrt(w) if unit else 0.02)
+                position = len(art.specs)
 
-                def codes(rng, weight_maker=weight_maker, state=state):
-                    weight = weight_maker(rng)
-                    weight_scale = np.float32(448.0) / np.float32(np.abs(weight).max())
-                    state["weight_scale"] = weight_scale
+                def weight_and_scale(art=art, position=position, maker=weight_maker):
+                    rng = np.random.Generator(np.random.PCG64(
+                        np.random.SeedSequence([art.seed, position])))
+                    weight = maker(rng)
+                    return weight, np.float32(448.0) / np.float32(np.abs(weight).max())
+
+                def codes(rng, draw=weight_and_scale):
+                    weight, weight_scale = draw()
                     return e4m3_encode(weight * weight_scale)
 
-                def scales(rng, state=state):
+                def scales(rng, draw=weight_and_scale):
+                    _, weight_scale = draw()
                     input_scale = np.float32(448.0) / np.float32(fp8_input_amax)
                     return np.array([input_scale, np.float32(1.0) /
-                                     (input_scale * state["weight_scale"])],
-                                    dtype=np.float32)
+                                     (input_scale * weight_scale)], dtype=np.float32)
 
                 art.add(p + ".projections.weight", "F8_E4M3", (3 * w, w), codes)
                 art.add(p + ".projections.fp8_runtime_scales", "F32", (2,), scales)

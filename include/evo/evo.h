@@ -63,7 +63,11 @@ typedef enum evo_backend {
 
 enum {
   /* Reference: include/evo/evo.h:52-56. */
-  EVO_MODEL_FLAG_TEST_ONLY_ALLOW_SYNTHETIC = 1u << 0u
+  EVO_MODEL_FLAG_TEST_ONLY_ALLOW_SYNTHETIC = 1u << 0u,
+  /* HIP: convert BF16 Hyena input projections to software E4M3 at load with
+   * the converter's per-tensor amax rule (weight scale 448/amax(W), fixed
+   * activation scale 448/8). Artifacts storing F8_E4M3 keep their scales. */
+  EVO_MODEL_FLAG_HIP_FP8_PROJECTIONS = 1u << 8u
 };
 
 enum {

@@ -25,6 +25,20 @@
 extern "C" {
 #endif
 
+/* Whole-sequence prefill with tokens (uint32 [count]) and logits (F32
+ * [count, vocab]) in device memory, for callers that keep the stream on the
+ * GPU (serving loops, benchmarks): same chunk loop, caches and numerics as
+ * evo_context_prefill, but no host copies; synchronises the context stream
+ * once at the end. The context is reset first (position 0), so one context can
+ * serve successive sequences. Token ids >= vocab fail the call.
+ * Replaces the CUDA `PipelineModel::prefill` loop driven from
+ * `src/c_api.cpp:962-989`, minus the host logits. */
+EVO_API evo_status evo_hip_context_prefill_resident(evo_context *context,
+                                                    const uint32_t *tokens,
+                                                    size_t count, float *logits);
+/* The context's HIP stream (hipStream_t), for ordering caller work. */
+EVO_API void *evo_hip_context_stream(const evo_context *context);
+
 /* Storage type of activation tensors passed to the Hyena operator. */
 typedef enum evo_hip_dtype { EVO_HIP_F32 = 0, EVO_HIP_BF16 = 1 } evo_hip_dtype;
 typedef enum evo_hip_hyena_kind {
