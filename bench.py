@@ -80,15 +80,19 @@ def kernel_rooflines(split):
     # dominant kernel: gated MLP l1/l2 GEMM of one block at L=8192
     m, n, k = 8192, 2 * 11264, 4096
     x = torch.randn(m, k, device="cuda", generator=g)
+    planes = torch.empty(2, m, k, dtype=torch.int16, device="cuda")
+    native.call("evo_hip_split_f32", x.data_ptr(), m * k, planes[0].data_ptr(),
+                planes[1].data_ptr(), stream)
     w = (torch.randn(n, k, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
     y = torch.empty(m, n, device="cuda")
-    ms = event_time(lambda: native.call("evo_hip_linear", x.data_ptr(), w.data_ptr(), None,
-                                        None, m, n, k, 1 if split else 0, y.data_ptr(),
+    lo = planes[1].data_ptr() if split else None
+    ms = event_time(lambda: native.call("evo_hip_linear", planes[0].data_ptr(), lo,
+                                        w.data_ptr(), None, None, m, n, k, y.data_ptr(),
                                         stream), 5)
     flops = 2.0 * m * n * k
-    out["gemm"] = dict(kernel="gemm_bf16w_kernel<%s>" % ("true" if split else "false"),
+    out["gemm"] = dict(kernel="gemm_kernel<%s>" % ("true" if split else "false"),
                        ms=ms, flops=flops, tflops=flops / ms / 1e9)
-    del x, w, y
+    del x, w, y, planes
     # config 2: fused Hyena HCL operator, BF16 [8192, 12288] in, [8192, 4096] out
     length, width, state = 8192, 4096, 16
     proj = torch.randn(length, 3 * width, device="cuda", generator=g).to(torch.bfloat16)

@@ -57,11 +57,11 @@ __global__ void qkv_rope_kernel(const float *__restrict__ projected, size_t rows
   }
 }
 
-template <int kDim>  // head_dim
+template <int kDim, typename O>  // head_dim, output type
 __global__ __launch_bounds__(256) void attention_kernel(
     const float *__restrict__ q, const float *__restrict__ k_cache,
     const float *__restrict__ v_cache, size_t rows, size_t prefix,
-    size_t heads, float *__restrict__ out) {
+    size_t heads, O out) {
   constexpr int kQ = 64, kKeys = 64, kPart = kDim / 4;
   __shared__ float k_s[kKeys * kDim];
   __shared__ float v_s[kKeys * kDim];
@@ -130,7 +130,7 @@ __global__ __launch_bounds__(256) void attention_kernel(
   if (active) {
 #pragma unroll
     for (int d = 0; d < kPart; ++d)
-      out[row * width + head * kDim + part * kPart + d] = acc[d] / denominator;
+      put(out, row * width + head * kDim + part * kPart + d, acc[d] / denominator);
   }
 }
 
@@ -152,29 +152,26 @@ Status qkv_rope(const float *projected, size_t rows, size_t width, size_t heads,
   return launch_status("qkv_rope_kernel");
 }
 
-Status causal_attention(const float *q, const float *k_cache,
-                        const float *v_cache, size_t rows, size_t prefix,
-                        size_t heads, size_t head_dim, float *out,
+template <typename O>
+Status launch_attention(const float *q, const float *k_cache, const float *v_cache,
+                        size_t rows, size_t prefix, size_t heads, size_t head_dim, O out,
                         hipStream_t stream) {
-  if (q == nullptr || k_cache == nullptr || v_cache == nullptr ||
-      out == nullptr || rows == 0 || heads == 0 || heads > 65535)
-    return {ErrorCode::kInvalidArgument, "causal_attention: invalid arguments"};
   const dim3 grid(ceil_div(rows, 64), static_cast<unsigned>(heads));
   switch (head_dim) {
   case 16:
-    hipLaunchKernelGGL(attention_kernel<16>, grid, dim3(256), 0, stream, q, k_cache,
+    hipLaunchKernelGGL((attention_kernel<16, O>), grid, dim3(256), 0, stream, q, k_cache,
                        v_cache, rows, prefix, heads, out);
     break;
   case 32:
-    hipLaunchKernelGGL(attention_kernel<32>, grid, dim3(256), 0, stream, q, k_cache,
+    hipLaunchKernelGGL((attention_kernel<32, O>), grid, dim3(256), 0, stream, q, k_cache,
                        v_cache, rows, prefix, heads, out);
     break;
   case 64:
-    hipLaunchKernelGGL(attention_kernel<64>, grid, dim3(256), 0, stream, q, k_cache,
+    hipLaunchKernelGGL((attention_kernel<64, O>), grid, dim3(256), 0, stream, q, k_cache,
                        v_cache, rows, prefix, heads, out);
     break;
   case 128:
-    hipLaunchKernelGGL(attention_kernel<128>, grid, dim3(256), 0, stream, q, k_cache,
+    hipLaunchKernelGGL((attention_kernel<128, O>), grid, dim3(256), 0, stream, q, k_cache,
                        v_cache, rows, prefix, heads, out);
     break;
   default:
@@ -182,6 +179,21 @@ Status causal_attention(const float *q, const float *k_cache,
             "causal_attention: head_dim must be 16, 32, 64 or 128"};
   }
   return launch_status("attention_kernel");
+}
+
+Status causal_attention(const float *q, const float *k_cache,
+                        const float *v_cache, size_t rows, size_t prefix,
+                        size_t heads, size_t head_dim, float *out_f32,
+                        uint16_t *out_hi, uint16_t *out_lo, hipStream_t stream) {
+  if (q == nullptr || k_cache == nullptr || v_cache == nullptr ||
+      (out_f32 == nullptr && out_hi == nullptr) || rows == 0 || heads == 0 ||
+      heads > 65535)
+    return {ErrorCode::kInvalidArgument, "causal_attention: invalid arguments"};
+  if (out_f32 != nullptr)
+    return launch_attention(q, k_cache, v_cache, rows, prefix, heads, head_dim, out_f32,
+                            stream);
+  return launch_attention(q, k_cache, v_cache, rows, prefix, heads, head_dim,
+                          SplitOut{out_hi, out_lo}, stream);
 }
 
 }  // namespace evo::hip

@@ -569,15 +569,22 @@ evo_status evo_hip_hyena_forward(evo_hip_hyena_kind kind, evo_hip_dtype dtype,
                              direct, poles, residues, state_size};
     const auto s = static_cast<hipStream_t>(stream);
     if (dtype == EVO_HIP_F32)
-      return publish(evo::hip::hyena_forward<float>(
+      return publish(evo::hip::hyena_forward<float, float *>(
           kind, static_cast<const float *>(projection), length, width, w, short_history,
           inner_history, modal_state, workspace, workspace_bytes,
           static_cast<float *>(output), s));
     if (dtype == EVO_HIP_BF16)
-      return publish(evo::hip::hyena_forward<uint16_t>(
+      return publish(evo::hip::hyena_forward<uint16_t, uint16_t *>(
           kind, static_cast<const uint16_t *>(projection), length, width, w, short_history,
           inner_history, modal_state, workspace, workspace_bytes,
           static_cast<uint16_t *>(output), s));
+    if (dtype == EVO_HIP_SPLIT) {
+      auto *hi = static_cast<uint16_t *>(output);
+      return publish(evo::hip::hyena_forward<float, evo::hip::SplitOut>(
+          kind, static_cast<const float *>(projection), length, width, w, short_history,
+          inner_history, modal_state, workspace, workspace_bytes,
+          evo::hip::SplitOut{hi, hi == nullptr ? nullptr : hi + length * width}, s));
+    }
     return publish(EVO_STATUS_INVALID_ARGUMENT, "invalid_argument: unknown dtype");
   });
 }
@@ -608,15 +615,24 @@ evo_status evo_hip_fp8_linear(const uint8_t *in_codes, const uint8_t *w_codes, f
   });
 }
 
-evo_status evo_hip_linear(const float *x, const uint16_t *w, const uint16_t *bias,
-                          const float *residual, size_t m, size_t n, size_t k, int split,
-                          float *out, void *stream) {
+evo_status evo_hip_split_f32(const float *x, size_t count, uint16_t *hi, uint16_t *lo,
+                            void *stream) {
+  return protect([&]() -> evo_status {
+    return publish(evo::hip::split_planes(x, count, hi, lo, static_cast<hipStream_t>(stream)));
+  });
+}
+
+evo_status evo_hip_linear(const uint16_t *x_hi, const uint16_t *x_lo, const uint16_t *w,
+                          const uint16_t *bias, const float *residual, size_t m, size_t n,
+                          size_t k, float *out, void *stream) {
   return protect([&]() -> evo_status {
     const evo::hip::GemmEpilogue mode =
         bias != nullptr ? (residual != nullptr ? evo::hip::kGemmBiasResidual : evo::hip::kGemmBias)
                         : (residual != nullptr ? evo::hip::kGemmResidual : evo::hip::kGemmStore);
-    return publish(evo::hip::gemm_bf16w(x, w, out, m, n, k, n, mode, bias, residual, false, 0,
-                                        split != 0, static_cast<hipStream_t>(stream)));
+    return publish(evo::hip::gemm_bf16w(evo::hip::Activation{x_hi, x_lo, k}, w,
+                                        evo::hip::GemmOutput{out, nullptr, nullptr, n}, m, n,
+                                        k, mode, bias, residual, false, 0,
+                                        static_cast<hipStream_t>(stream)));
   });
 }
 
@@ -643,29 +659,35 @@ evo_status evo_hip_pack_mlp(const uint16_t *l1, const uint16_t *l2, size_t inner
   });
 }
 
-evo_status evo_hip_gated_mlp(const float *x, const uint16_t *w12, const uint16_t *l3,
-                             size_t m, size_t width, size_t inner, int gelu, int split,
-                             float *inner_workspace, const float *residual, float *out,
+evo_status evo_hip_gated_mlp(const uint16_t *x_hi, const uint16_t *x_lo, const uint16_t *w12,
+                             const uint16_t *l3, size_t m, size_t width, size_t inner, int gelu,
+                             uint16_t *inner_workspace, const float *residual, float *out,
                              void *stream) {
   return protect([&]() -> evo_status {
+    if (inner_workspace == nullptr)
+      return publish(EVO_STATUS_INVALID_ARGUMENT, "invalid_argument: MLP workspace is null");
     const size_t padded = (inner + 31) / 32 * 32;
     const auto s = static_cast<hipStream_t>(stream);
-    auto status = evo::hip::gemm_bf16w(x, w12, inner_workspace, m, 2 * padded, width, inner,
-                                       evo::hip::kGemmGated, nullptr, nullptr, gelu != 0,
-                                       inner, split != 0, s);
+    uint16_t *inner_lo = x_lo != nullptr ? inner_workspace + m * inner : nullptr;
+    auto status = evo::hip::gemm_bf16w(
+        evo::hip::Activation{x_hi, x_lo, width}, w12,
+        evo::hip::GemmOutput{nullptr, inner_workspace, inner_lo, inner}, m, 2 * padded, width,
+        evo::hip::kGemmGated, nullptr, nullptr, gelu != 0, inner, s);
     if (!status.ok())
       return publish(status);
     return publish(evo::hip::gemm_bf16w(
-        inner_workspace, l3, out, m, width, inner, width,
+        evo::hip::Activation{inner_workspace, inner_lo, inner}, l3,
+        evo::hip::GemmOutput{out, nullptr, nullptr, width}, m, width, inner,
         residual != nullptr ? evo::hip::kGemmResidual : evo::hip::kGemmStore, nullptr,
-        residual, false, 0, split != 0, s));
+        residual, false, 0, s));
   });
 }
 
 evo_status evo_hip_rms_norm(const float *x, size_t rows, size_t width, const float *scale,
-                            float eps, float *out, void *stream) {
+                            float eps, float *out, uint16_t *out_hi, uint16_t *out_lo,
+                            void *stream) {
   return protect([&]() -> evo_status {
-    return publish(evo::hip::rms_norm(x, rows, width, scale, eps, out,
+    return publish(evo::hip::rms_norm(x, rows, width, scale, eps, out, out_hi, out_lo,
                                       static_cast<hipStream_t>(stream)));
   });
 }
@@ -682,7 +704,8 @@ evo_status evo_hip_attention(const float *projected, size_t rows, size_t width, 
     if (!status.ok())
       return publish(status);
     return publish(evo::hip::causal_attention(query, key_cache, value_cache, rows, prefix,
-                                              heads, heads == 0 ? 0 : width / heads, out, s));
+                                              heads, heads == 0 ? 0 : width / heads, out,
+                                              nullptr, nullptr, s));
   });
 }
 

@@ -8,6 +8,7 @@
 #include <cstdint>
 #include <string>
 
+#include "ops.hpp"
 #include "status.hpp"
 
 namespace evo::hip {
@@ -44,13 +45,14 @@ template <>
 __device__ inline float load_act<uint16_t>(const uint16_t *p, size_t i) {
   return bf16_to_f32(p[i]);
 }
-template <typename T> __device__ inline void store_act(T *p, size_t i, float v);
-template <> __device__ inline void store_act<float>(float *p, size_t i, float v) {
-  p[i] = v;
-}
-template <>
-__device__ inline void store_act<uint16_t>(uint16_t *p, size_t i, float v) {
-  p[i] = f32_to_bf16(v);
+// Stores of producer kernels (SplitOut is declared in ops.hpp).
+__device__ inline void put(float *out, size_t i, float v) { out[i] = v; }
+__device__ inline void put(uint16_t *out, size_t i, float v) { out[i] = f32_to_bf16(v); }
+__device__ inline void put(const SplitOut &out, size_t i, float v) {
+  const uint16_t hi = f32_to_bf16(v);
+  out.hi[i] = hi;
+  if (out.lo != nullptr)
+    out.lo[i] = f32_to_bf16(v - bf16_to_f32(hi));
 }
 
 inline Status hip_status(const hipError_t error, const char *what) {

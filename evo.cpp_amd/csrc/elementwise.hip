@@ -40,11 +40,11 @@ __device__ inline float wave_sum(float v) {
 
 __global__ __launch_bounds__(256) void rms_norm_kernel(
     const float *__restrict__ x, size_t width, const float *__restrict__ scale,
-    float eps, float *__restrict__ out) {
+    float eps, float *__restrict__ out, uint16_t *__restrict__ out_hi,
+    uint16_t *__restrict__ out_lo) {
   __shared__ float partial[4];
   const size_t row = blockIdx.x;
   const float *src = x + row * width;
-  float *dst = out + row * width;
   float sum = 0.0F;
   const bool vec = (width % 4) == 0;
   if (vec) {
@@ -62,17 +62,14 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(
   __syncthreads();
   const float total = partial[0] + partial[1] + partial[2] + partial[3];
   const float denominator = sqrtf(total / static_cast<float>(width)) + eps;
-  if (vec) {
-    for (size_t c = threadIdx.x * 4; c < width; c += 256 * 4) {
-      const float4 v = *reinterpret_cast<const float4 *>(src + c);
-      const float4 s = *reinterpret_cast<const float4 *>(scale + c);
-      *reinterpret_cast<float4 *>(dst + c) =
-          make_float4(v.x / denominator * s.x, v.y / denominator * s.y,
-                      v.z / denominator * s.z, v.w / denominator * s.w);
-    }
-  } else {
-    for (size_t c = threadIdx.x; c < width; c += 256)
-      dst[c] = src[c] / denominator * scale[c];
+  const SplitOut planes{out_hi, out_lo};
+  for (size_t c = threadIdx.x; c < width; c += 256) {
+    const float value = src[c] / denominator * scale[c];
+    const size_t index = row * width + c;
+    if (out != nullptr)
+      out[index] = value;
+    if (out_hi != nullptr)
+      put(planes, index, value);
   }
 }
 
@@ -109,12 +106,13 @@ Status embed_tokens(const uint32_t *tokens, size_t rows, const uint16_t *table,
 }
 
 Status rms_norm(const float *x, size_t rows, size_t width, const float *scale,
-                float eps, float *out, hipStream_t stream) {
-  if (x == nullptr || scale == nullptr || out == nullptr || rows == 0 ||
-      width == 0 || rows > (1U << 31))
+                float eps, float *out, uint16_t *out_hi, uint16_t *out_lo,
+                hipStream_t stream) {
+  if (x == nullptr || scale == nullptr || (out == nullptr && out_hi == nullptr) ||
+      rows == 0 || width == 0 || rows > (1U << 31))
     return {ErrorCode::kInvalidArgument, "rms_norm: invalid arguments"};
   hipLaunchKernelGGL(rms_norm_kernel, dim3(static_cast<unsigned>(rows)), dim3(256),
-                     0, stream, x, width, scale, eps, out);
+                     0, stream, x, width, scale, eps, out, out_hi, out_lo);
   return launch_status("rms_norm_kernel");
 }
 

@@ -3,164 +3,170 @@
 //
 //   C[M,N] = A[M,K] . W[N,K]^T  (+ fused epilogue)
 //
-// A is the F32 activation (row-major), W the BF16 weight in nn.Linear layout
-// ([out, in], K contiguous), accumulation F32. Reference semantics: the
-// F32-activation x BF16-weight dot of evo.cpp `src/cpu/model.cpp:284-314`.
+// W is the BF16 weight in nn.Linear layout ([out, in], K contiguous); the
+// accumulation is F32. Reference semantics: the F32-activation x BF16-weight
+// dot of evo.cpp `src/cpu/model.cpp:284-314`.
 //
-// Precision: in the "split" variant each F32 activation is written as
-// hi + lo with hi = bf16(a) and lo = bf16(a - hi); both halves are multiplied
-// by the (exactly BF16) weight on MFMA, so the product carries ~16 significant
-// bits of the activation (relative error ~2^-17) for twice the MFMA work. The
-// "bf16" variant keeps only hi (one MFMA pass).
+// Activations arrive as split BF16 planes written by the producing kernel:
+// hi = bf16(a) and lo = bf16(a - hi). With lo present ("split", profile
+// hip-f32) both planes are multiplied by the exactly-BF16 weight, so each
+// product carries ~16 significant bits of the activation (relative error
+// ~2^-17) for twice the MFMA work; without lo (profile hip-bf16) one pass.
 //
-// Tiling for CDNA4: 256 threads = 4 waves; block tile 128x128, K step 32;
-// each wave owns a 64x64 sub-tile = 2x2 MFMA 32x32x16 tiles (64 F32
-// accumulators per lane). Global loads are 16-byte vectors, staged through
-// LDS rows padded to 40 BF16 (80 B) so the 16-byte per-lane fragment reads of
-// 32 consecutive rows spread over the banks. The next K tile is fetched into
-// registers while the current one is multiplied.
+// Tiling for CDNA4: 512 threads = 8 waves as 4 (M) x 2 (N); block tile
+// 256 x 256, K step 32; each wave owns 64 x 128 = 2 x 4 MFMA 32x32x16 tiles
+// (128 F32 accumulators per lane). Operands are staged through LDS with
+// 16-byte loads into rows padded to 40 BF16 (80 B), double-buffered so one
+// barrier per K step separates the prefetch of step k+1 from the MFMAs of k.
+// Tiles are renumbered so that each of the 8 XCDs (own L2) receives a
+// contiguous band of the tile grid, walked in groups of 8 tile-rows.
 #include "common.hpp"
 #include "ops.hpp"
 
 namespace evo::hip {
 namespace {
 
-constexpr int kBM = 128;
-constexpr int kBN = 128;
+constexpr int kBM = 256;
+constexpr int kBN = 256;
 constexpr int kBK = 32;
-constexpr int kLdsStride = kBK + 8;  // BF16 elements per LDS row
+constexpr int kThreads = 512;
+constexpr int kStride = kBK + 8;  // BF16 per LDS row
+constexpr int kXcds = 8;
+constexpr int kGroupM = 8;
 
 struct Epilogue {
   int mode;              // GemmEpilogue
-  const uint16_t *bias;  // BF16 [N] (bias modes)
-  const float *residual; // F32 [M, ldc] (residual modes)
-  int gelu;              // gated mode: 1 = erf-GELU on the l1 half
-  int gated_width;       // gated mode: number of valid output columns
+  const uint16_t *bias;  // BF16 [N]
+  const float *residual; // F32 [M, ldc]
+  int gelu;              // gated: erf-GELU on the l1 half
+  int gated_width;       // gated: valid output columns
 };
 
 __device__ inline float gelu_erf(const float x) {
   return 0.5F * x * (1.0F + erff(x * 0.7071067811865475244F));
 }
 
+// Maps the hardware block id to a (tile_m, tile_n) pair: consecutive ids go
+// to different XCDs, so id -> (xcd, slot) -> contiguous band per XCD.
+// XCD x receives total/8 tiles (+1 for the first total%8 XCDs), so the map
+// from hardware id to linear tile is a bijection for every grid size.
+__device__ inline void tile_of(int id, int tiles_m, int tiles_n, int *tm, int *tn) {
+  const int total = tiles_m * tiles_n;
+  const int q = total / kXcds, r = total % kXcds;
+  const int xcd = id % kXcds;
+  const int linear = xcd * q + min(xcd, r) + id / kXcds;
+  const int group_size = kGroupM * tiles_n;
+  const int group = linear / group_size;
+  const int first_m = group * kGroupM;
+  const int rows = min(tiles_m - first_m, kGroupM);
+  const int in_group = linear % group_size;
+  *tm = first_m + in_group % rows;
+  *tn = in_group / rows;
+}
+
 template <bool kSplit>
-__global__ __launch_bounds__(256) void gemm_bf16w_kernel(
-    const float *__restrict__ A, const uint16_t *__restrict__ W,
-    float *__restrict__ C, const int M, const int N, const int K,
-    const int ldc, const Epilogue epi) {
-  __shared__ __attribute__((aligned(16))) uint16_t a_hi[kBM * kLdsStride];
-  __shared__ __attribute__((aligned(16))) uint16_t a_lo[kSplit ? kBM * kLdsStride : 8];
-  __shared__ __attribute__((aligned(16))) uint16_t w_s[kBN * kLdsStride];
+__global__ __launch_bounds__(kThreads) void gemm_kernel(
+    const uint16_t *__restrict__ a_hi, const uint16_t *__restrict__ a_lo, int lda,
+    const uint16_t *__restrict__ W, int M, int N, int K, float *__restrict__ C,
+    uint16_t *__restrict__ c_hi, uint16_t *__restrict__ c_lo, int ldc,
+    const Epilogue epi) {
+  constexpr int kPlaneA = kBM * kStride;
+  constexpr int kStage = (kSplit ? 2 : 1) * kPlaneA + kBN * kStride;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * kStage];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wave_m = wave >> 1;
-  const int wave_n = wave & 1;
-  const int block_m = blockIdx.y * kBM;
-  const int block_n = blockIdx.x * kBN;
+  const int wave_m = wave >> 1;  // 0..3
+  const int wave_n = wave & 1;   // 0..1
+  const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
+  int tm, tn;
+  tile_of(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
+  const int block_m = tm * kBM, block_n = tn * kBN;
 
-  // Loader mapping: thread -> (row, 16-element K segment).
-  const int load_row = tid >> 1;
-  const int load_k = (tid & 1) * 16;
-  const int a_row = block_m + load_row;
-  const int w_row = block_n + load_row;
+  // Loader: each operand tile is 256 rows x 32 BF16 = 1024 x 16 B; thread t
+  // moves chunks t and t + 512: row = c / 4, 8-element segment = c % 4.
+  uint4 ra_hi[2], ra_lo[2], rw[2];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      const int c = tid + v * kThreads;
+      const int r = c >> 2, k = k0 + (c & 3) * 8;
+      const bool ka = k < K;
+      const int ar = block_m + r, wr = block_n + r;
+      const size_t a_off = static_cast<size_t>(ar) * lda + k;
+      ra_hi[v] = (ar < M && ka) ? *reinterpret_cast<const uint4 *>(a_hi + a_off) : make_uint4(0, 0, 0, 0);
+      if (kSplit)
+        ra_lo[v] = (ar < M && ka) ? *reinterpret_cast<const uint4 *>(a_lo + a_off) : make_uint4(0, 0, 0, 0);
+      rw[v] = (wr < N && ka) ? *reinterpret_cast<const uint4 *>(W + static_cast<size_t>(wr) * K + k)
+                             : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto stash = [&](int buffer) {
+    uint16_t *stage = lds + buffer * kStage;
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      const int c = tid + v * kThreads;
+      const int r = c >> 2, seg = (c & 3) * 8;
+      *reinterpret_cast<uint4 *>(stage + r * kStride + seg) = ra_hi[v];
+      if (kSplit)
+        *reinterpret_cast<uint4 *>(stage + kPlaneA + r * kStride + seg) = ra_lo[v];
+      *reinterpret_cast<uint4 *>(stage + (kSplit ? 2 : 1) * kPlaneA + r * kStride + seg) = rw[v];
+    }
+  };
 
-  f32x16 acc[2][2];
+  f32x16 acc[2][4];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e)
         acc[i][j][e] = 0.0F;
 
-  float a_reg[16];
-  uint4 w_reg[2];
-
-  auto fetch = [&](const int k0) {
-    const int k = k0 + load_k;
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      float4 value = make_float4(0.F, 0.F, 0.F, 0.F);
-      if (a_row < M && k + v * 4 < K)
-        value = *reinterpret_cast<const float4 *>(A + static_cast<size_t>(a_row) * K + k + v * 4);
-      a_reg[v * 4 + 0] = value.x;
-      a_reg[v * 4 + 1] = value.y;
-      a_reg[v * 4 + 2] = value.z;
-      a_reg[v * 4 + 3] = value.w;
-    }
-#pragma unroll
-    for (int v = 0; v < 2; ++v) {
-      uint4 value = make_uint4(0U, 0U, 0U, 0U);
-      if (w_row < N && k + v * 8 < K)
-        value = *reinterpret_cast<const uint4 *>(W + static_cast<size_t>(w_row) * K + k + v * 8);
-      w_reg[v] = value;
-    }
-  };
-
-  auto stash = [&]() {
-    uint32_t hi[8], lo[8];
-#pragma unroll
-    for (int p = 0; p < 8; ++p) {
-      const float x0 = a_reg[2 * p], x1 = a_reg[2 * p + 1];
-      const uint16_t h0 = f32_to_bf16(x0), h1 = f32_to_bf16(x1);
-      hi[p] = static_cast<uint32_t>(h0) | (static_cast<uint32_t>(h1) << 16U);
-      if (kSplit) {
-        const uint16_t l0 = f32_to_bf16(x0 - bf16_to_f32(h0));
-        const uint16_t l1 = f32_to_bf16(x1 - bf16_to_f32(h1));
-        lo[p] = static_cast<uint32_t>(l0) | (static_cast<uint32_t>(l1) << 16U);
-      }
-    }
-    uint4 *dst_hi = reinterpret_cast<uint4 *>(a_hi + load_row * kLdsStride + load_k);
-    dst_hi[0] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-    dst_hi[1] = make_uint4(hi[4], hi[5], hi[6], hi[7]);
-    if (kSplit) {
-      uint4 *dst_lo = reinterpret_cast<uint4 *>(a_lo + load_row * kLdsStride + load_k);
-      dst_lo[0] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-      dst_lo[1] = make_uint4(lo[4], lo[5], lo[6], lo[7]);
-    }
-    uint4 *dst_w = reinterpret_cast<uint4 *>(w_s + load_row * kLdsStride + load_k);
-    dst_w[0] = w_reg[0];
-    dst_w[1] = w_reg[1];
-  };
-
+  const int steps = (K + kBK - 1) / kBK;
   fetch(0);
-  for (int k0 = 0; k0 < K; k0 += kBK) {
-    __syncthreads();
-    stash();
-    __syncthreads();
-    if (k0 + kBK < K)
-      fetch(k0 + kBK);
+  stash(0);
+  __syncthreads();
+  for (int s = 0; s < steps; ++s) {
+    const int buffer = s & 1;
+    if (s + 1 < steps)
+      fetch((s + 1) * kBK);
+    const uint16_t *stage = lds + buffer * kStage;
+    const uint16_t *sa_hi = stage;
+    const uint16_t *sa_lo = stage + kPlaneA;
+    const uint16_t *sw = stage + (kSplit ? 2 : 1) * kPlaneA;
 #pragma unroll
     for (int ks = 0; ks < kBK; ks += 16) {
       const int koff = ks + (lane >> 5) * 8;
-      bf16x8 bh[2], bl_unused;
-      (void)bl_unused;
+      bf16x8 b[4];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int col = wave_n * 64 + j * 32 + (lane & 31);
-        bh[j] = *reinterpret_cast<const bf16x8 *>(w_s + col * kLdsStride + koff);
-      }
+      for (int j = 0; j < 4; ++j)
+        b[j] = *reinterpret_cast<const bf16x8 *>(
+            sw + (wave_n * 128 + j * 32 + (lane & 31)) * kStride + koff);
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int row = wave_m * 64 + i * 32 + (lane & 31);
-        const bf16x8 ah = *reinterpret_cast<const bf16x8 *>(a_hi + row * kLdsStride + koff);
+        const bf16x8 ah = *reinterpret_cast<const bf16x8 *>(sa_hi + row * kStride + koff);
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, b[j], acc[i][j], 0, 0, 0);
         if (kSplit) {
-          const bf16x8 al = *reinterpret_cast<const bf16x8 *>(a_lo + row * kLdsStride + koff);
+          const bf16x8 al = *reinterpret_cast<const bf16x8 *>(sa_lo + row * kStride + koff);
 #pragma unroll
-          for (int j = 0; j < 2; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh[j], acc[i][j], 0, 0, 0);
+          for (int j = 0; j < 4; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, b[j], acc[i][j], 0, 0, 0);
         }
       }
     }
+    if (s + 1 < steps)
+      stash(buffer ^ 1);
+    __syncthreads();
   }
 
-  // Epilogue. Accumulator e of tile (i, j): row i*32 + (e/4)*8 + (lane/32)*4 + e%4,
-  // column j*32 + lane%32 of the wave's 64x64 sub-tile.
-  const int col_base = block_n + wave_n * 64 + (lane & 31);
+  // Epilogue. Accumulator e of tile (i, j): row i*32 + (e/4)*8 + (lane/32)*4
+  // + e%4 and column j*32 + lane%32 of the wave's 64 x 128 sub-tile.
+  const int wave_col = block_n + wave_n * 128;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
 #pragma unroll
@@ -169,69 +175,100 @@ __global__ __launch_bounds__(256) void gemm_bf16w_kernel(
       if (row >= M)
         continue;
       if (epi.mode == kGemmGated) {
-        // Columns [64q, 64q+32) hold l1 rows, [64q+32, 64q+64) the matching l2
-        // rows, so one lane owns both operands of its gated output.
-        const int out_col = (block_n + wave_n * 64) / 2 + (lane & 31);
-        if (out_col < epi.gated_width) {
-          const float first = acc[i][0][e];
-          const float activated = epi.gelu ? gelu_erf(first) : first;
-          C[static_cast<size_t>(row) * ldc + out_col] = activated * acc[i][1][e];
+        // Columns [64q, 64q+32) hold l1 rows and [64q+32, 64q+64) the
+        // matching l2 rows: tiles (0,1) and (2,3) pair up in-lane.
+#pragma unroll
+        for (int pair = 0; pair < 2; ++pair) {
+          const int out_col = wave_col / 2 + pair * 32 + (lane & 31);
+          if (out_col < epi.gated_width) {
+            const float first = acc[i][2 * pair][e];
+            const float value = (epi.gelu ? gelu_erf(first) : first) * acc[i][2 * pair + 1][e];
+            const size_t index = static_cast<size_t>(row) * ldc + out_col;
+            const uint16_t hi = f32_to_bf16(value);
+            c_hi[index] = hi;
+            if (c_lo != nullptr)
+              c_lo[index] = f32_to_bf16(value - bf16_to_f32(hi));
+          }
         }
         continue;
       }
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int col = col_base + j * 32;
+      for (int j = 0; j < 4; ++j) {
+        const int col = wave_col + j * 32 + (lane & 31);
         if (col >= N)
           continue;
         float value = acc[i][j][e];
         const size_t index = static_cast<size_t>(row) * ldc + col;
-        if (epi.mode == kGemmBiasResidual) {
+        if (epi.mode == kGemmBias || epi.mode == kGemmBiasResidual)
           value = value + bf16_to_f32(epi.bias[col]);
+        if (epi.mode == kGemmResidual || epi.mode == kGemmBiasResidual)
           value = value + epi.residual[index];
-        } else if (epi.mode == kGemmResidual) {
-          value = value + epi.residual[index];
-        } else if (epi.mode == kGemmBias) {
-          value = value + bf16_to_f32(epi.bias[col]);
-        }
         C[index] = value;
       }
     }
   }
 }
 
+__global__ void split_kernel(const float *__restrict__ x, size_t n,
+                             uint16_t *__restrict__ hi, uint16_t *__restrict__ lo) {
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    const uint16_t h = f32_to_bf16(x[i]);
+    hi[i] = h;
+    if (lo != nullptr)
+      lo[i] = f32_to_bf16(x[i] - bf16_to_f32(h));
+  }
+}
+
 }  // namespace
 
-Status gemm_bf16w(const float *A, const uint16_t *W, float *C, size_t M,
-                  size_t N, size_t K, size_t ldc, GemmEpilogue mode,
+Status split_planes(const float *x, size_t n, uint16_t *hi, uint16_t *lo,
+                    hipStream_t stream) {
+  if (x == nullptr || hi == nullptr || n == 0)
+    return {ErrorCode::kInvalidArgument, "split_planes: invalid arguments"};
+  const unsigned grid = static_cast<unsigned>(std::min<size_t>((n + 255) / 256, 16384));
+  hipLaunchKernelGGL(split_kernel, dim3(grid), dim3(256), 0, stream, x, n, hi, lo);
+  return launch_status("split_kernel");
+}
+
+Status gemm_bf16w(const Activation &a, const uint16_t *W, const GemmOutput &out,
+                  size_t M, size_t N, size_t K, GemmEpilogue mode,
                   const uint16_t *bias, const float *residual, bool gelu,
-                  size_t gated_width, bool split, hipStream_t stream) {
-  if (A == nullptr || W == nullptr || C == nullptr || M == 0 || N == 0 ||
-      K == 0 || K % 8 != 0 || M > (1U << 30) || N > (1U << 30) ||
-      K > (1U << 30))
+                  size_t gated_width, hipStream_t stream) {
+  const bool split = a.lo != nullptr;
+  if (a.hi == nullptr || W == nullptr || M == 0 || N == 0 || K == 0 || K % 8 != 0 ||
+      a.ld < K || a.ld % 8 != 0 || M > (1U << 30) || N > (1U << 30) || K > (1U << 30))
     return {ErrorCode::kInvalidArgument,
-            "gemm_bf16w: null operand or unsupported shape (K must be a positive multiple of 8)"};
+            "gemm_bf16w: null operand or unsupported shape (K and lda multiples of 8)"};
   if ((mode == kGemmBias || mode == kGemmBiasResidual) && bias == nullptr)
     return {ErrorCode::kInvalidArgument, "gemm_bf16w: bias epilogue needs a bias"};
   if ((mode == kGemmResidual || mode == kGemmBiasResidual) && residual == nullptr)
     return {ErrorCode::kInvalidArgument, "gemm_bf16w: residual epilogue needs a residual"};
-  if (mode == kGemmGated && (N % 64 != 0 || gated_width * 2 > N))
-    return {ErrorCode::kInvalidArgument,
-            "gemm_bf16w: gated epilogue needs N = 2*padded width, multiple of 64"};
-  if (mode != kGemmGated && ldc < N)
-    return {ErrorCode::kInvalidArgument, "gemm_bf16w: ldc < N"};
+  if (mode == kGemmGated) {
+    if (N % 64 != 0 || gated_width * 2 > N || out.hi == nullptr || out.ld < gated_width)
+      return {ErrorCode::kInvalidArgument,
+              "gemm_bf16w: gated epilogue needs N = 2*padded width (multiple of 64) "
+              "and split-plane output"};
+  } else if (out.f32 == nullptr || out.ld < N) {
+    return {ErrorCode::kInvalidArgument, "gemm_bf16w: F32 output with ldc >= N required"};
+  }
   Epilogue epi{static_cast<int>(mode), bias, residual, gelu ? 1 : 0,
                static_cast<int>(gated_width)};
-  const dim3 grid(ceil_div(N, kBN), ceil_div(M, kBM));
+  const size_t tiles = static_cast<size_t>(ceil_div(M, kBM)) * ceil_div(N, kBN);
+  if (tiles > (1U << 31))
+    return {ErrorCode::kInvalidArgument, "gemm_bf16w: grid too large"};
+  const dim3 grid(static_cast<unsigned>(tiles));
   if (split)
-    hipLaunchKernelGGL(gemm_bf16w_kernel<true>, grid, dim3(256), 0, stream, A, W, C,
-                       static_cast<int>(M), static_cast<int>(N), static_cast<int>(K),
-                       static_cast<int>(ldc), epi);
+    hipLaunchKernelGGL(gemm_kernel<true>, grid, dim3(kThreads), 0, stream, a.hi, a.lo,
+                       static_cast<int>(a.ld), W, static_cast<int>(M), static_cast<int>(N),
+                       static_cast<int>(K), out.f32, out.hi, out.lo,
+                       static_cast<int>(out.ld), epi);
   else
-    hipLaunchKernelGGL(gemm_bf16w_kernel<false>, grid, dim3(256), 0, stream, A, W, C,
-                       static_cast<int>(M), static_cast<int>(N), static_cast<int>(K),
-                       static_cast<int>(ldc), epi);
-  return launch_status("gemm_bf16w_kernel");
+    hipLaunchKernelGGL(gemm_kernel<false>, grid, dim3(kThreads), 0, stream, a.hi, a.lo,
+                       static_cast<int>(a.ld), W, static_cast<int>(M), static_cast<int>(N),
+                       static_cast<int>(K), out.f32, out.hi, out.lo,
+                       static_cast<int>(out.ld), epi);
+  return launch_status("gemm_kernel");
 }
 
 }  // namespace evo::hip

@@ -142,13 +142,13 @@ __global__ void hcl_carry_kernel(float *__restrict__ chunk_state, size_t G,
 }
 
 // ---- HCL phase 3: rescan each chunk from its true start state.
-template <typename T>
+template <typename T, typename O>
 __global__ __launch_bounds__(kChannels) void hcl_output_kernel(
     const T *__restrict__ P, const float *__restrict__ short_history,
     const uint16_t *__restrict__ short_filter, int short_len, size_t L,
     size_t W, const float *__restrict__ poles,
     const float *__restrict__ residues, const float *__restrict__ direct,
-    int S, const float *__restrict__ chunk_state, T *__restrict__ out) {
+    int S, const float *__restrict__ chunk_state, O out) {
   const size_t c = blockIdx.x * static_cast<size_t>(kChannels) + threadIdx.x;
   if (c >= W)
     return;
@@ -174,7 +174,7 @@ __global__ __launch_bounds__(kChannels) void hcl_output_kernel(
       s[m] = p[m] * s[m] + u;
       modal += r[m] * s[m];
     }
-    store_act(out, t * W + c, x2 * (modal + d * u));
+    put(out, t * W + c, x2 * (modal + d * u));
   }
 }
 
@@ -184,13 +184,13 @@ __global__ __launch_bounds__(kChannels) void hcl_output_kernel(
 template <int kTile>
 __device__ inline void stage_u(const void *, int) {}
 
-template <typename T, int kTile, int kMaxTaps>
+template <typename T, typename O, int kTile, int kMaxTaps>
 __global__ __launch_bounds__(256) void hyena_fir_kernel(
     const T *__restrict__ P, const float *__restrict__ short_history,
     const uint16_t *__restrict__ short_filter, int short_len,
     const float *__restrict__ inner_history, const float *__restrict__ filter,
     size_t groups, int k, int causal, const float *__restrict__ direct,
-    size_t L, size_t W, T *__restrict__ out) {
+    size_t L, size_t W, O out) {
   extern __shared__ float smem[];
   float *u_s = smem;                                  // [(k-1) + kTile][64]
   float *x2_s = smem + (kMaxTaps - 1 + kTile) * 64;   // [kTile][64]
@@ -242,7 +242,7 @@ __global__ __launch_bounds__(256) void hyena_fir_kernel(
     total += current * h[causal ? 0 : hist];
     if (direct != nullptr)
       total += d * current;
-    store_act(out, static_cast<size_t>(t) * W + c, x2_s[r * 64 + lane] * total);
+    put(out, static_cast<size_t>(t) * W + c, x2_s[r * 64 + lane] * total);
   }
 }
 
@@ -300,13 +300,13 @@ size_t hyena_workspace_bytes(int kind, size_t length, size_t width,
   return hcl_chunks(length) * state * width * sizeof(float);
 }
 
-template <typename T>
+template <typename T, typename O>
 Status hyena_forward(int kind, const T *projection, size_t length,
                      size_t width, const HyenaWeights &wt,
                      float *short_history, float *inner_history,
                      float *modal_state, void *workspace,
-                     size_t workspace_bytes, T *out, hipStream_t stream) {
-  if (projection == nullptr || out == nullptr || wt.short_filter == nullptr ||
+                     size_t workspace_bytes, O out, hipStream_t stream) {
+  if (projection == nullptr || wt.short_filter == nullptr ||
       length == 0 || width == 0 || wt.short_len < 1 ||
       wt.short_len > kMaxShort || length > (1UL << 40))
     return {ErrorCode::kInvalidArgument, "hyena_forward: invalid arguments"};
@@ -332,7 +332,7 @@ Status hyena_forward(int kind, const T *projection, size_t length,
     hipLaunchKernelGGL(hcl_carry_kernel, dim3(ceil_div(width * wt.state, 256)), dim3(256),
                        0, stream, chunk_state, G, length, width, S, wt.poles, modal_state);
     EVO_TRY(launch_status("hcl_carry_kernel"));
-    hipLaunchKernelGGL(hcl_output_kernel<T>, grid, dim3(kChannels), 0, stream,
+    hipLaunchKernelGGL((hcl_output_kernel<T, O>), grid, dim3(kChannels), 0, stream,
                        projection, short_history, wt.short_filter, short_len,
                        length, width, wt.poles, wt.residues, wt.direct, S,
                        chunk_state, out);
@@ -350,7 +350,7 @@ Status hyena_forward(int kind, const T *projection, size_t length,
       static_assert(((kTaps - 1 + kTile) + kTile) * 64 * sizeof(float) <= 65536, "LDS");
       const size_t lds = ((kTaps - 1 + kTile) + kTile) * 64 * sizeof(float);
       const dim3 grid(channel_blocks.x, ceil_div(length, kTile));
-      hipLaunchKernelGGL((hyena_fir_kernel<T, kTile, kTaps>), grid, dim3(256), lds, stream,
+      hipLaunchKernelGGL((hyena_fir_kernel<T, O, kTile, kTaps>), grid, dim3(256), lds, stream,
                          projection, short_history, wt.short_filter, short_len,
                          inner_history, wt.inner_filter, wt.groups, k, causal,
                          direct, length, width, out);
@@ -359,11 +359,11 @@ Status hyena_forward(int kind, const T *projection, size_t length,
       const size_t lds = ((kTaps - 1 + kTile) + kTile) * 64 * sizeof(float);
       // 98 KB of the CU's 160 KB LDS: opt in above the 64 KB default.
       EVO_TRY(hip_status(hipFuncSetAttribute(
-                             reinterpret_cast<const void *>(&hyena_fir_kernel<T, kTile, kTaps>),
+                             reinterpret_cast<const void *>(&hyena_fir_kernel<T, O, kTile, kTaps>),
                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)),
                          "hyena_fir_kernel LDS opt-in"));
       const dim3 grid(channel_blocks.x, ceil_div(length, kTile));
-      hipLaunchKernelGGL((hyena_fir_kernel<T, kTile, kTaps>), grid, dim3(256), lds, stream,
+      hipLaunchKernelGGL((hyena_fir_kernel<T, O, kTile, kTaps>), grid, dim3(256), lds, stream,
                          projection, short_history, wt.short_filter, short_len,
                          inner_history, wt.inner_filter, wt.groups, k, causal,
                          direct, length, width, out);
@@ -387,13 +387,17 @@ Status hyena_forward(int kind, const T *projection, size_t length,
   return Status::Ok();
 }
 
-template Status hyena_forward<float>(int, const float *, size_t, size_t,
-                                     const HyenaWeights &, float *, float *,
-                                     float *, void *, size_t, float *,
-                                     hipStream_t);
-template Status hyena_forward<uint16_t>(int, const uint16_t *, size_t, size_t,
-                                        const HyenaWeights &, float *, float *,
-                                        float *, void *, size_t, uint16_t *,
-                                        hipStream_t);
+template Status hyena_forward<float, float *>(int, const float *, size_t, size_t,
+                                              const HyenaWeights &, float *, float *,
+                                              float *, void *, size_t, float *,
+                                              hipStream_t);
+template Status hyena_forward<uint16_t, uint16_t *>(int, const uint16_t *, size_t, size_t,
+                                                    const HyenaWeights &, float *, float *,
+                                                    float *, void *, size_t, uint16_t *,
+                                                    hipStream_t);
+template Status hyena_forward<float, SplitOut>(int, const float *, size_t, size_t,
+                                               const HyenaWeights &, float *, float *,
+                                               float *, void *, size_t, SplitOut,
+                                               hipStream_t);
 
 }  // namespace evo::hip

@@ -399,20 +399,32 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
   const size_t w = c.width;
   const bool split = options_.split_activations;
   float *hidden = hidden_.as<float>(), *residual = residual_.as<float>(),
-        *normed = normed_.as<float>(), *projected = projected_.as<float>(),
-        *mixed = mixed_.as<float>();
+        *projected = projected_.as<float>();
+  // GEMM activations live as split BF16 planes [2][rows][cols] (lo plane
+  // unused in the hip-bf16 profile).
+  uint16_t *normed_hi = normed_.as<uint16_t>(), *normed_lo = normed_hi + rows * w;
+  uint16_t *mixed_hi = mixed_.as<uint16_t>(), *mixed_lo = mixed_hi + rows * w;
+  uint16_t *gated_hi = gated_.as<uint16_t>(), *gated_lo = gated_hi + rows * c.inner;
+  const Activation normed{normed_hi, split ? normed_lo : nullptr, w};
+  const Activation mixed{mixed_hi, split ? mixed_lo : nullptr, w};
+  const Activation gated{gated_hi, split ? gated_lo : nullptr, c.inner};
+  const SplitOut mixed_out{mixed_hi, split ? mixed_lo : nullptr};
   for (size_t i = 0; i < c.layers; ++i) {
     const Layer &L = model_->layer[i];
     Cache &k = cache_[i];
-    EVO_TRY(rms_norm(hidden, rows, w, L.pre_norm.as<float>(), c.eps, normed, stream_));
+    EVO_TRY(rms_norm(hidden, rows, w, L.pre_norm.as<float>(), c.eps, nullptr, normed_hi,
+                     split ? normed_lo : nullptr, stream_));
     if (L.fp8) {
-      EVO_TRY(e4m3_quantize_f32(normed, rows * w, L.fp8_input_scale, codes_.as<uint8_t>(), stream_));
+      // codes of bf16(x) * input_scale: the hi plane is bf16(x) exactly.
+      EVO_TRY(e4m3_quantize_bf16(normed.hi, rows * w, L.fp8_input_scale,
+                                 codes_.as<uint8_t>(), stream_));
       const Fp8Mode mode = (w % 128 != 0) ? kFp8Exact : options_.fp8_mode;
       EVO_TRY(fp8_linear(codes_.as<uint8_t>(), L.projection.as<uint8_t>(), projected, rows,
                          3 * w, w, L.fp8_output_scale, mode, stream_));
     } else {
-      EVO_TRY(gemm_bf16w(normed, L.projection.as<uint16_t>(), projected, rows, 3 * w, w,
-                         3 * w, kGemmStore, nullptr, nullptr, false, 0, split, stream_));
+      EVO_TRY(gemm_bf16w(normed, L.projection.as<uint16_t>(),
+                         GemmOutput{projected, nullptr, nullptr, 3 * w}, rows, 3 * w, w,
+                         kGemmStore, nullptr, nullptr, false, 0, stream_));
     }
     if (L.type == Mixer::kAttention) {
       float *query = query_.as<float>();
@@ -420,7 +432,8 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
                        c.rope_scale, position_, query, k.keys.as<float>(),
                        k.values.as<float>(), stream_));
       EVO_TRY(causal_attention(query, k.keys.as<float>(), k.values.as<float>(), rows,
-                               position_, c.heads, c.head_dim(), mixed, stream_));
+                               position_, c.heads, c.head_dim(), nullptr, mixed_out.hi,
+                               mixed_out.lo, stream_));
     } else {
       HyenaWeights hw{};
       hw.short_filter = L.short_filter.as<uint16_t>();
@@ -434,25 +447,28 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
       hw.state = c.state;
       const int kind = L.type == Mixer::kHcs ? kHyenaHcs
                        : L.type == Mixer::kHcm ? kHyenaHcm : kHyenaHcl;
-      EVO_TRY(hyena_forward<float>(kind, projected, rows, w, hw,
-                                   k.short_history.as<float>(),
-                                   k.inner_history.as<float>(),
-                                   k.modal_state.as<float>(), workspace_.as<void>(),
-                                   workspace_.bytes(), mixed, stream_));
+      EVO_TRY((hyena_forward<float, SplitOut>(kind, projected, rows, w, hw,
+                                              k.short_history.as<float>(),
+                                              k.inner_history.as<float>(),
+                                              k.modal_state.as<float>(),
+                                              workspace_.as<void>(), workspace_.bytes(),
+                                              mixed_out, stream_)));
     }
     // residual = (mixed . Wout^T + bias) + hidden   (`src/cpu/model.cpp:641-645`)
-    EVO_TRY(gemm_bf16w(mixed, L.out_weight.as<uint16_t>(), residual, rows, w, w, w,
+    EVO_TRY(gemm_bf16w(mixed, L.out_weight.as<uint16_t>(),
+                       GemmOutput{residual, nullptr, nullptr, w}, rows, w, w,
                        kGemmBiasResidual, L.out_bias.as<uint16_t>(), hidden, false, 0,
-                       split, stream_));
-    EVO_TRY(rms_norm(residual, rows, w, L.post_norm.as<float>(), c.eps, normed, stream_));
-    // gated = act(l1 x) * (l2 x), act = erf-GELU in block 0 only (`:650-667`)
-    EVO_TRY(gemm_bf16w(normed, L.mlp_in.as<uint16_t>(), gated_.as<float>(), rows,
-                       2 * c.inner_padded, w, c.inner, kGemmGated, nullptr, nullptr,
-                       i == 0, c.inner, split, stream_));
-    // hidden = gated . l3^T + residual
-    EVO_TRY(gemm_bf16w(gated_.as<float>(), L.mlp_out.as<uint16_t>(), hidden, rows, w,
-                       c.inner, w, kGemmResidual, nullptr, residual, false, 0, split,
                        stream_));
+    EVO_TRY(rms_norm(residual, rows, w, L.post_norm.as<float>(), c.eps, nullptr, normed_hi,
+                     split ? normed_lo : nullptr, stream_));
+    // gated = act(l1 x) * (l2 x), act = erf-GELU in block 0 only (`:650-667`)
+    EVO_TRY(gemm_bf16w(normed, L.mlp_in.as<uint16_t>(),
+                       GemmOutput{nullptr, gated_hi, split ? gated_lo : nullptr, c.inner},
+                       rows, 2 * c.inner_padded, w, kGemmGated, nullptr, nullptr, i == 0,
+                       c.inner, stream_));
+    // hidden = gated . l3^T + residual
+    EVO_TRY(gemm_bf16w(gated, L.mlp_out.as<uint16_t>(), GemmOutput{hidden, nullptr, nullptr, w},
+                       rows, w, c.inner, kGemmResidual, nullptr, residual, false, 0, stream_));
     if (capture != nullptr && capture_layer == i)
       EVO_TRY(hip_check(hipMemcpyAsync(capture, hidden, rows * w * 4,
                                        hipMemcpyDeviceToHost, stream_),
@@ -483,11 +499,13 @@ Status Context::enqueue(const uint32_t *device_tokens, size_t rows, bool initial
                        c.width, hidden_.as<float>(), flag_.as<int>(), stream_));
   EVO_TRY(run_layers(rows, capture_layer, capture));
   if (device_logits != nullptr) {
+    uint16_t *hi = normed_.as<uint16_t>();
+    uint16_t *lo = options_.split_activations ? hi + rows * c.width : nullptr;
     EVO_TRY(rms_norm(hidden_.as<float>(), rows, c.width, model_->final_norm.as<float>(),
-                     c.eps, normed_.as<float>(), stream_));
-    EVO_TRY(gemm_bf16w(normed_.as<float>(), model_->embedding.as<uint16_t>(), device_logits,
-                       rows, c.vocab, c.width, c.vocab, kGemmStore, nullptr, nullptr, false,
-                       0, options_.split_activations, stream_));
+                     c.eps, nullptr, hi, lo, stream_));
+    EVO_TRY(gemm_bf16w(Activation{hi, lo, c.width}, model_->embedding.as<uint16_t>(),
+                       GemmOutput{device_logits, nullptr, nullptr, c.vocab}, rows, c.vocab,
+                       c.width, kGemmStore, nullptr, nullptr, false, 0, stream_));
   }
   position_ = initial ? rows : position_ + rows;
   return Status::Ok();

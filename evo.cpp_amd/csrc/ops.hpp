@@ -21,11 +21,36 @@ enum GemmEpilogue : int {
   kGemmGated = 4,
 };
 
-// C = A . W^T with A F32 [M,K], W BF16 [N,K]; see gemm.hip.
-Status gemm_bf16w(const float *A, const uint16_t *W, float *C, size_t M,
-                  size_t N, size_t K, size_t ldc, GemmEpilogue mode,
+// Output of a producer kernel feeding a GEMM: split BF16 planes
+// hi = bf16(v), lo = bf16(v - hi) (lo null: BF16 activations only).
+struct SplitOut {
+  uint16_t *hi;
+  uint16_t *lo;
+};
+
+// A GEMM activation as split BF16 planes: hi = bf16(a), lo = bf16(a - hi)
+// (lo null: BF16 activations), row stride ld elements.
+struct Activation {
+  const uint16_t *hi;
+  const uint16_t *lo;
+  size_t ld;
+};
+// GEMM output: F32 (store/bias/residual modes) or split planes (gated mode,
+// lo may be null), row stride ld elements.
+struct GemmOutput {
+  float *f32;
+  uint16_t *hi;
+  uint16_t *lo;
+  size_t ld;
+};
+// C = A . W^T with W BF16 [N,K]; see gemm.hip.
+Status gemm_bf16w(const Activation &a, const uint16_t *W, const GemmOutput &out,
+                  size_t M, size_t N, size_t K, GemmEpilogue mode,
                   const uint16_t *bias, const float *residual, bool gelu,
-                  size_t gated_width, bool split, hipStream_t stream);
+                  size_t gated_width, hipStream_t stream);
+// hi[i] = bf16(x[i]), lo[i] = bf16(x[i] - hi[i]) (lo may be null).
+Status split_planes(const float *x, size_t n, uint16_t *hi, uint16_t *lo,
+                    hipStream_t stream);
 
 // ---- Software FP8 (fp8.hip).
 // codes[i] = E4M3FN_RNE_satfinite(float(bf16(x[i])) * scale).
@@ -48,8 +73,10 @@ Status fp8_linear(const uint8_t *in_codes, const uint8_t *w_codes, float *out,
 Status embed_tokens(const uint32_t *tokens, size_t rows, const uint16_t *table,
                     size_t vocab, size_t width, float *out, int *invalid,
                     hipStream_t stream);
+// Writes the F32 result to out_f32 and/or split planes (out_hi, out_lo).
 Status rms_norm(const float *x, size_t rows, size_t width, const float *scale,
-                float eps, float *out, hipStream_t stream);
+                float eps, float *out_f32, uint16_t *out_hi, uint16_t *out_lo,
+                hipStream_t stream);
 // Copies the last `history` rows of the sequence [old_history ; x] into
 // history (F32 [history, channels]), keeping continuation caches.
 Status update_history(const float *x, size_t rows, size_t channels,
@@ -74,12 +101,13 @@ struct HyenaWeights {
 };
 size_t hyena_workspace_bytes(int kind, size_t length, size_t width,
                              size_t state);
-template <typename T>
+// O: float* (F32 out), uint16_t* (BF16 out) or SplitOut (GEMM planes).
+template <typename T, typename O>
 Status hyena_forward(int kind, const T *projection, size_t length,
                      size_t width, const HyenaWeights &weights,
                      float *short_history, float *inner_history,
                      float *modal_state, void *workspace,
-                     size_t workspace_bytes, T *out, hipStream_t stream);
+                     size_t workspace_bytes, O out, hipStream_t stream);
 
 // ---- Attention (attention.hip).
 // Splits the QKV projection [rows, 3W] into rotated Q and K and plain V,
@@ -90,9 +118,10 @@ Status qkv_rope(const float *projected, size_t rows, size_t width, size_t heads,
                 hipStream_t stream);
 // Causal attention of `rows` queries at positions prefix.. against keys
 // [0, prefix + rows). Layout [time, heads, head_dim] = [time, W].
+// Output: F32 (out_f32) or split planes (out_hi, out_lo).
 Status causal_attention(const float *q, const float *k_cache,
                         const float *v_cache, size_t rows, size_t prefix,
-                        size_t heads, size_t head_dim, float *out,
-                        hipStream_t stream);
+                        size_t heads, size_t head_dim, float *out_f32,
+                        uint16_t *out_hi, uint16_t *out_lo, hipStream_t stream);
 
 }  // namespace evo::hip

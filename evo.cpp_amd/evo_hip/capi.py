@@ -51,6 +51,9 @@ class EvoLibrary:
 
     def __init__(self, path: str):
         self.path = os.path.abspath(path)
+        if "libevo_hip" in os.path.basename(path):
+            from .native import share_hip_runtime
+            share_hip_runtime()
         lib = ctypes.CDLL(self.path)
         self.lib = lib
         lib.evo_abi_version.restype = ctypes.c_uint32

@@ -16,7 +16,7 @@ c_size, c_void, c_float, c_int = (ctypes.c_size_t, ctypes.c_void_p,
                                    ctypes.c_float, ctypes.c_int)
 
 HYENA_HCS, HYENA_HCM, HYENA_HCL = 0, 1, 2
-DTYPE_F32, DTYPE_BF16 = 0, 1
+DTYPE_F32, DTYPE_BF16, DTYPE_SPLIT = 0, 1, 2
 FP8_MFMA_K32, FP8_MFMA_K128, FP8_EXACT = 0, 1, 2
 
 # name -> (restype, argtypes) for include/evo/hip_ops.h
@@ -29,12 +29,15 @@ _OPS = {
     "evo_hip_e4m3_quantize": (c_int, [c_int, c_void, c_size, c_float, c_void, c_void]),
     "evo_hip_fp8_linear": (c_int, [c_void, c_void, c_void, c_size, c_size, c_size,
                                    c_float, c_int, c_void]),
-    "evo_hip_linear": (c_int, [c_void, c_void, c_void, c_void, c_size, c_size, c_size,
-                               c_int, c_void, c_void]),
+    "evo_hip_split_f32": (c_int, [c_void, c_size, c_void, c_void, c_void]),
+    "evo_hip_linear": (c_int, [c_void, c_void, c_void, c_void, c_void, c_size, c_size,
+                               c_size, c_void, c_void]),
     "evo_hip_pack_mlp": (c_int, [c_void, c_void, c_size, c_size, c_void, c_void]),
-    "evo_hip_gated_mlp": (c_int, [c_void, c_void, c_void, c_size, c_size, c_size, c_int,
+    "evo_hip_gated_mlp": (c_int, [c_void, c_void, c_void, c_void, c_size, c_size, c_size,
                                   c_int, c_void, c_void, c_void, c_void]),
-    "evo_hip_rms_norm": (c_int, [c_void, c_size, c_size, c_void, c_float, c_void, c_void]),
+    "evo_hip_rms_norm": (c_int, [c_void, c_size, c_size, c_void, c_float, c_void, c_void,
+                                 c_void, c_void]),
+    "evo_hip_context_prefill_resident": (c_int, [c_void, c_void, c_size, c_void]),
     "evo_hip_attention": (c_int, [c_void, c_size, c_size, c_size, c_int, c_void, c_float,
                                   c_size, c_void, c_void, c_void, c_void, c_void]),
 }
@@ -44,8 +47,20 @@ class OpError(RuntimeError):
     pass
 
 
+def share_hip_runtime() -> None:
+    """PyTorch-ROCm ships its own libamdhip64 with the system soname
+    (libamdhip64.so.7). Loading torch first makes libevo_hip.so bind to that
+    same runtime, so device pointers and streams are shared; loading the
+    library first would put two HIP runtimes in one process."""
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+
+
 @lru_cache(maxsize=None)
 def load(path: str = LIBRARY_PATH) -> ctypes.CDLL:
+    share_hip_runtime()
     if not os.path.exists(path):
         raise OpError(f"{path} is missing: build it with __graft_entry__.build() "
                       "(make -C evo.cpp_amd); there is no fallback implementation")

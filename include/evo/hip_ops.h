@@ -40,7 +40,13 @@ EVO_API evo_status evo_hip_context_prefill_resident(evo_context *context,
 EVO_API void *evo_hip_context_stream(const evo_context *context);
 
 /* Storage type of activation tensors passed to the Hyena operator. */
-typedef enum evo_hip_dtype { EVO_HIP_F32 = 0, EVO_HIP_BF16 = 1 } evo_hip_dtype;
+/* EVO_HIP_SPLIT: F32 input, output as split BF16 planes [2][rows][cols]
+ * (hi = bf16(y), lo = bf16(y - hi)), the GEMM activation layout. */
+typedef enum evo_hip_dtype {
+  EVO_HIP_F32 = 0,
+  EVO_HIP_BF16 = 1,
+  EVO_HIP_SPLIT = 2
+} evo_hip_dtype;
 typedef enum evo_hip_hyena_kind {
   EVO_HIP_HYENA_HCS = 0,
   EVO_HIP_HYENA_HCM = 1,
@@ -92,33 +98,42 @@ EVO_API evo_status evo_hip_fp8_linear(const uint8_t *in_codes,
                                       float output_scale, int mode,
                                       void *stream);
 
-/* out[M,N] = x[M,K] . w[N,K]^T (+ bf16 bias[N]) (+ residual[M,N]), F32 x and
- * out, BF16 w. split != 0 uses two BF16 MFMA passes per F32 activation.
+/* GEMM activation layout: hi[i] = bf16(x[i]), lo[i] = bf16(x[i] - hi[i])
+ * (lo may be NULL for BF16-only activations). */
+EVO_API evo_status evo_hip_split_f32(const float *x, size_t count, uint16_t *hi,
+                                     uint16_t *lo, void *stream);
+
+/* out[M,N] = x[M,K] . w[N,K]^T (+ bf16 bias[N]) (+ residual[M,N]); x as
+ * split BF16 planes (x_lo NULL: one BF16 MFMA pass), w BF16, out F32.
  * Replaces `bf16_linear` (`include/evo/cuda/ops.hpp:61-70`) and the CPU
  * `linear` (`src/cpu/model.cpp:284-314`). */
-EVO_API evo_status evo_hip_linear(const float *x, const uint16_t *w,
-                                  const uint16_t *bias, const float *residual,
-                                  size_t m, size_t n, size_t k, int split,
-                                  float *out, void *stream);
+EVO_API evo_status evo_hip_linear(const uint16_t *x_hi, const uint16_t *x_lo,
+                                  const uint16_t *w, const uint16_t *bias,
+                                  const float *residual, size_t m, size_t n,
+                                  size_t k, float *out, void *stream);
 
-/* Gated MLP out[M,F] = l3(act(l1 x) * l2 x) with act = erf-GELU when gelu != 0.
- * w12 is the interleaved [2*Fp, K] l1/l2 weight (32-row blocks, Fp = F
- * rounded up to 32) built by evo_hip_pack_mlp; inner [M, F] is workspace.
+/* Gated MLP out[M,W] = l3(act(l1 x) * l2 x) (+ residual) with act = erf-GELU
+ * when gelu != 0. w12 is the interleaved [2*Fp, W] l1/l2 weight (32-row
+ * blocks, Fp = F rounded up to 32) built by evo_hip_pack_mlp;
+ * inner_workspace holds the gated [M, F] activation as split planes
+ * (2*M*F uint16, or M*F when x_lo is NULL).
  * Replaces `bf16_mlp` (`include/evo/cuda/ops.hpp:133-138`). */
 EVO_API evo_status evo_hip_pack_mlp(const uint16_t *l1, const uint16_t *l2,
                                     size_t inner, size_t width, uint16_t *w12,
                                     void *stream);
-EVO_API evo_status evo_hip_gated_mlp(const float *x, const uint16_t *w12,
-                                     const uint16_t *l3, size_t m, size_t width,
-                                     size_t inner, int gelu, int split,
-                                     float *inner_workspace,
+EVO_API evo_status evo_hip_gated_mlp(const uint16_t *x_hi, const uint16_t *x_lo,
+                                     const uint16_t *w12, const uint16_t *l3,
+                                     size_t m, size_t width, size_t inner,
+                                     int gelu, uint16_t *inner_workspace,
                                      const float *residual, float *out,
                                      void *stream);
 
-/* RMSNorm y = x / (sqrt(mean(x^2)) + eps) * scale over rows of width.
+/* RMSNorm y = x / (sqrt(mean(x^2)) + eps) * scale over rows of width,
+ * written as F32 (out) and/or split BF16 planes (out_hi, out_lo).
  * Replaces `bf16_rms_norm` (`include/evo/cuda/ops.hpp:117-120`). */
 EVO_API evo_status evo_hip_rms_norm(const float *x, size_t rows, size_t width,
                                     const float *scale, float eps, float *out,
+                                    uint16_t *out_hi, uint16_t *out_lo,
                                     void *stream);
 
 /* Attention block body: split Wqkv output [rows, 3W], RoPE, append to K/V

@@ -10,6 +10,9 @@ sys.path.insert(0, os.path.join(ROOT, "tests"))
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
+    # torch first: libevo_hip.so then binds to torch's HIP runtime (same
+    # soname), so one runtime owns every device pointer and stream.
+    import torch  # noqa: F401
 
 
 @pytest.fixture(scope="session")

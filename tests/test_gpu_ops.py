@@ -91,16 +91,24 @@ def test_qgmma_exact_bit_exact(m, k, n):
 @pytest.mark.parametrize("mode", [N.FP8_MFMA_K32, N.FP8_MFMA_K128])
 @pytest.mark.parametrize("m,k,n", [(128, 128, 128), (200, 512, 300), (1024, 4096, 256)])
 def test_fp8_mfma_close_to_qgmma(mode, m, k, n):
-    """MFMA chunks are F32-exact sums; they differ from QGMMA only by its
-    per-term truncation (a few E8M13 ulps, 2^-13 relative), which can move the
-    final BF16 rounding by one BF16 ulp: bound per element 2^-7 |ref| plus
-    2^-12 of the output scale, and at most 10 % of the elements may differ."""
+    """MFMA chunks are F32 sums; the reference additionally truncates every
+    aligned term toward zero (13 fractional bits under the group maximum),
+    a sign-random deviation of ~sqrt(K) half-quanta, i.e. about 2^-8 of the
+    accumulator at K = 4096, on top of the final BF16 rounding. Bounds: RMS
+    difference <= 2^-8 of the RMS output, worst element <= 2^-6 of the
+    output scale. The per-promotion E8M13 truncation (toward zero) that
+    mfma-k32 reproduces makes it track the reference more closely than an
+    exact float64 dot does."""
     a, w = fp8_case(11 + m, m, k, n)
-    expected = O.qgmma(a, w, 0.03125)
-    actual = fp8_gpu(a, w, 0.03125, mode)
-    bound = 2.0 ** -7 * np.abs(expected) + 2.0 ** -12 * np.abs(expected).max()
-    assert np.all(np.abs(actual - expected) <= bound)
-    assert np.mean(actual != expected) < 0.10
+    expected = O.qgmma(a, w, 0.03125).astype(np.float64)
+    actual = fp8_gpu(a, w, 0.03125, mode).astype(np.float64)
+    rms = np.sqrt(np.mean(expected ** 2))
+    assert np.sqrt(np.mean((actual - expected) ** 2)) <= 2.0 ** -8 * rms
+    assert np.abs(actual - expected).max() <= 2.0 ** -6 * np.abs(expected).max()
+    dec = np.vectorize(lambda c: O.lib().oracle_e4m3_decode(int(c)))
+    exact = (dec(a) @ dec(w).T) * 0.03125
+    if mode == N.FP8_MFMA_K32 and k >= 512:
+        assert np.mean((actual - expected) ** 2) < np.mean((exact - expected) ** 2)
 
 
 def test_fp8_mfma_exact_on_representable_sums():
@@ -133,10 +141,27 @@ def test_linear_split_matches_oracle(m, n, k, bias, residual):
     if residual:
         expected = expected + res
     out = empty((m, n))
-    N.call("evo_hip_linear", p(dev(x)), p(dev(w)), p(dev(b) if bias else None),
-           p(dev(res) if residual else None), m, n, k, 1, p(out), stream())
+    hi, lo = split_gpu(x)
+    N.call("evo_hip_linear", p(hi), p(lo), p(dev(w)), p(dev(b) if bias else None),
+           p(dev(res) if residual else None), m, n, k, p(out), stream())
     # split-BF16 activations: ~2^-17 relative per product, F32 accumulation
     assert rel_err(host(out), expected) < 2e-5
+
+
+def split_gpu(x):
+    hi, lo = empty(x.shape, np.uint16), empty(x.shape, np.uint16)
+    N.call("evo_hip_split_f32", p(dev(x)), x.size, p(hi), p(lo), stream())
+    return hi, lo
+
+
+def test_split_planes_exact():
+    x = rng(2).standard_normal(4099).astype(np.float32) * 100
+    hi, lo = split_gpu(x)
+    h, l = host(hi).view(np.uint16), host(lo).view(np.uint16)
+    assert np.array_equal(h, bf16_bits(x))
+    assert np.array_equal(l, bf16_bits(x - bf16_to_f32(h)))
+    # hi + lo carries 16 significant bits: |x - (hi + lo)| <= 2^-16 |x|
+    assert np.all(np.abs(x - bf16_to_f32(h) - bf16_to_f32(l)) <= 2.0 ** -16 * np.abs(x))
 
 
 def test_linear_bf16_profile_is_bf16_accurate():
@@ -144,7 +169,8 @@ def test_linear_bf16_profile_is_bf16_accurate():
     x = r.standard_normal((96, 512)).astype(np.float32)
     w = bf16_bits(r.standard_normal((160, 512)).astype(np.float32) / 22.6)
     out = empty((96, 160))
-    N.call("evo_hip_linear", p(dev(x)), p(dev(w)), None, None, 96, 160, 512, 0,
+    hi, _ = split_gpu(x)
+    N.call("evo_hip_linear", p(hi), None, p(dev(w)), None, None, 96, 160, 512,
            p(out), stream())
     expected = O.linear_bf16w(bf16_to_f32(bf16_bits(x)), w)
     assert rel_err(host(out), expected) < 2e-5
@@ -163,8 +189,9 @@ def test_gated_mlp(gelu):
     padded = (inner + 31) // 32 * 32
     w12 = zeros((2 * padded, width), np.uint16)
     N.call("evo_hip_pack_mlp", p(dev(l1)), p(dev(l2)), inner, width, p(w12), stream())
-    scratch, out = empty((m, inner)), empty((m, width))
-    N.call("evo_hip_gated_mlp", p(dev(x)), p(w12), p(dev(l3)), m, width, inner, gelu, 1,
+    scratch, out = empty((2 * m * inner,), np.uint16), empty((m, width))
+    hi, lo = split_gpu(x)
+    N.call("evo_hip_gated_mlp", p(hi), p(lo), p(w12), p(dev(l3)), m, width, inner, gelu,
            p(scratch), p(dev(res)), p(out), stream())
     first = O.linear_bf16w(x, l1).astype(np.float64)
     second = O.linear_bf16w(x, l2).astype(np.float64)
@@ -181,9 +208,15 @@ def test_rms_norm(oracle):
         expected = np.zeros_like(x)
         oracle.oracle_rms_norm(O.ptr(x), rows, width, O.ptr(scale), 1e-6, O.ptr(expected))
         out = empty((rows, width))
+        hi, lo = empty((rows, width), np.uint16), empty((rows, width), np.uint16)
         N.call("evo_hip_rms_norm", p(dev(x)), rows, width, p(dev(scale)), 1e-6, p(out),
-               stream())
-        assert rel_err(host(out), expected) < 1e-5
+               p(hi), p(lo), stream())
+        got = host(out)
+        assert rel_err(got, expected) < 1e-5
+        # the planes are the split of the F32 result
+        assert np.array_equal(host(hi).view(np.uint16), bf16_bits(got))
+        assert np.array_equal(host(lo).view(np.uint16),
+                              bf16_bits(got - bf16_to_f32(bf16_bits(got))))
 
 
 # --------------------------------------------------------------- Hyena
@@ -224,6 +257,9 @@ def hyena_gpu(kind, case, dtype=N.DTYPE_F32, rows=None, caches=None, projection=
     if dtype == N.DTYPE_BF16:
         proj_d = dev(bf16_bits(proj))
         out = empty((length, width), np.uint16)
+    elif dtype == N.DTYPE_SPLIT:
+        proj_d = dev(proj)
+        out = empty((2, length, width), np.uint16)
     else:
         proj_d = dev(proj)
         out = empty((length, width))
@@ -237,6 +273,9 @@ def hyena_gpu(kind, case, dtype=N.DTYPE_F32, rows=None, caches=None, projection=
            p(caches.get("short")), p(caches.get("inner")), p(caches.get("modal")),
            p(ws), ws_bytes, p(out), stream())
     result = host(out)
+    if dtype == N.DTYPE_SPLIT:
+        planes = bf16_to_f32(result.view(np.uint16))
+        return planes[0].astype(np.float64) + planes[1]
     return bf16_to_f32(result.view(np.uint16)) if dtype == N.DTYPE_BF16 else result
 
 
@@ -250,6 +289,14 @@ def test_hyena_f32_matches_oracle(kind, inner_len, length, width):
                       inner_len=inner_len or 7)
     expected = hyena_oracle(kind, case)
     assert rel_err(hyena_gpu(kind, case), expected) < 1e-5
+
+
+@pytest.mark.parametrize("kind,inner_len", KINDS)
+def test_hyena_split_output(kind, inner_len):
+    """F32 in, split planes out: hi + lo reproduces the F32 result to 2^-16."""
+    case = hyena_case(91 + kind, kind, 513, 96, inner_len=inner_len or 7)
+    expected = hyena_oracle(kind, case)
+    assert rel_err(hyena_gpu(kind, case, dtype=N.DTYPE_SPLIT), expected) < 2e-5
 
 
 @pytest.mark.parametrize("kind,inner_len", KINDS)
