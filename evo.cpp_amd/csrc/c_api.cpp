@@ -694,18 +694,23 @@ evo_status evo_hip_rms_norm(const float *x, size_t rows, size_t width, const flo
 
 evo_status evo_hip_attention(const float *projected, size_t rows, size_t width, size_t heads,
                              int column_split, const float *inv_freq, float rope_scale,
-                             size_t prefix, float *query, float *key_cache,
-                             float *value_cache, float *out, void *stream) {
+                             size_t prefix, uint16_t *query, uint16_t *key_cache,
+                             uint16_t *value_cache, size_t capacity, float *out,
+                             void *stream) {
   return protect([&]() -> evo_status {
     const auto s = static_cast<hipStream_t>(stream);
+    if (prefix + rows > capacity)
+      return publish(EVO_STATUS_INVALID_ARGUMENT,
+                     "invalid_argument: attention rows exceed the cache capacity");
     auto status = evo::hip::qkv_rope(projected, rows, width, heads, column_split != 0,
-                                     inv_freq, rope_scale, prefix, query, key_cache,
-                                     value_cache, s);
+                                     inv_freq, rope_scale, prefix, query, rows * width,
+                                     key_cache, value_cache, capacity * width, s);
     if (!status.ok())
       return publish(status);
-    return publish(evo::hip::causal_attention(query, key_cache, value_cache, rows, prefix,
-                                              heads, heads == 0 ? 0 : width / heads, out,
-                                              nullptr, nullptr, s));
+    return publish(evo::hip::causal_attention(query, rows * width, key_cache, value_cache,
+                                              capacity * width, rows, prefix, heads,
+                                              heads == 0 ? 0 : width / heads, out, nullptr,
+                                              nullptr, s));
   });
 }
 

@@ -369,6 +369,7 @@ Status Context::initialize(std::shared_ptr<const Model> model, size_t capacity,
     const Layer &L = model_->layer[i];
     Cache &k = cache_[i];
     if (L.type == Mixer::kAttention) {
+      // split BF16 planes [2][capacity][W]
       EVO_TRY(k.keys.allocate(capacity * w * 4, "key cache"));
       EVO_TRY(k.values.allocate(capacity * w * 4, "value cache"));
       continue;
@@ -427,13 +428,15 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
                          kGemmStore, nullptr, nullptr, false, 0, stream_));
     }
     if (L.type == Mixer::kAttention) {
-      float *query = query_.as<float>();
+      uint16_t *query = query_.as<uint16_t>();
+      const size_t cache_plane = capacity_ * w;
       EVO_TRY(qkv_rope(projected, rows, w, c.heads, c.column_split, L.inv_freq.as<float>(),
-                       c.rope_scale, position_, query, k.keys.as<float>(),
-                       k.values.as<float>(), stream_));
-      EVO_TRY(causal_attention(query, k.keys.as<float>(), k.values.as<float>(), rows,
-                               position_, c.heads, c.head_dim(), nullptr, mixed_out.hi,
-                               mixed_out.lo, stream_));
+                       c.rope_scale, position_, query, rows * w, k.keys.as<uint16_t>(),
+                       k.values.as<uint16_t>(), cache_plane, stream_));
+      EVO_TRY(causal_attention(query, rows * w, k.keys.as<uint16_t>(),
+                               k.values.as<uint16_t>(), cache_plane, rows, position_,
+                               c.heads, c.head_dim(), nullptr, mixed_out.hi, mixed_out.lo,
+                               stream_));
     } else {
       HyenaWeights hw{};
       hw.short_filter = L.short_filter.as<uint16_t>();

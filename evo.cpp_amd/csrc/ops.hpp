@@ -109,19 +109,20 @@ Status hyena_forward(int kind, const T *projection, size_t length,
                      float *modal_state, void *workspace,
                      size_t workspace_bytes, O out, hipStream_t stream);
 
-// ---- Attention (attention.hip).
-// Splits the QKV projection [rows, 3W] into rotated Q and K and plain V,
-// appending K/V rows at position `prefix` of the caches [capacity, W].
+// ---- Attention (attention.hip). Q and the K/V caches are split BF16 planes:
+// plane 0 (hi) at the pointer, plane 1 (lo) `*_plane` elements further.
+// qkv_rope splits the QKV projection [rows, 3W] into rotated Q, rotated K and
+// V, appending K/V rows at position `prefix` of the caches [capacity, W].
 Status qkv_rope(const float *projected, size_t rows, size_t width, size_t heads,
                 bool column_split, const float *inv_freq, float rope_scale,
-                size_t prefix, float *q, float *k_cache, float *v_cache,
-                hipStream_t stream);
+                size_t prefix, uint16_t *q, size_t q_plane, uint16_t *k_cache,
+                uint16_t *v_cache, size_t cache_plane, hipStream_t stream);
 // Causal attention of `rows` queries at positions prefix.. against keys
-// [0, prefix + rows). Layout [time, heads, head_dim] = [time, W].
-// Output: F32 (out_f32) or split planes (out_hi, out_lo).
-Status causal_attention(const float *q, const float *k_cache,
-                        const float *v_cache, size_t rows, size_t prefix,
-                        size_t heads, size_t head_dim, float *out_f32,
+// [0, prefix + rows). Layout [time, heads, head_dim] = [time, W]. Output F32
+// (out_f32) or split planes (out_hi, out_lo).
+Status causal_attention(const uint16_t *q, size_t q_plane, const uint16_t *k_cache,
+                        const uint16_t *v_cache, size_t cache_plane, size_t rows,
+                        size_t prefix, size_t heads, size_t head_dim, float *out_f32,
                         uint16_t *out_hi, uint16_t *out_lo, hipStream_t stream);
 
 }  // namespace evo::hip

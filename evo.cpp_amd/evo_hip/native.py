@@ -39,7 +39,7 @@ _OPS = {
                                  c_void, c_void]),
     "evo_hip_context_prefill_resident": (c_int, [c_void, c_void, c_size, c_void]),
     "evo_hip_attention": (c_int, [c_void, c_size, c_size, c_size, c_int, c_void, c_float,
-                                  c_size, c_void, c_void, c_void, c_void, c_void]),
+                                  c_size, c_void, c_void, c_void, c_size, c_void, c_void]),
 }
 
 

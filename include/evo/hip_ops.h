@@ -136,18 +136,19 @@ EVO_API evo_status evo_hip_rms_norm(const float *x, size_t rows, size_t width,
                                     uint16_t *out_hi, uint16_t *out_lo,
                                     void *stream);
 
-/* Attention block body: split Wqkv output [rows, 3W], RoPE, append to K/V
- * caches [capacity, W] at `prefix`, causal softmax attention into out
- * [rows, W]; query is [rows, W] workspace.
+/* Attention block body: split the Wqkv output [rows, 3W], apply RoPE at
+ * positions prefix.., append K/V at `prefix` of the caches, causal softmax
+ * attention into out [rows, W] F32. query is workspace of 2*rows*W uint16;
+ * key_cache / value_cache hold split BF16 planes [2][capacity][W] uint16.
  * Replaces `bf16_split_qkv` + `bf16_apply_rope` + `bf16_kv_append` +
  * `bf16_online_causal_attention` (`include/evo/cuda/attention.hpp:100-133`). */
 EVO_API evo_status evo_hip_attention(const float *projected, size_t rows,
                                      size_t width, size_t heads,
                                      int column_split, const float *inv_freq,
                                      float rope_scale, size_t prefix,
-                                     float *query, float *key_cache,
-                                     float *value_cache, float *out,
-                                     void *stream);
+                                     uint16_t *query, uint16_t *key_cache,
+                                     uint16_t *value_cache, size_t capacity,
+                                     float *out, void *stream);
 
 #ifdef __cplusplus
 }

@@ -59,9 +59,11 @@ def make(tmp_path, shape, seed, **kw):
     return path
 
 
-@pytest.mark.parametrize("length,arena", [(100, None), (300, 64), (37, 16)])
-def test_tiny_model_logits(hip, tmp_path, length, arena):
-    shape = A.tiny_shape(width=64, layers=8, heads=4, inner=96, groups=16, attn=(3,))
+@pytest.mark.parametrize("length,arena,heads", [(100, None, 4), (300, 64, 4), (37, 16, 4),
+                                               (200, None, 2), (333, 128, 2)])
+def test_tiny_model_logits(hip, tmp_path, length, arena, heads):
+    """heads 4 -> head_dim 16 (VALU attention), heads 2 -> 32 (MFMA attention)."""
+    shape = A.tiny_shape(width=64, layers=8, heads=heads, inner=96, groups=16, attn=(3,))
     path = make(tmp_path, shape, seed=11)
     tokens = A.acgt_tokens(length, seed=length)
     expected = O.OracleModel(path).prefill(tokens)

@@ -328,8 +328,9 @@ def test_hyena_continuation_equals_one_pass(kind, inner_len, split):
 
 
 # ----------------------------------------------------------- attention
-@pytest.mark.parametrize("rows,heads,head_dim,prefix", [(70, 4, 16, 0), (130, 2, 128, 0),
-                                                        (64, 3, 64, 33)])
+@pytest.mark.parametrize("rows,heads,head_dim,prefix", [
+    (70, 4, 16, 0), (130, 2, 128, 0), (64, 3, 64, 33), (300, 2, 128, 129), (1, 4, 32, 0),
+    (257, 1, 32, 0), (1000, 2, 128, 0)])
 def test_attention_matches_oracle(oracle, rows, heads, head_dim, prefix):
     r = rng(rows + heads)
     width = heads * head_dim
@@ -349,11 +350,11 @@ def test_attention_matches_oracle(oracle, rows, heads, head_dim, prefix):
     O.check(oracle.oracle_causal_attention(O.ptr(q), O.ptr(k), O.ptr(v), total, heads,
                                            head_dim, O.ptr(expected)))
     expected = expected.reshape(total, width)[prefix:]
-    kc, vc = zeros((total, width)), zeros((total, width))
-    query, out = empty((total, width)), empty((total, width))
+    kc, vc = zeros((2, total, width), np.uint16), zeros((2, total, width), np.uint16)
+    query, out = empty((2, total, width), np.uint16), empty((total, width))
     if prefix:
         N.call("evo_hip_attention", p(dev(proj[:prefix])), prefix, width, heads, 1,
-               p(dev(inv_freq)), 8.0, 0, p(query), p(kc), p(vc), p(out), stream())
+               p(dev(inv_freq)), 8.0, 0, p(query), p(kc), p(vc), total, p(out), stream())
     N.call("evo_hip_attention", p(dev(proj[prefix:])), rows, width, heads, 1,
-           p(dev(inv_freq)), 8.0, prefix, p(query), p(kc), p(vc), p(out), stream())
+           p(dev(inv_freq)), 8.0, prefix, p(query), p(kc), p(vc), total, p(out), stream())
     assert rel_err(host(out)[:rows], expected) < 1e-5
