@@ -332,7 +332,7 @@ evo_status evo_context_create(const evo_model *model, const evo_context_params *
     hip_options.split_activations = (options.flags & EVO_CONTEXT_FLAG_HIP_BF16) == 0;
     hip_options.fp8_mode = (options.flags & EVO_CONTEXT_FLAG_HIP_FP8_EXACT) != 0
                                ? evo::hip::kFp8Exact
-                               : evo::hip::kFp8MfmaK32;
+                               : evo::hip::kFp8MfmaK128;
     auto handle = std::make_unique<evo_context>();
     handle->state = model->state;
     handle->hip = std::make_unique<evo::hip::Context>();

@@ -101,7 +101,7 @@ private:
 
 struct ContextOptions {
   bool split_activations{true};   // "hip-f32" (true) or "hip-bf16" (false)
-  Fp8Mode fp8_mode{kFp8MfmaK32};
+  Fp8Mode fp8_mode{kFp8MfmaK128};
 };
 
 class Context {

@@ -79,7 +79,8 @@ enum {
    * each F32 activation into two BF16 terms. */
   EVO_CONTEXT_FLAG_HIP_BF16 = 1u << 8u,
   /* Software-FP8 projections run through the bit-exact integer QGMMA
-   * emulation instead of the E4M3 MFMA path ("hip-fp8-exact"). */
+   * emulation ("+fp8-exact") instead of the default E4M3 MFMA path, which
+   * promotes each 128-K chunk into an E8M13-truncated accumulator. */
   EVO_CONTEXT_FLAG_HIP_FP8_EXACT = 1u << 9u
 };
 
