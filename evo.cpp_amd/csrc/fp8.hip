@@ -93,9 +93,10 @@ __device__ inline int float_exponent(const float v) {
 constexpr int kExactTile = 16;
 constexpr int kGroup = 32;
 
+template <typename Out>
 __global__ __launch_bounds__(256) void qgmma_exact_kernel(
     const uint8_t *__restrict__ a, const uint8_t *__restrict__ w,
-    float *__restrict__ out, int M, int N, int K, float output_scale) {
+    Out *__restrict__ out, int M, int N, int K, float output_scale) {
   __shared__ uint16_t a_tile[kExactTile][kGroup];
   __shared__ uint16_t w_tile[kGroup][kExactTile + 1];
   const int t = threadIdx.x;
@@ -146,17 +147,17 @@ __global__ __launch_bounds__(256) void qgmma_exact_kernel(
     __syncthreads();
   }
   if (row < M && col < N)
-    out[static_cast<size_t>(row) * N + col] = round_bf16(acc * output_scale);
+    put(out, static_cast<size_t>(row) * N + col, round_bf16(acc * output_scale));
 }
 
 // MFMA path. Block 128x128 outputs, 4 waves of 64x64 (2x2 tiles 32x32),
 // K staged 128 bytes per step through LDS rows padded to 144 B.
 constexpr int kBM = 128, kBN = 128, kBK = 128, kStride = kBK + 16;
 
-template <int kChunk>
+template <int kChunk, typename Out>
 __global__ __launch_bounds__(256) void fp8_mfma_kernel(
     const uint8_t *__restrict__ a, const uint8_t *__restrict__ w,
-    float *__restrict__ out, int M, int N, int K, float output_scale) {
+    Out *__restrict__ out, int M, int N, int K, float output_scale) {
   __shared__ __attribute__((aligned(16))) uint8_t a_s[kBM * kStride];
   __shared__ __attribute__((aligned(16))) uint8_t w_s[kBN * kStride];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -276,7 +277,7 @@ __global__ __launch_bounds__(256) void fp8_mfma_kernel(
       for (int j = 0; j < 2; ++j) {
         const int col = block_n + wave_n * 64 + j * 32 + (lane & 31);
         if (col < N)
-          out[static_cast<size_t>(row) * N + col] = round_bf16(acc[i][j][e] * output_scale);
+          put(out, static_cast<size_t>(row) * N + col, round_bf16(acc[i][j][e] * output_scale));
       }
     }
 }
@@ -310,9 +311,10 @@ Status e4m3_quantize_bf16(const uint16_t *x, size_t n, float scale,
   return launch_status("quantize_bf16_kernel");
 }
 
-Status fp8_linear(const uint8_t *in_codes, const uint8_t *w_codes, float *out,
-                  size_t M, size_t N, size_t K, float output_scale,
-                  Fp8Mode mode, hipStream_t stream) {
+template <typename Out>
+Status fp8_linear_impl(const uint8_t *in_codes, const uint8_t *w_codes, Out *out,
+                       size_t M, size_t N, size_t K, float output_scale,
+                       Fp8Mode mode, hipStream_t stream) {
   if (in_codes == nullptr || w_codes == nullptr || out == nullptr || M == 0 ||
       N == 0 || K == 0 || K % 32 != 0 || !(output_scale > 0.0F) ||
       !__builtin_isfinite(output_scale) || M > (1U << 30) || N > (1U << 30))
@@ -320,7 +322,7 @@ Status fp8_linear(const uint8_t *in_codes, const uint8_t *w_codes, float *out,
             "fp8_linear: invalid arguments (K must be a positive multiple of 32)"};
   const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
   if (mode == kFp8Exact) {
-    hipLaunchKernelGGL(qgmma_exact_kernel, dim3(ceil_div(N, kExactTile), ceil_div(M, kExactTile)),
+    hipLaunchKernelGGL(qgmma_exact_kernel<Out>, dim3(ceil_div(N, kExactTile), ceil_div(M, kExactTile)),
                        dim3(256), 0, stream, in_codes, w_codes, out, m, n, k, output_scale);
     return launch_status("qgmma_exact_kernel");
   }
@@ -328,14 +330,26 @@ Status fp8_linear(const uint8_t *in_codes, const uint8_t *w_codes, float *out,
     return {ErrorCode::kInvalidArgument, "fp8_linear: MFMA modes need K % 128 == 0"};
   const dim3 grid(ceil_div(N, kBN), ceil_div(M, kBM));
   if (mode == kFp8MfmaK32)
-    hipLaunchKernelGGL(fp8_mfma_kernel<32>, grid, dim3(256), 0, stream, in_codes,
+    hipLaunchKernelGGL((fp8_mfma_kernel<32, Out>), grid, dim3(256), 0, stream, in_codes,
                        w_codes, out, m, n, k, output_scale);
   else if (mode == kFp8MfmaK128)
-    hipLaunchKernelGGL(fp8_mfma_kernel<128>, grid, dim3(256), 0, stream, in_codes,
+    hipLaunchKernelGGL((fp8_mfma_kernel<128, Out>), grid, dim3(256), 0, stream, in_codes,
                        w_codes, out, m, n, k, output_scale);
   else
     return {ErrorCode::kInvalidArgument, "fp8_linear: unknown mode"};
   return launch_status("fp8_mfma_kernel");
+}
+
+Status fp8_linear(const uint8_t *in_codes, const uint8_t *w_codes, float *out,
+                  size_t M, size_t N, size_t K, float output_scale,
+                  Fp8Mode mode, hipStream_t stream) {
+  return fp8_linear_impl(in_codes, w_codes, out, M, N, K, output_scale, mode, stream);
+}
+
+Status fp8_linear(const uint8_t *in_codes, const uint8_t *w_codes, uint16_t *out,
+                  size_t M, size_t N, size_t K, float output_scale,
+                  Fp8Mode mode, hipStream_t stream) {
+  return fp8_linear_impl(in_codes, w_codes, out, M, N, K, output_scale, mode, stream);
 }
 
 }  // namespace evo::hip

@@ -13,11 +13,16 @@
 // product carries ~16 significant bits of the activation (relative error
 // ~2^-17) for twice the MFMA work; without lo (profile hip-bf16) one pass.
 //
-// Tiling for CDNA4: 512 threads = 8 waves as 4 (M) x 2 (N); block tile
-// 256 x 256, K step 32; each wave owns 64 x 128 = 2 x 4 MFMA 32x32x16 tiles
-// (128 F32 accumulators per lane). Operands are staged through LDS with
-// 16-byte loads into rows padded to 40 BF16 (80 B), double-buffered so one
-// barrier per K step separates the prefetch of step k+1 from the MFMAs of k.
+// Tiling for CDNA4: 256 threads = 4 waves as 2 (M) x 2 (N); block tile
+// 256 x 256, K step 32; each wave owns 128 x 128 = 4 x 4 MFMA 32x32x16 tiles
+// (256 F32 accumulators per lane, held in AGPRs at one wave per SIMD). The
+// large wave tile keeps LDS traffic at 12 KB per 32 MFMAs per wave, well
+// under the CU's LDS bandwidth (a 64 x 128 wave tile needs twice that and
+// saturates it). Operands are staged through LDS with 16-byte loads into
+// rows padded to 40 BF16 (80 B), double-buffered so one barrier per K step
+// separates the prefetch of step k+1 from the MFMAs of step k; within a K
+// step the hi-plane sweep and the lo-plane sweep each issue 16 independent
+// MFMAs.
 // Tiles are renumbered so that each of the 8 XCDs (own L2) receives a
 // contiguous band of the tile grid, walked in groups of 8 tile-rows.
 #include "common.hpp"
@@ -29,7 +34,7 @@ namespace {
 constexpr int kBM = 256;
 constexpr int kBN = 256;
 constexpr int kBK = 32;
-constexpr int kThreads = 512;
+constexpr int kThreads = 256;
 constexpr int kStride = kBK + 8;  // BF16 per LDS row
 constexpr int kXcds = 8;
 constexpr int kGroupM = 8;
@@ -44,6 +49,52 @@ struct Epilogue {
 
 __device__ inline float gelu_erf(const float x) {
   return 0.5F * x * (1.0F + erff(x * 0.7071067811865475244F));
+}
+
+// Epilogue of one 32x32 accumulator tile: element e sits at row
+// row0 + (e/4)*8 + e%4 (row0 already includes the lane-half offset) and
+// column col of the output.
+__device__ __forceinline__ void store_tile(const f32x16 &tile, int row0, int col, int M,
+                                           int N, int ldc, const Epilogue &epi, float *C) {
+  if (col >= N)
+    return;
+  const float bias = (epi.mode == kGemmBias || epi.mode == kGemmBiasResidual)
+                         ? bf16_to_f32(epi.bias[col]) : 0.0F;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int row = row0 + (e >> 2) * 8 + (e & 3);
+    if (row < M) {
+      const size_t index = static_cast<size_t>(row) * ldc + col;
+      float value = tile[e];
+      if (epi.mode == kGemmBias || epi.mode == kGemmBiasResidual)
+        value = value + bias;
+      if (epi.mode == kGemmResidual || epi.mode == kGemmBiasResidual)
+        value = value + epi.residual[index];
+      C[index] = value;
+    }
+  }
+}
+
+// Gated epilogue: `first` holds l1 outputs and `second` the matching l2
+// outputs of the same 32 gated columns; writes act(first) * second as planes.
+__device__ __forceinline__ void store_gated(const f32x16 &first, const f32x16 &second,
+                                            int row0, int col, int M, int ldc,
+                                            const Epilogue &epi, uint16_t *c_hi,
+                                            uint16_t *c_lo) {
+  if (col >= epi.gated_width)
+    return;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int row = row0 + (e >> 2) * 8 + (e & 3);
+    if (row < M) {
+      const float value = (epi.gelu ? gelu_erf(first[e]) : first[e]) * second[e];
+      const size_t index = static_cast<size_t>(row) * ldc + col;
+      const uint16_t hi = f32_to_bf16(value);
+      c_hi[index] = hi;
+      if (c_lo != nullptr)
+        c_lo[index] = f32_to_bf16(value - bf16_to_f32(hi));
+    }
+  }
 }
 
 // Maps the hardware block id to a (tile_m, tile_n) pair: consecutive ids go
@@ -65,7 +116,7 @@ __device__ inline void tile_of(int id, int tiles_m, int tiles_n, int *tm, int *t
 }
 
 template <bool kSplit>
-__global__ __launch_bounds__(kThreads) void gemm_kernel(
+__global__ __launch_bounds__(kThreads) void gemm_staged_kernel(
     const uint16_t *__restrict__ a_hi, const uint16_t *__restrict__ a_lo, int lda,
     const uint16_t *__restrict__ W, int M, int N, int K, float *__restrict__ C,
     uint16_t *__restrict__ c_hi, uint16_t *__restrict__ c_lo, int ldc,
@@ -77,7 +128,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wave_m = wave >> 1;  // 0..3
+  const int wave_m = wave >> 1;  // 0..1
   const int wave_n = wave & 1;   // 0..1
   const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
   int tm, tn;
@@ -85,11 +136,12 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(
   const int block_m = tm * kBM, block_n = tn * kBN;
 
   // Loader: each operand tile is 256 rows x 32 BF16 = 1024 x 16 B; thread t
-  // moves chunks t and t + 512: row = c / 4, 8-element segment = c % 4.
-  uint4 ra_hi[2], ra_lo[2], rw[2];
+  // moves chunks t + 256 v (v = 0..3): row = c / 4, 8-element segment c % 4.
+  constexpr int kChunks = 1024 / kThreads;
+  uint4 ra_hi[kChunks], ra_lo[kChunks], rw[kChunks];
   auto fetch = [&](int k0) {
 #pragma unroll
-    for (int v = 0; v < 2; ++v) {
+    for (int v = 0; v < kChunks; ++v) {
       const int c = tid + v * kThreads;
       const int r = c >> 2, k = k0 + (c & 3) * 8;
       const bool ka = k < K;
@@ -105,7 +157,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(
   auto stash = [&](int buffer) {
     uint16_t *stage = lds + buffer * kStage;
 #pragma unroll
-    for (int v = 0; v < 2; ++v) {
+    for (int v = 0; v < kChunks; ++v) {
       const int c = tid + v * kThreads;
       const int r = c >> 2, seg = (c & 3) * 8;
       *reinterpret_cast<uint4 *>(stage + r * kStride + seg) = ra_hi[v];
@@ -115,9 +167,9 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(
     }
   };
 
-  f32x16 acc[2][4];
+  f32x16 acc[4][4];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -139,24 +191,31 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(
 #pragma unroll
     for (int ks = 0; ks < kBK; ks += 16) {
       const int koff = ks + (lane >> 5) * 8;
-      bf16x8 b[4];
+      bf16x8 b[4], ah[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         b[j] = *reinterpret_cast<const bf16x8 *>(
             sw + (wave_n * 128 + j * 32 + (lane & 31)) * kStride + koff);
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int row = wave_m * 64 + i * 32 + (lane & 31);
-        const bf16x8 ah = *reinterpret_cast<const bf16x8 *>(sa_hi + row * kStride + koff);
+      for (int i = 0; i < 4; ++i)
+        ah[i] = *reinterpret_cast<const bf16x8 *>(
+            sa_hi + (wave_m * 128 + i * 32 + (lane & 31)) * kStride + koff);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, b[j], acc[i][j], 0, 0, 0);
-        if (kSplit) {
-          const bf16x8 al = *reinterpret_cast<const bf16x8 *>(sa_lo + row * kStride + koff);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], b[j], acc[i][j], 0, 0, 0);
+      if (kSplit) {
+        bf16x8 al[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          al[i] = *reinterpret_cast<const bf16x8 *>(
+              sa_lo + (wave_m * 128 + i * 32 + (lane & 31)) * kStride + koff);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
           for (int j = 0; j < 4; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, b[j], acc[i][j], 0, 0, 0);
-        }
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], b[j], acc[i][j], 0, 0, 0);
       }
     }
     if (s + 1 < steps)
@@ -165,13 +224,13 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(
   }
 
   // Epilogue. Accumulator e of tile (i, j): row i*32 + (e/4)*8 + (lane/32)*4
-  // + e%4 and column j*32 + lane%32 of the wave's 64 x 128 sub-tile.
+  // + e%4 and column j*32 + lane%32 of the wave's 128 x 128 sub-tile.
   const int wave_col = block_n + wave_n * 128;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < 4; ++i) {
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const int row = block_m + wave_m * 64 + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+      const int row = block_m + wave_m * 128 + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
       if (row >= M)
         continue;
       if (epi.mode == kGemmGated) {
@@ -206,6 +265,176 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(
         C[index] = value;
       }
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Main kernel: operands move global -> LDS by DMA (global_load_lds_dwordx4),
+// so no VGPRs stage them. LDS plane layout: 256 rows x four 16-byte units
+// (32 BF16 of K); unit (row, seg) lives at row*4 + (seg ^ ((row >> 2) & 3)),
+// which spreads the 16-byte fragment reads of 16 consecutive rows over all
+// 64 banks without padding. One DMA instruction writes 64 consecutive units
+// (16 rows), so lane l of instruction t loads row 16t + l/4, segment
+// (l%4) ^ ((row >> 2) & 3). Three stages rotate: while step s is multiplied,
+// steps s+1 and s+2 are in flight. Rows beyond M or N read a clamped valid
+// row; their results are never stored. Requires K % 32 == 0.
+constexpr int kStages = 3;
+constexpr int kPlane = kBM * kBK;  // BF16 per plane (no padding)
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// One 16-byte-per-lane global -> LDS DMA: lane l's 16 bytes land at LDS byte
+// address lds + 16 l (lds must be wave-uniform). Issued through inline asm so
+// the compiler does not serialise it with the LDS reads of other stage
+// buffers (it cannot tell them apart and would wait for every DMA); the
+// kernel accounts for completion itself with s_waitcnt vmcnt. M0 is written
+// here and is not live across this asm in the kernels that use it.
+__device__ inline void dma16(const void *global, const uint16_t *lds) {
+  const unsigned address = __builtin_amdgcn_readfirstlane(
+      static_cast<unsigned>(reinterpret_cast<size_t>((const lds_void *)(lds))));
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(global), "s"(address) : "memory");
+}
+
+__device__ inline int swizzled_unit(int row, int seg) {
+  return row * 4 + (seg ^ ((row >> 2) & 3));
+}
+
+template <bool kSplit>
+__global__ __launch_bounds__(kThreads) void gemm_kernel(
+    const uint16_t *__restrict__ a_hi, const uint16_t *__restrict__ a_lo, int lda,
+    const uint16_t *__restrict__ W, int M, int N, int K, float *__restrict__ C,
+    uint16_t *__restrict__ c_hi, uint16_t *__restrict__ c_lo, int ldc,
+    const Epilogue epi) {
+  constexpr int kPlanes = kSplit ? 3 : 2;  // A hi, (A lo), W
+  constexpr int kStage = kPlanes * kPlane;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[kStages * kStage];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wave_m = wave >> 1;  // 0..1
+  const int wave_n = wave & 1;   // 0..1
+  const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
+  int tm, tn;
+  tile_of(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
+  const int block_m = tm * kBM, block_n = tn * kBN;
+
+  // This lane's four DMA rows (instructions t = wave*4 + i) and segments.
+  const uint16_t *src_a_hi[4], *src_a_lo[4], *src_w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int t = wave * 4 + i;
+    const int r = 16 * t + (lane >> 2);
+    const int seg = (lane & 3) ^ ((r >> 2) & 3);
+    const int ar = min(block_m + r, M - 1), wr = min(block_n + r, N - 1);
+    src_a_hi[i] = a_hi + static_cast<size_t>(ar) * lda + seg * 8;
+    src_a_lo[i] = kSplit ? a_lo + static_cast<size_t>(ar) * lda + seg * 8 : nullptr;
+    src_w[i] = W + static_cast<size_t>(wr) * K + seg * 8;
+  }
+  auto issue = [&](int step) {
+    uint16_t *stage = lds + (step % kStages) * kStage;
+    const int k0 = step * kBK;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int unit0 = (wave * 4 + i) * 64;  // first unit of this instruction
+      dma16(src_a_hi[i] + k0, stage + unit0 * 8);
+      if (kSplit)
+        dma16(src_a_lo[i] + k0, stage + kPlane + unit0 * 8);
+      dma16(src_w[i] + k0, stage + (kPlanes - 1) * kPlane + unit0 * 8);
+    }
+  };
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        acc[i][j][e] = 0.0F;
+
+  const int steps = K / kBK;
+  issue(0);
+  if (steps > 1)
+    issue(1);
+  for (int s = 0; s < steps; ++s) {
+    // Wait for this wave's DMA of step s (the step s+1 batch may stay in
+    // flight), then for every wave's.
+    if (s + 1 < steps) {
+      if (kSplit)
+        asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    __syncthreads();
+    if (s + 2 < steps)
+      issue(s + 2);  // into the buffer of step s-1, which every wave has left
+    const uint16_t *stage = lds + (s % kStages) * kStage;
+    const uint16_t *sa_hi = stage;
+    const uint16_t *sa_lo = stage + kPlane;
+    const uint16_t *sw = stage + (kPlanes - 1) * kPlane;
+    // Fragments of both 16-wide K halves; the reads of half 1 are issued
+    // before the MFMAs of half 0 so their latency hides behind them.
+    bf16x8 b[2][4], ah[2][4], al[2][4];
+    auto read = [&](int ks) {
+      const int seg = 2 * ks + (lane >> 5);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        b[ks][j] = *reinterpret_cast<const bf16x8 *>(
+            sw + swizzled_unit(wave_n * 128 + j * 32 + (lane & 31), seg) * 8);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        ah[ks][i] = *reinterpret_cast<const bf16x8 *>(
+            sa_hi + swizzled_unit(wave_m * 128 + i * 32 + (lane & 31), seg) * 8);
+      if (kSplit) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          al[ks][i] = *reinterpret_cast<const bf16x8 *>(
+              sa_lo + swizzled_unit(wave_m * 128 + i * 32 + (lane & 31), seg) * 8);
+      }
+    };
+    auto multiply = [&](int ks) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[ks][i], b[ks][j], acc[i][j], 0, 0, 0);
+      if (kSplit) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[ks][i], b[ks][j], acc[i][j], 0, 0, 0);
+      }
+    };
+    read(0);
+    __builtin_amdgcn_sched_barrier(0);
+    read(1);
+    __builtin_amdgcn_sched_barrier(0);
+    multiply(0);
+    __builtin_amdgcn_sched_barrier(0);
+    multiply(1);
+  }
+
+  const int wave_col = block_n + wave_n * 128;
+  const int wave_row = block_m + wave_m * 128 + (lane >> 5) * 4;
+  if (epi.mode == kGemmGated) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int pair = 0; pair < 2; ++pair)
+        store_gated(acc[i][2 * pair], acc[i][2 * pair + 1], wave_row + i * 32,
+                    wave_col / 2 + pair * 32 + (lane & 31), M, ldc, epi, c_hi, c_lo);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        store_tile(acc[i][j], wave_row + i * 32, wave_col + j * 32 + (lane & 31), M, N, ldc,
+                   epi, C);
   }
 }
 
@@ -258,17 +487,24 @@ Status gemm_bf16w(const Activation &a, const uint16_t *W, const GemmOutput &out,
   if (tiles > (1U << 31))
     return {ErrorCode::kInvalidArgument, "gemm_bf16w: grid too large"};
   const dim3 grid(static_cast<unsigned>(tiles));
+  const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
+  const int lda = static_cast<int>(a.ld), ldc = static_cast<int>(out.ld);
+  if (K % kBK == 0) {
+    if (split)
+      hipLaunchKernelGGL(gemm_kernel<true>, grid, dim3(kThreads), 0, stream, a.hi, a.lo, lda,
+                         W, m, n, k, out.f32, out.hi, out.lo, ldc, epi);
+    else
+      hipLaunchKernelGGL(gemm_kernel<false>, grid, dim3(kThreads), 0, stream, a.hi, a.lo, lda,
+                         W, m, n, k, out.f32, out.hi, out.lo, ldc, epi);
+    return launch_status("gemm_kernel");
+  }
   if (split)
-    hipLaunchKernelGGL(gemm_kernel<true>, grid, dim3(kThreads), 0, stream, a.hi, a.lo,
-                       static_cast<int>(a.ld), W, static_cast<int>(M), static_cast<int>(N),
-                       static_cast<int>(K), out.f32, out.hi, out.lo,
-                       static_cast<int>(out.ld), epi);
+    hipLaunchKernelGGL(gemm_staged_kernel<true>, grid, dim3(kThreads), 0, stream, a.hi, a.lo,
+                       lda, W, m, n, k, out.f32, out.hi, out.lo, ldc, epi);
   else
-    hipLaunchKernelGGL(gemm_kernel<false>, grid, dim3(kThreads), 0, stream, a.hi, a.lo,
-                       static_cast<int>(a.ld), W, static_cast<int>(M), static_cast<int>(N),
-                       static_cast<int>(K), out.f32, out.hi, out.lo,
-                       static_cast<int>(out.ld), epi);
-  return launch_status("gemm_kernel");
+    hipLaunchKernelGGL(gemm_staged_kernel<false>, grid, dim3(kThreads), 0, stream, a.hi, a.lo,
+                       lda, W, m, n, k, out.f32, out.hi, out.lo, ldc, epi);
+  return launch_status("gemm_staged_kernel");
 }
 
 }  // namespace evo::hip

@@ -25,7 +25,7 @@ namespace evo::hip {
 namespace {
 
 constexpr int kChannels = 64;    // channels per block (one wave)
-constexpr int kChunk = 128;      // HCL rows per chunk
+constexpr int kChunk = 64;       // HCL rows per chunk
 constexpr int kMaxState = 16;
 constexpr int kMaxShort = 8;
 
@@ -73,8 +73,73 @@ __device__ inline void load_short_taps(const uint16_t *filter, int k, size_t c,
       taps[s][j] = j < k ? bf16_to_f32(filter[(3 * c + s) * k + j]) : 0.0F;
 }
 
-// ---- HCL phase 1: final local state of every chunk from a zero start.
+// ---- HCL row streaming. Each thread keeps the last kWin rows of its three
+// projection columns in registers, so every row of P is loaded once; rows
+// are fetched kBatch at a time to keep that many loads in flight. The short
+// FIR taps are stored right-aligned in a kWin-wide window (zeros in front),
+// which keeps the oldest-first accumulation order of the reference.
+constexpr int kBatch = 8;
+
+template <int kWin>
+__device__ inline void load_window_taps(const uint16_t *filter, int k, size_t c,
+                                        float (&taps)[3][kWin]) {
+#pragma unroll
+  for (int s = 0; s < 3; ++s)
+#pragma unroll
+    for (int i = 0; i < kWin; ++i) {
+      const int j = i - (kWin - k);  // tap index of window slot i
+      taps[s][i] = j >= 0 ? bf16_to_f32(filter[(3 * c + s) * k + j]) : 0.0F;
+    }
+}
+
+template <typename T, int kWin>
+struct RowStream {
+  float win[3][kWin];  // win[s][kWin-1] = current row
+  float taps[3][kWin];
+
+  // Fills the window with the rows before t0 (history rows when t0 is 0).
+  __device__ void prime(const T *P, const float *short_history, int k,
+                        size_t cols3, long t0, size_t c) {
+#pragma unroll
+    for (int i = 0; i < kWin - 1; ++i) {
+      const long t = t0 - (kWin - 1) + i;
+      // Rows older than the filter reach only meet zero taps.
+      const bool used = t >= t0 - (k - 1);
+#pragma unroll
+      for (int s = 0; s < 3; ++s)
+        win[s][i + 1] = used ? p_at(P, short_history, cols3, k - 1, t, 3 * c + s) : 0.0F;
+    }
+  }
+  // Shifts in one row and returns the FIR outputs of its three columns.
+  __device__ void push(const float (&row)[3], float (&fir)[3]) {
+#pragma unroll
+    for (int s = 0; s < 3; ++s) {
+#pragma unroll
+      for (int i = 0; i < kWin - 1; ++i)
+        win[s][i] = win[s][i + 1];
+      win[s][kWin - 1] = row[s];
+      float total = 0.0F;
+#pragma unroll
+      for (int i = 0; i < kWin; ++i)
+        total += win[s][i] * taps[s][i];
+      fir[s] = total;
+    }
+  }
+};
+
+// Loads rows [t, t + kBatch) (clipped to t1) of the channel's 3 columns.
 template <typename T>
+__device__ inline void load_batch(const T *P, size_t cols3, size_t t, size_t t1,
+                                  size_t c, float (&rows)[kBatch][3]) {
+#pragma unroll
+  for (int b = 0; b < kBatch; ++b)
+#pragma unroll
+    for (int s = 0; s < 3; ++s)
+      rows[b][s] = t + b < t1 ? load_act(P, (t + b) * cols3 + 3 * c + s) : 0.0F;
+}
+
+// ---- HCL phase 1: final local state of every chunk from a zero start.
+template <typename T, int kWin>
 __global__ __launch_bounds__(kChannels) void hcl_chunk_state_kernel(
     const T *__restrict__ P, const float *__restrict__ short_history,
     const uint16_t *__restrict__ short_filter, int short_len, size_t L,
@@ -84,25 +149,31 @@ __global__ __launch_bounds__(kChannels) void hcl_chunk_state_kernel(
     return;
   const size_t g = blockIdx.y;
   const size_t t0 = g * kChunk, t1 = min(L, t0 + kChunk);
-  float taps[3][kMaxShort];
-  load_short_taps(short_filter, short_len, c, taps);
+  const size_t cols3 = 3 * W;
+  RowStream<T, kWin> stream;
+  load_window_taps(short_filter, short_len, c, stream.taps);
+  stream.prime(P, short_history, short_len, cols3, static_cast<long>(t0), c);
   float p[kMaxState], s[kMaxState];
 #pragma unroll
   for (int m = 0; m < kMaxState; ++m) {
     p[m] = m < S ? poles[c * S + m] : 0.0F;
     s[m] = 0.0F;
   }
-  const size_t cols3 = 3 * W;
-  for (size_t t = t0; t < t1; ++t) {
-    const float x1 = short_fir(P, short_history, taps[1], short_len, cols3, (long)t, 3 * c + 1);
-    const float v = short_fir(P, short_history, taps[2], short_len, cols3, (long)t, 3 * c + 2);
-    const float u = x1 * v;
+  for (size_t t = t0; t < t1; t += kBatch) {
+    float rows[kBatch][3];
+    load_batch(P, cols3, t, t1, c, rows);
 #pragma unroll
-    for (int m = 0; m < kMaxState; ++m)
-      s[m] = p[m] * s[m] + u;
+    for (int b = 0; b < kBatch; ++b) {
+      if (t + b >= t1)
+        break;
+      float fir[3];
+      stream.push(rows[b], fir);
+      const float u = fir[1] * fir[2];
+#pragma unroll
+      for (int m = 0; m < kMaxState; ++m)
+        s[m] = p[m] * s[m] + u;
+    }
   }
-  const size_t G = gridDim.y;
-  (void)G;
 #pragma unroll
   for (int m = 0; m < kMaxState; ++m)
     if (m < S)
@@ -142,7 +213,7 @@ __global__ void hcl_carry_kernel(float *__restrict__ chunk_state, size_t G,
 }
 
 // ---- HCL phase 3: rescan each chunk from its true start state.
-template <typename T, typename O>
+template <typename T, typename O, int kWin>
 __global__ __launch_bounds__(kChannels) void hcl_output_kernel(
     const T *__restrict__ P, const float *__restrict__ short_history,
     const uint16_t *__restrict__ short_filter, int short_len, size_t L,
@@ -154,8 +225,10 @@ __global__ __launch_bounds__(kChannels) void hcl_output_kernel(
     return;
   const size_t g = blockIdx.y;
   const size_t t0 = g * kChunk, t1 = min(L, t0 + kChunk);
-  float taps[3][kMaxShort];
-  load_short_taps(short_filter, short_len, c, taps);
+  const size_t cols3 = 3 * W;
+  RowStream<T, kWin> stream;
+  load_window_taps(short_filter, short_len, c, stream.taps);
+  stream.prime(P, short_history, short_len, cols3, static_cast<long>(t0), c);
   float p[kMaxState], r[kMaxState], s[kMaxState];
 #pragma unroll
   for (int m = 0; m < kMaxState; ++m) {
@@ -164,17 +237,24 @@ __global__ __launch_bounds__(kChannels) void hcl_output_kernel(
     s[m] = m < S ? chunk_state[(g * S + m) * W + c] : 0.0F;
   }
   const float d = direct[c];
-  const size_t cols3 = 3 * W;
-  for (size_t t = t0; t < t1; ++t) {
-    float x2, u;
-    gates(P, short_history, taps, short_len, cols3, (long)t, c, &x2, &u);
-    float modal = 0.0F;
+  for (size_t t = t0; t < t1; t += kBatch) {
+    float rows[kBatch][3];
+    load_batch(P, cols3, t, t1, c, rows);
 #pragma unroll
-    for (int m = 0; m < kMaxState; ++m) {
-      s[m] = p[m] * s[m] + u;
-      modal += r[m] * s[m];
+    for (int b = 0; b < kBatch; ++b) {
+      if (t + b >= t1)
+        break;
+      float fir[3];
+      stream.push(rows[b], fir);
+      const float x2 = fir[0], u = fir[1] * fir[2];
+      float modal = 0.0F;
+#pragma unroll
+      for (int m = 0; m < kMaxState; ++m) {
+        s[m] = p[m] * s[m] + u;
+        modal += r[m] * s[m];
+      }
+      put(out, (t + b) * W + c, x2 * (modal + d * u));
     }
-    put(out, t * W + c, x2 * (modal + d * u));
   }
 }
 
@@ -291,6 +371,24 @@ __global__ void short_history_kernel(const T *__restrict__ P, size_t L,
 
 size_t hcl_chunks(size_t length) { return (length + kChunk - 1) / kChunk; }
 
+template <typename T, typename O, int kWin>
+Status launch_hcl(const T *projection, const float *short_history, const HyenaWeights &wt,
+                  int short_len, size_t length, size_t width, int S, size_t G,
+                  float *chunk_state, float *modal_state, O out, hipStream_t stream) {
+  const dim3 grid(ceil_div(width, kChannels), static_cast<unsigned>(G));
+  hipLaunchKernelGGL((hcl_chunk_state_kernel<T, kWin>), grid, dim3(kChannels), 0, stream,
+                     projection, short_history, wt.short_filter, short_len, length, width,
+                     wt.poles, S, chunk_state);
+  EVO_TRY(launch_status("hcl_chunk_state_kernel"));
+  hipLaunchKernelGGL(hcl_carry_kernel, dim3(ceil_div(width * S, 256)), dim3(256), 0, stream,
+                     chunk_state, G, length, width, S, wt.poles, modal_state);
+  EVO_TRY(launch_status("hcl_carry_kernel"));
+  hipLaunchKernelGGL((hcl_output_kernel<T, O, kWin>), grid, dim3(kChannels), 0, stream,
+                     projection, short_history, wt.short_filter, short_len, length, width,
+                     wt.poles, wt.residues, wt.direct, S, chunk_state, out);
+  return launch_status("hcl_output_kernel");
+}
+
 }  // namespace
 
 size_t hyena_workspace_bytes(int kind, size_t length, size_t width,
@@ -324,19 +422,13 @@ Status hyena_forward(int kind, const T *projection, size_t length,
       return {ErrorCode::kInvalidArgument, "hyena_forward: sequence too long for one call"};
     float *chunk_state = static_cast<float *>(workspace);
     const int S = static_cast<int>(wt.state);
-    const dim3 grid(channel_blocks.x, static_cast<unsigned>(G));
-    hipLaunchKernelGGL(hcl_chunk_state_kernel<T>, grid, dim3(kChannels), 0, stream,
-                       projection, short_history, wt.short_filter, short_len,
-                       length, width, wt.poles, S, chunk_state);
-    EVO_TRY(launch_status("hcl_chunk_state_kernel"));
-    hipLaunchKernelGGL(hcl_carry_kernel, dim3(ceil_div(width * wt.state, 256)), dim3(256),
-                       0, stream, chunk_state, G, length, width, S, wt.poles, modal_state);
-    EVO_TRY(launch_status("hcl_carry_kernel"));
-    hipLaunchKernelGGL((hcl_output_kernel<T, O>), grid, dim3(kChannels), 0, stream,
-                       projection, short_history, wt.short_filter, short_len,
-                       length, width, wt.poles, wt.residues, wt.direct, S,
-                       chunk_state, out);
-    EVO_TRY(launch_status("hcl_output_kernel"));
+    if (short_len <= 4) {
+      EVO_TRY((launch_hcl<T, O, 4>(projection, short_history, wt, short_len, length, width,
+                                   S, G, chunk_state, modal_state, out, stream)));
+    } else {
+      EVO_TRY((launch_hcl<T, O, kMaxShort>(projection, short_history, wt, short_len, length,
+                                           width, S, G, chunk_state, modal_state, out, stream)));
+    }
   } else if (kind == kHyenaHcs || kind == kHyenaHcm) {
     if (wt.inner_filter == nullptr || wt.groups == 0 || width % wt.groups != 0 ||
         wt.inner_len < 1 || wt.inner_len > 128 ||
@@ -395,6 +487,10 @@ template Status hyena_forward<uint16_t, uint16_t *>(int, const uint16_t *, size_
                                                     const HyenaWeights &, float *, float *,
                                                     float *, void *, size_t, uint16_t *,
                                                     hipStream_t);
+template Status hyena_forward<uint16_t, SplitOut>(int, const uint16_t *, size_t, size_t,
+                                                  const HyenaWeights &, float *, float *,
+                                                  float *, void *, size_t, SplitOut,
+                                                  hipStream_t);
 template Status hyena_forward<float, SplitOut>(int, const float *, size_t, size_t,
                                                const HyenaWeights &, float *, float *,
                                                float *, void *, size_t, SplitOut,

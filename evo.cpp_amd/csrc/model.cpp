@@ -420,8 +420,11 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
       EVO_TRY(e4m3_quantize_bf16(normed.hi, rows * w, L.fp8_input_scale,
                                  codes_.as<uint8_t>(), stream_));
       const Fp8Mode mode = (w % 128 != 0) ? kFp8Exact : options_.fp8_mode;
-      EVO_TRY(fp8_linear(codes_.as<uint8_t>(), L.projection.as<uint8_t>(), projected, rows,
-                         3 * w, w, L.fp8_output_scale, mode, stream_));
+      // The product is BF16 by definition: store it as BF16 and halve the
+      // projection's HBM traffic for the Hyena kernels that read it.
+      EVO_TRY(fp8_linear(codes_.as<uint8_t>(), L.projection.as<uint8_t>(),
+                         projected_.as<uint16_t>(), rows, 3 * w, w, L.fp8_output_scale,
+                         mode, stream_));
     } else {
       EVO_TRY(gemm_bf16w(normed, L.projection.as<uint16_t>(),
                          GemmOutput{projected, nullptr, nullptr, 3 * w}, rows, 3 * w, w,
@@ -450,12 +453,20 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
       hw.state = c.state;
       const int kind = L.type == Mixer::kHcs ? kHyenaHcs
                        : L.type == Mixer::kHcm ? kHyenaHcm : kHyenaHcl;
-      EVO_TRY((hyena_forward<float, SplitOut>(kind, projected, rows, w, hw,
-                                              k.short_history.as<float>(),
-                                              k.inner_history.as<float>(),
-                                              k.modal_state.as<float>(),
-                                              workspace_.as<void>(), workspace_.bytes(),
-                                              mixed_out, stream_)));
+      if (L.fp8)
+        EVO_TRY((hyena_forward<uint16_t, SplitOut>(kind, projected_.as<uint16_t>(), rows, w,
+                                                   hw, k.short_history.as<float>(),
+                                                   k.inner_history.as<float>(),
+                                                   k.modal_state.as<float>(),
+                                                   workspace_.as<void>(), workspace_.bytes(),
+                                                   mixed_out, stream_)));
+      else
+        EVO_TRY((hyena_forward<float, SplitOut>(kind, projected, rows, w, hw,
+                                                k.short_history.as<float>(),
+                                                k.inner_history.as<float>(),
+                                                k.modal_state.as<float>(),
+                                                workspace_.as<void>(), workspace_.bytes(),
+                                                mixed_out, stream_)));
     }
     // residual = (mixed . Wout^T + bias) + hidden   (`src/cpu/model.cpp:641-645`)
     EVO_TRY(gemm_bf16w(mixed, L.out_weight.as<uint16_t>(),

@@ -68,6 +68,11 @@ enum Fp8Mode : int {
 Status fp8_linear(const uint8_t *in_codes, const uint8_t *w_codes, float *out,
                   size_t M, size_t N, size_t K, float output_scale,
                   Fp8Mode mode, hipStream_t stream);
+// Same product with the BF16 result stored as BF16 (exact: the value already
+// is a BF16 number).
+Status fp8_linear(const uint8_t *in_codes, const uint8_t *w_codes, uint16_t *out,
+                  size_t M, size_t N, size_t K, float output_scale,
+                  Fp8Mode mode, hipStream_t stream);
 
 // ---- Elementwise / normalisation (elementwise.hip).
 Status embed_tokens(const uint32_t *tokens, size_t rows, const uint16_t *table,
