@@ -568,20 +568,29 @@ evo_status evo_hip_hyena_forward(evo_hip_hyena_kind kind, evo_hip_dtype dtype,
     evo::hip::HyenaWeights w{short_filter, short_len, inner_filter, groups, inner_len,
                              direct, poles, residues, state_size};
     const auto s = static_cast<hipStream_t>(stream);
+    const bool planar = (static_cast<int>(dtype) & EVO_HIP_PLANAR) != 0;
+    dtype = static_cast<evo_hip_dtype>(static_cast<int>(dtype) & ~EVO_HIP_PLANAR);
     if (dtype == EVO_HIP_F32)
       return publish(evo::hip::hyena_forward<float, float *>(
-          kind, static_cast<const float *>(projection), length, width, w, short_history,
+          kind, static_cast<const float *>(projection), length, width, planar, w, short_history,
           inner_history, modal_state, workspace, workspace_bytes,
           static_cast<float *>(output), s));
     if (dtype == EVO_HIP_BF16)
       return publish(evo::hip::hyena_forward<uint16_t, uint16_t *>(
-          kind, static_cast<const uint16_t *>(projection), length, width, w, short_history,
+          kind, static_cast<const uint16_t *>(projection), length, width, planar, w, short_history,
           inner_history, modal_state, workspace, workspace_bytes,
           static_cast<uint16_t *>(output), s));
     if (dtype == EVO_HIP_SPLIT) {
       auto *hi = static_cast<uint16_t *>(output);
       return publish(evo::hip::hyena_forward<float, evo::hip::SplitOut>(
-          kind, static_cast<const float *>(projection), length, width, w, short_history,
+          kind, static_cast<const float *>(projection), length, width, planar, w, short_history,
+          inner_history, modal_state, workspace, workspace_bytes,
+          evo::hip::SplitOut{hi, hi == nullptr ? nullptr : hi + length * width}, s));
+    }
+    if (dtype == EVO_HIP_BF16_SPLIT) {
+      auto *hi = static_cast<uint16_t *>(output);
+      return publish(evo::hip::hyena_forward<uint16_t, evo::hip::SplitOut>(
+          kind, static_cast<const uint16_t *>(projection), length, width, planar, w, short_history,
           inner_history, modal_state, workspace, workspace_bytes,
           evo::hip::SplitOut{hi, hi == nullptr ? nullptr : hi + length * width}, s));
     }

@@ -24,6 +24,10 @@ __host__ __device__ inline float bf16_to_f32(const uint16_t bits) {
 }
 
 __host__ __device__ inline uint16_t f32_to_bf16(const float value) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  // gfx950 converts in hardware (v_cvt_pk_bf16_f32, round to nearest even).
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(value));
+#endif
   const uint32_t bits = __builtin_bit_cast(uint32_t, value);
   if ((bits & 0x7fffffffU) > 0x7f800000U)
     return static_cast<uint16_t>((bits >> 16U) | 0x40U);

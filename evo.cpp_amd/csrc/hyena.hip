@@ -29,6 +29,15 @@ constexpr int kChunk = 64;       // HCL rows per chunk
 constexpr int kMaxState = 16;
 constexpr int kMaxShort = 8;
 
+// Column of projection stream s (0 = x2, 1 = x1, 2 = v) of channel c. The
+// reference layout interleaves the streams (3c + s); the planar layout keeps
+// each stream contiguous (s * W + c), so a wave's 64 channels of one stream
+// are one 128-byte (BF16) segment. `planar` is W for the planar layout and 0
+// for the interleaved one. The short FIR history uses the same columns.
+__device__ inline size_t pcol(size_t c, int s, size_t planar) {
+  return planar != 0 ? static_cast<size_t>(s) * planar + c : 3 * c + static_cast<size_t>(s);
+}
+
 // Reads column `col` of P at row t (t may be negative: the short history holds
 // rows -(short_len-1)..-1, oldest first).
 template <typename T>
@@ -58,11 +67,11 @@ __device__ inline float short_fir(const T *P, const float *short_history,
 template <typename T>
 __device__ inline void gates(const T *P, const float *short_history,
                              const float (&taps)[3][kMaxShort], int k,
-                             size_t cols3, long t, size_t c, float *x2,
-                             float *u) {
-  *x2 = short_fir(P, short_history, taps[0], k, cols3, t, 3 * c);
-  const float x1 = short_fir(P, short_history, taps[1], k, cols3, t, 3 * c + 1);
-  const float v = short_fir(P, short_history, taps[2], k, cols3, t, 3 * c + 2);
+                             size_t cols3, size_t planar, long t, size_t c,
+                             float *x2, float *u) {
+  *x2 = short_fir(P, short_history, taps[0], k, cols3, t, pcol(c, 0, planar));
+  const float x1 = short_fir(P, short_history, taps[1], k, cols3, t, pcol(c, 1, planar));
+  const float v = short_fir(P, short_history, taps[2], k, cols3, t, pcol(c, 2, planar));
   *u = x1 * v;
 }
 
@@ -99,7 +108,7 @@ struct RowStream {
 
   // Fills the window with the rows before t0 (history rows when t0 is 0).
   __device__ void prime(const T *P, const float *short_history, int k,
-                        size_t cols3, long t0, size_t c) {
+                        size_t cols3, size_t planar, long t0, size_t c) {
 #pragma unroll
     for (int i = 0; i < kWin - 1; ++i) {
       const long t = t0 - (kWin - 1) + i;
@@ -107,7 +116,7 @@ struct RowStream {
       const bool used = t >= t0 - (k - 1);
 #pragma unroll
       for (int s = 0; s < 3; ++s)
-        win[s][i + 1] = used ? p_at(P, short_history, cols3, k - 1, t, 3 * c + s) : 0.0F;
+        win[s][i + 1] = used ? p_at(P, short_history, cols3, k - 1, t, pcol(c, s, planar)) : 0.0F;
     }
   }
   // Shifts in one row and returns the FIR outputs of its three columns.
@@ -127,15 +136,15 @@ struct RowStream {
   }
 };
 
-// Loads rows [t, t + kBatch) (clipped to t1) of the channel's 3 columns.
-template <typename T>
-__device__ inline void load_batch(const T *P, size_t cols3, size_t t, size_t t1,
-                                  size_t c, float (&rows)[kBatch][3]) {
+// Loads rows [t, t + kB) (clipped to t1) of the channel's 3 columns.
+template <typename T, int kB>
+__device__ inline void load_batch(const T *P, size_t cols3, size_t planar, size_t t,
+                                  size_t t1, size_t c, float (&rows)[kB][3]) {
 #pragma unroll
-  for (int b = 0; b < kBatch; ++b)
+  for (int b = 0; b < kB; ++b)
 #pragma unroll
     for (int s = 0; s < 3; ++s)
-      rows[b][s] = t + b < t1 ? load_act(P, (t + b) * cols3 + 3 * c + s) : 0.0F;
+      rows[b][s] = t + b < t1 ? load_act(P, (t + b) * cols3 + pcol(c, s, planar)) : 0.0F;
 }
 
 // ---- HCL phase 1: final local state of every chunk from a zero start.
@@ -143,7 +152,7 @@ template <typename T, int kWin>
 __global__ __launch_bounds__(kChannels) void hcl_chunk_state_kernel(
     const T *__restrict__ P, const float *__restrict__ short_history,
     const uint16_t *__restrict__ short_filter, int short_len, size_t L,
-    size_t W, const float *__restrict__ poles, int S, float *__restrict__ chunk_state) {
+    size_t W, size_t planar, const float *__restrict__ poles, int S, float *__restrict__ chunk_state) {
   const size_t c = blockIdx.x * static_cast<size_t>(kChannels) + threadIdx.x;
   if (c >= W)
     return;
@@ -152,7 +161,7 @@ __global__ __launch_bounds__(kChannels) void hcl_chunk_state_kernel(
   const size_t cols3 = 3 * W;
   RowStream<T, kWin> stream;
   load_window_taps(short_filter, short_len, c, stream.taps);
-  stream.prime(P, short_history, short_len, cols3, static_cast<long>(t0), c);
+  stream.prime(P, short_history, short_len, cols3, planar, static_cast<long>(t0), c);
   float p[kMaxState], s[kMaxState];
 #pragma unroll
   for (int m = 0; m < kMaxState; ++m) {
@@ -161,7 +170,7 @@ __global__ __launch_bounds__(kChannels) void hcl_chunk_state_kernel(
   }
   for (size_t t = t0; t < t1; t += kBatch) {
     float rows[kBatch][3];
-    load_batch(P, cols3, t, t1, c, rows);
+    load_batch(P, cols3, planar, t, t1, c, rows);
 #pragma unroll
     for (int b = 0; b < kBatch; ++b) {
       if (t + b >= t1)
@@ -217,7 +226,7 @@ template <typename T, typename O, int kWin>
 __global__ __launch_bounds__(kChannels) void hcl_output_kernel(
     const T *__restrict__ P, const float *__restrict__ short_history,
     const uint16_t *__restrict__ short_filter, int short_len, size_t L,
-    size_t W, const float *__restrict__ poles,
+    size_t W, size_t planar, const float *__restrict__ poles,
     const float *__restrict__ residues, const float *__restrict__ direct,
     int S, const float *__restrict__ chunk_state, O out) {
   const size_t c = blockIdx.x * static_cast<size_t>(kChannels) + threadIdx.x;
@@ -228,7 +237,7 @@ __global__ __launch_bounds__(kChannels) void hcl_output_kernel(
   const size_t cols3 = 3 * W;
   RowStream<T, kWin> stream;
   load_window_taps(short_filter, short_len, c, stream.taps);
-  stream.prime(P, short_history, short_len, cols3, static_cast<long>(t0), c);
+  stream.prime(P, short_history, short_len, cols3, planar, static_cast<long>(t0), c);
   float p[kMaxState], r[kMaxState], s[kMaxState];
 #pragma unroll
   for (int m = 0; m < kMaxState; ++m) {
@@ -239,7 +248,7 @@ __global__ __launch_bounds__(kChannels) void hcl_output_kernel(
   const float d = direct[c];
   for (size_t t = t0; t < t1; t += kBatch) {
     float rows[kBatch][3];
-    load_batch(P, cols3, t, t1, c, rows);
+    load_batch(P, cols3, planar, t, t1, c, rows);
 #pragma unroll
     for (int b = 0; b < kBatch; ++b) {
       if (t + b >= t1)
@@ -270,7 +279,7 @@ __global__ __launch_bounds__(256) void hyena_fir_kernel(
     const uint16_t *__restrict__ short_filter, int short_len,
     const float *__restrict__ inner_history, const float *__restrict__ filter,
     size_t groups, int k, int causal, const float *__restrict__ direct,
-    size_t L, size_t W, O out) {
+    size_t L, size_t W, size_t planar, O out) {
   extern __shared__ float smem[];
   float *u_s = smem;                                  // [(k-1) + kTile][64]
   float *x2_s = smem + (kMaxTaps - 1 + kTile) * 64;   // [kTile][64]
@@ -290,7 +299,7 @@ __global__ __launch_bounds__(256) void hyena_fir_kernel(
     float x2 = 0.0F, u = 0.0F;
     if (valid && t < static_cast<long>(L)) {
       if (t >= 0) {
-        gates(P, short_history, taps, short_len, cols3, t, c, &x2, &u);
+        gates(P, short_history, taps, short_len, cols3, planar, t, c, &x2, &u);
       } else {
         const long h = static_cast<long>(hist) + t;
         u = (inner_history != nullptr && h >= 0) ? inner_history[h * W + c] : 0.0F;
@@ -326,13 +335,242 @@ __global__ __launch_bounds__(256) void hyena_fir_kernel(
   }
 }
 
+// ---- HCS / HCM on MFMA: the grouped FIR of a 16-channel slice as a
+// Toeplitz product. For output rows [r0, r0+16) and window rows
+// i = r0 .. r0+159 (window row i holds u at t0 - (k-1) + i):
+//
+//   Y[r][c] = sum_i T[r][i - r0] * U[i][c],   T[r][j] = h[tap(j - r)]
+//
+// where old = j - r in [0, k) is the distance from the oldest row of the
+// filter span (cross-correlation pairs it with tap `old`, causal convolution
+// with tap k-1-old) and T is 0 elsewhere. T does not depend on r0, so each
+// wave builds its A fragments once. U is staged in LDS as split BF16 planes
+// (u = hi + lo, |lo| <= 2^-9 |u|), transposed to [channel][row] so that one
+// ds_read_b128 yields a B fragment; the taps are split the same way and
+// three passes (h_hi u_hi + h_hi u_lo + h_lo u_hi) keep F32 accuracy. Every
+// channel of a 16-column slice must share one filter group.
+constexpr int kFirTile = 128;    // output rows per block
+constexpr int kFirThreads = 1024; // 16 waves
+
+template <int kMaxTaps>
+struct FirMfmaShape {
+  static constexpr int kSteps = (16 + kMaxTaps - 1 + 31) / 32;  // K=32 steps per row block
+  static constexpr int kSpan = (kFirTile - 16) + 32 * kSteps;   // window rows a read may touch
+  // Row stride (BF16) of a channel: a multiple of 8 (16-byte reads) with an
+  // odd number of 16-byte units, so 8 lanes on 8 channels hit 8 bank groups.
+  static constexpr int kStride = ((kSpan + 7) / 8 % 2 == 1) ? (kSpan + 7) / 8 * 8
+                                                             : (kSpan + 7) / 8 * 8 + 8;
+  static constexpr size_t kLdsBytes =
+      2 * kChannels * kStride * sizeof(uint16_t) + kFirTile * kChannels * sizeof(float);
+};
+
+// Toeplitz A fragments of every filter group: entry ((g * kSteps + q) * 2 +
+// plane) * 64 + lane holds lane's 8 BF16 values of K step q (plane 0 = hi,
+// 1 = lo of the F32 tap).
+template <int kMaxTaps>
+__global__ __launch_bounds__(64) void toeplitz_fragments_kernel(const float *__restrict__ filter,
+                                                              int k, int causal,
+                                                              uint4 *__restrict__ table) {
+  constexpr int kSteps = FirMfmaShape<kMaxTaps>::kSteps;
+  const int lane = threadIdx.x;
+  const int q = blockIdx.y;
+  const size_t g = blockIdx.x;
+  const float *h = filter + g * k;
+  uint16_t hi[8], lo[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int old = 32 * q + 8 * (lane >> 4) + e - (lane & 15);
+    float tap = 0.0F;
+    if (old >= 0 && old < k)
+      tap = h[causal ? k - 1 - old : old];
+    hi[e] = f32_to_bf16(tap);
+    lo[e] = f32_to_bf16(tap - bf16_to_f32(hi[e]));
+  }
+  const size_t base = ((g * kSteps + q) * 2) * 64 + lane;
+  table[base] = __builtin_bit_cast(uint4, hi);
+  table[base + 64] = __builtin_bit_cast(uint4, lo);
+}
+
+__device__ inline bf16x8 load_frag(const uint16_t *p) {
+  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(p));
+}
+
+template <typename T, typename O, int kMaxTaps, int kWin>
+__global__ __launch_bounds__(kFirThreads) void hyena_fir_mfma_kernel(
+    const T *__restrict__ P, const float *__restrict__ short_history,
+    const uint16_t *__restrict__ short_filter, int short_len,
+    const float *__restrict__ inner_history, const uint4 *__restrict__ fragments,
+    size_t group_size, int k, int causal, const float *__restrict__ direct,
+    size_t L, size_t W, size_t planar, O out) {
+  using Shape = FirMfmaShape<kMaxTaps>;
+  extern __shared__ __attribute__((aligned(16))) unsigned char fir_smem[];
+  uint16_t *u_hi = reinterpret_cast<uint16_t *>(fir_smem);    // [64][kStride]
+  uint16_t *u_lo = u_hi + kChannels * Shape::kStride;         // [64][kStride]
+  float *x2_s = reinterpret_cast<float *>(u_lo + kChannels * Shape::kStride);  // [kFirTile][64]
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const size_t c_block = blockIdx.x * static_cast<size_t>(kChannels);
+  const size_t c = c_block + lane;
+  const long t0 = static_cast<long>(blockIdx.y) * kFirTile;
+  const int hist = k - 1;
+  const long window = kFirTile + hist;  // staged rows
+  const size_t cols3 = 3 * W;
+
+  // ---- Stage u (and x2 of the output rows): wave w owns a contiguous run
+  // of kRows (even) window rows. Interior runs load all their rows (plus the
+  // short-FIR lead-in) in one batch and evaluate the FIR from registers;
+  // runs that touch the history, the window end or the sequence end take
+  // the general path.
+  {
+    constexpr int kWaves = kFirThreads / 64;
+    constexpr int kRows = ((Shape::kSpan + kWaves - 1) / kWaves + 1) / 2 * 2;
+    const int i0 = wave * kRows, i1 = min(i0 + kRows, Shape::kSpan);
+    const long tw = t0 - hist + i0;  // time of the run's first row
+    const bool interior = tw - (kWin - 1) >= 0 && i0 + kRows <= window &&
+                          tw + kRows <= static_cast<long>(L);
+    if (interior) {
+      float taps[3][kWin];
+      load_window_taps(short_filter, short_len, c, taps);
+      const T *base = P + static_cast<size_t>(tw - (kWin - 1)) * cols3;
+      float v[kRows + kWin - 1][3];
+#pragma unroll
+      for (int s = 0; s < 3; ++s) {
+        const T *column = base + pcol(c, s, planar);
+#pragma unroll
+        for (int b = 0; b < kRows + kWin - 1; ++b)
+          v[b][s] = load_act(column, static_cast<size_t>(b) * cols3);
+      }
+      uint32_t *hi_pairs = reinterpret_cast<uint32_t *>(u_hi + lane * Shape::kStride + i0);
+      uint32_t *lo_pairs = reinterpret_cast<uint32_t *>(u_lo + lane * Shape::kStride + i0);
+#pragma unroll
+      for (int b = 0; b < kRows; b += 2) {
+        uint32_t hi_pair = 0, lo_pair = 0;
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          float fir[3];
+#pragma unroll
+          for (int s = 0; s < 3; ++s) {
+            float total = 0.0F;
+#pragma unroll
+            for (int j = 0; j < kWin; ++j)
+              total += v[b + half + j][s] * taps[s][j];
+            fir[s] = total;
+          }
+          const float u = fir[1] * fir[2];
+          const uint16_t hi = f32_to_bf16(u);
+          hi_pair |= static_cast<uint32_t>(hi) << (16 * half);
+          lo_pair |= static_cast<uint32_t>(f32_to_bf16(u - bf16_to_f32(hi))) << (16 * half);
+          if (i0 + b + half >= hist)
+            x2_s[(i0 + b + half - hist) * kChannels + lane] = fir[0];
+        }
+        hi_pairs[b / 2] = hi_pair;
+        lo_pairs[b / 2] = lo_pair;
+      }
+    } else {
+      // Rows before t = 0 come from the inner history; rows past the window
+      // or the sequence are zero (they only meet zero taps or unstored
+      // outputs).
+      int i = i0;
+      for (; i < i1; ++i) {
+        const long t = t0 - hist + i;
+        if (t >= 0 && i < window && t < static_cast<long>(L))
+          break;
+        float u = 0.0F;
+        if (t < 0 && i < window && inner_history != nullptr)
+          u = inner_history[static_cast<size_t>(hist + t) * W + c];
+        const uint16_t hi = f32_to_bf16(u);
+        u_hi[lane * Shape::kStride + i] = hi;
+        u_lo[lane * Shape::kStride + i] = f32_to_bf16(u - bf16_to_f32(hi));
+      }
+      const int i_end = static_cast<int>(min<long>(
+          i1, min<long>(window, static_cast<long>(L) - (t0 - hist))));
+      if (i < i_end) {
+        RowStream<T, kWin> stream;
+        load_window_taps(short_filter, short_len, c, stream.taps);
+        stream.prime(P, short_history, short_len, cols3, planar, t0 - hist + i, c);
+        for (; i < i_end; i += kBatch) {
+          const size_t t = static_cast<size_t>(t0 - hist + i);
+          float rows[kBatch][3];
+          load_batch(P, cols3, planar, t, t + min(kBatch, i_end - i), c, rows);
+#pragma unroll
+          for (int b = 0; b < kBatch; ++b) {
+            if (i + b >= i_end)
+              break;
+            float fir[3];
+            stream.push(rows[b], fir);
+            const float u = fir[1] * fir[2];
+            const uint16_t hi = f32_to_bf16(u);
+            u_hi[lane * Shape::kStride + i + b] = hi;
+            u_lo[lane * Shape::kStride + i + b] = f32_to_bf16(u - bf16_to_f32(hi));
+            if (i + b >= hist)
+              x2_s[(i + b - hist) * kChannels + lane] = fir[0];
+          }
+        }
+        i = i_end;
+      }
+      for (; i < i1; ++i) {
+        u_hi[lane * Shape::kStride + i] = 0;
+        u_lo[lane * Shape::kStride + i] = 0;
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- Products: wave w takes channel slice w % 4 and row blocks w/4, +2, ...
+  const int slice = wave & 3;
+  const int ch = slice * 16 + (lane & 15);
+  const size_t group = (c_block + slice * 16) / group_size;
+  bf16x8 t_hi[Shape::kSteps], t_lo[Shape::kSteps];
+#pragma unroll
+  for (int q = 0; q < Shape::kSteps; ++q) {
+    const size_t base = ((group * Shape::kSteps + q) * 2) * 64 + lane;
+    t_hi[q] = __builtin_bit_cast(bf16x8, fragments[base]);
+    t_lo[q] = __builtin_bit_cast(bf16x8, fragments[base + 64]);
+  }
+  const float d = direct != nullptr ? direct[c_block + ch] : 0.0F;
+  const uint16_t *row_hi = u_hi + ch * Shape::kStride;
+  const uint16_t *row_lo = u_lo + ch * Shape::kStride;
+  for (int rb = wave >> 2; rb < kFirTile / 16; rb += kFirThreads / 64 / 4) {
+    const int r0 = rb * 16;
+    if (t0 + r0 >= static_cast<long>(L))
+      break;
+    f32x4 acc = {0.0F, 0.0F, 0.0F, 0.0F};
+#pragma unroll
+    for (int q = 0; q < Shape::kSteps; ++q) {
+      const int i = r0 + 32 * q + 8 * (lane >> 4);
+      const bf16x8 b_hi = load_frag(row_hi + i);
+      const bf16x8 b_lo = load_frag(row_lo + i);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(t_hi[q], b_hi, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(t_hi[q], b_lo, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(t_lo[q], b_hi, acc, 0, 0, 0);
+    }
+    // y replaces x2 in LDS (each element is read and written by one lane).
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int r = r0 + 4 * (lane >> 4) + e;
+      float total = acc[e];
+      if (direct != nullptr)
+        total += d * (bf16_to_f32(row_hi[r + hist]) + bf16_to_f32(row_lo[r + hist]));
+      x2_s[r * kChannels + ch] *= total;
+    }
+  }
+  __syncthreads();
+  // Row-contiguous stores: wave w writes rows w, w+16, ... across 64 channels.
+  for (int r = wave; r < kFirTile; r += kFirThreads / 64) {
+    const long t = t0 + r;
+    if (t >= static_cast<long>(L))
+      break;
+    put(out, static_cast<size_t>(t) * W + c, x2_s[r * kChannels + lane]);
+  }
+}
+
 // Rewrites the inner (u) history with the last k-1 rows of [history ; u].
 // Runs after the main kernel and before the short history moves on.
 template <typename T>
 __global__ void inner_history_kernel(const T *__restrict__ P,
                                      const float *__restrict__ short_history,
                                      const uint16_t *__restrict__ short_filter,
-                                     int short_len, size_t L, size_t W,
+                                     int short_len, size_t L, size_t W, size_t planar,
                                      float *inner_history, int hist) {
   const size_t c = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
   if (c >= W)
@@ -340,7 +578,11 @@ __global__ void inner_history_kernel(const T *__restrict__ P,
   float taps[3][kMaxShort];
   load_short_taps(short_filter, short_len, c, taps);
   const size_t cols3 = 3 * W;
-  for (int h = 0; h < hist; ++h) {
+  // With L >= hist every new row comes from u and rows are independent: one
+  // block row per history row. Otherwise rows shift in place, oldest first.
+  const int h_begin = gridDim.y > 1 ? static_cast<int>(blockIdx.y) : 0;
+  const int h_end = gridDim.y > 1 ? h_begin + 1 : hist;
+  for (int h = h_begin; h < h_end; ++h) {
     const long source = static_cast<long>(h) + static_cast<long>(L);  // in [hist ; u]
     float value;
     if (source < hist) {
@@ -348,7 +590,7 @@ __global__ void inner_history_kernel(const T *__restrict__ P,
     } else {
       const long t = source - hist;
       float x2, u;
-      gates(P, short_history, taps, short_len, cols3, t, c, &x2, &u);
+      gates(P, short_history, taps, short_len, cols3, planar, t, c, &x2, &u);
       value = u;
     }
     inner_history[static_cast<size_t>(h) * W + c] = value;
@@ -373,26 +615,71 @@ size_t hcl_chunks(size_t length) { return (length + kChunk - 1) / kChunk; }
 
 template <typename T, typename O, int kWin>
 Status launch_hcl(const T *projection, const float *short_history, const HyenaWeights &wt,
-                  int short_len, size_t length, size_t width, int S, size_t G,
+                  int short_len, size_t length, size_t width, size_t planar, int S, size_t G,
                   float *chunk_state, float *modal_state, O out, hipStream_t stream) {
   const dim3 grid(ceil_div(width, kChannels), static_cast<unsigned>(G));
   hipLaunchKernelGGL((hcl_chunk_state_kernel<T, kWin>), grid, dim3(kChannels), 0, stream,
                      projection, short_history, wt.short_filter, short_len, length, width,
-                     wt.poles, S, chunk_state);
+                     planar, wt.poles, S, chunk_state);
   EVO_TRY(launch_status("hcl_chunk_state_kernel"));
   hipLaunchKernelGGL(hcl_carry_kernel, dim3(ceil_div(width * S, 256)), dim3(256), 0, stream,
                      chunk_state, G, length, width, S, wt.poles, modal_state);
   EVO_TRY(launch_status("hcl_carry_kernel"));
   hipLaunchKernelGGL((hcl_output_kernel<T, O, kWin>), grid, dim3(kChannels), 0, stream,
                      projection, short_history, wt.short_filter, short_len, length, width,
-                     wt.poles, wt.residues, wt.direct, S, chunk_state, out);
+                     planar, wt.poles, wt.residues, wt.direct, S, chunk_state, out);
   return launch_status("hcl_output_kernel");
+}
+
+template <typename T, typename O, int kMaxTaps>
+Status launch_fir_mfma(const T *projection, const float *short_history,
+                       const HyenaWeights &wt, int short_len, const float *inner_history,
+                       size_t group_size, int k, int causal, const float *direct,
+                       size_t length, size_t width, size_t planar, void *workspace, O out,
+                       hipStream_t stream) {
+  constexpr size_t lds = FirMfmaShape<kMaxTaps>::kLdsBytes;
+  static_assert(lds <= 160 * 1024, "LDS");
+  auto *fragments = static_cast<uint4 *>(workspace);
+  hipLaunchKernelGGL(toeplitz_fragments_kernel<kMaxTaps>,
+                     dim3(static_cast<unsigned>(wt.groups), FirMfmaShape<kMaxTaps>::kSteps),
+                     dim3(64), 0, stream, wt.inner_filter, k, causal, fragments);
+  EVO_TRY(launch_status("toeplitz_fragments_kernel"));
+  const dim3 grid(static_cast<unsigned>(width / kChannels),
+                  static_cast<unsigned>(ceil_div(length, kFirTile)));
+  if (short_len <= 4) {
+    auto kernel = hyena_fir_mfma_kernel<T, O, kMaxTaps, 4>;
+    EVO_TRY(hip_status(hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           static_cast<int>(lds)),
+                       "hyena_fir_mfma_kernel LDS opt-in"));
+    hipLaunchKernelGGL(kernel, grid, dim3(kFirThreads), lds, stream, projection,
+                       short_history, wt.short_filter, short_len, inner_history,
+                       fragments, group_size, k, causal, direct, length, width, planar, out);
+  } else {
+    auto kernel = hyena_fir_mfma_kernel<T, O, kMaxTaps, kMaxShort>;
+    EVO_TRY(hip_status(hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           static_cast<int>(lds)),
+                       "hyena_fir_mfma_kernel LDS opt-in"));
+    hipLaunchKernelGGL(kernel, grid, dim3(kFirThreads), lds, stream, projection,
+                       short_history, wt.short_filter, short_len, inner_history,
+                       fragments, group_size, k, causal, direct, length, width, planar, out);
+  }
+  return launch_status("hyena_fir_mfma_kernel");
 }
 
 }  // namespace
 
 size_t hyena_workspace_bytes(int kind, size_t length, size_t width,
                              size_t state) {
+  if (kind == kHyenaHcs || kind == kHyenaHcm) {
+    // Toeplitz fragment table of the MFMA FIR: at most width/16 groups of
+    // kSteps x 2 planes x 64 lanes x 16 bytes.
+    if (width % kChannels != 0)
+      return 0;
+    const size_t steps = kind == kHyenaHcs ? FirMfmaShape<8>::kSteps : FirMfmaShape<128>::kSteps;
+    return width / 16 * steps * 2 * 64 * 16;
+  }
   if (kind != kHyenaHcl)
     return 0;
   return hcl_chunks(length) * state * width * sizeof(float);
@@ -400,7 +687,7 @@ size_t hyena_workspace_bytes(int kind, size_t length, size_t width,
 
 template <typename T, typename O>
 Status hyena_forward(int kind, const T *projection, size_t length,
-                     size_t width, const HyenaWeights &wt,
+                     size_t width, bool planar_projection, const HyenaWeights &wt,
                      float *short_history, float *inner_history,
                      float *modal_state, void *workspace,
                      size_t workspace_bytes, O out, hipStream_t stream) {
@@ -409,6 +696,7 @@ Status hyena_forward(int kind, const T *projection, size_t length,
       wt.short_len > kMaxShort || length > (1UL << 40))
     return {ErrorCode::kInvalidArgument, "hyena_forward: invalid arguments"};
   const int short_len = static_cast<int>(wt.short_len);
+  const size_t planar = planar_projection ? width : 0;
   const dim3 channel_blocks(ceil_div(width, kChannels));
   if (kind == kHyenaHcl) {
     if (wt.poles == nullptr || wt.residues == nullptr || wt.direct == nullptr ||
@@ -424,10 +712,10 @@ Status hyena_forward(int kind, const T *projection, size_t length,
     const int S = static_cast<int>(wt.state);
     if (short_len <= 4) {
       EVO_TRY((launch_hcl<T, O, 4>(projection, short_history, wt, short_len, length, width,
-                                   S, G, chunk_state, modal_state, out, stream)));
+                                   planar, S, G, chunk_state, modal_state, out, stream)));
     } else {
       EVO_TRY((launch_hcl<T, O, kMaxShort>(projection, short_history, wt, short_len, length,
-                                           width, S, G, chunk_state, modal_state, out, stream)));
+                                           width, planar, S, G, chunk_state, modal_state, out, stream)));
     }
   } else if (kind == kHyenaHcs || kind == kHyenaHcm) {
     if (wt.inner_filter == nullptr || wt.groups == 0 || width % wt.groups != 0 ||
@@ -437,7 +725,21 @@ Status hyena_forward(int kind, const T *projection, size_t length,
     const int k = static_cast<int>(wt.inner_len);
     const int causal = kind == kHyenaHcm ? 1 : 0;
     const float *direct = kind == kHyenaHcm ? wt.direct : nullptr;
-    if (k <= 8) {
+    const size_t group_size = width / wt.groups;
+    if (width % kChannels == 0 && group_size % 16 == 0) {
+      const size_t steps = k <= 8 ? FirMfmaShape<8>::kSteps : FirMfmaShape<128>::kSteps;
+      if (workspace == nullptr || workspace_bytes < wt.groups * steps * 2 * 64 * 16)
+        return {ErrorCode::kInvalidArgument, "hyena_forward: FIR workspace too small"};
+      if (k <= 8) {
+        EVO_TRY((launch_fir_mfma<T, O, 8>(projection, short_history, wt, short_len,
+                                          inner_history, group_size, k, causal, direct, length,
+                                          width, planar, workspace, out, stream)));
+      } else {
+        EVO_TRY((launch_fir_mfma<T, O, 128>(projection, short_history, wt, short_len,
+                                            inner_history, group_size, k, causal, direct,
+                                            length, width, planar, workspace, out, stream)));
+      }
+    } else if (k <= 8) {
       constexpr int kTile = 64, kTaps = 8;
       static_assert(((kTaps - 1 + kTile) + kTile) * 64 * sizeof(float) <= 65536, "LDS");
       const size_t lds = ((kTaps - 1 + kTile) + kTile) * 64 * sizeof(float);
@@ -445,7 +747,7 @@ Status hyena_forward(int kind, const T *projection, size_t length,
       hipLaunchKernelGGL((hyena_fir_kernel<T, O, kTile, kTaps>), grid, dim3(256), lds, stream,
                          projection, short_history, wt.short_filter, short_len,
                          inner_history, wt.inner_filter, wt.groups, k, causal,
-                         direct, length, width, out);
+                         direct, length, width, planar, out);
     } else {
       constexpr int kTile = 128, kTaps = 128;
       const size_t lds = ((kTaps - 1 + kTile) + kTile) * 64 * sizeof(float);
@@ -458,13 +760,14 @@ Status hyena_forward(int kind, const T *projection, size_t length,
       hipLaunchKernelGGL((hyena_fir_kernel<T, O, kTile, kTaps>), grid, dim3(256), lds, stream,
                          projection, short_history, wt.short_filter, short_len,
                          inner_history, wt.inner_filter, wt.groups, k, causal,
-                         direct, length, width, out);
+                         direct, length, width, planar, out);
     }
     EVO_TRY(launch_status("hyena_fir_kernel"));
     if (inner_history != nullptr && k > 1) {
-      hipLaunchKernelGGL(inner_history_kernel<T>, dim3(ceil_div(width, 256)), dim3(256), 0,
+      const unsigned rows = length >= static_cast<size_t>(k - 1) ? static_cast<unsigned>(k - 1) : 1;
+      hipLaunchKernelGGL(inner_history_kernel<T>, dim3(ceil_div(width, 256), rows), dim3(256), 0,
                          stream, projection, short_history, wt.short_filter,
-                         short_len, length, width, inner_history, k - 1);
+                         short_len, length, width, planar, inner_history, k - 1);
       EVO_TRY(launch_status("inner_history_kernel"));
     }
   } else {
@@ -479,19 +782,19 @@ Status hyena_forward(int kind, const T *projection, size_t length,
   return Status::Ok();
 }
 
-template Status hyena_forward<float, float *>(int, const float *, size_t, size_t,
+template Status hyena_forward<float, float *>(int, const float *, size_t, size_t, bool,
                                               const HyenaWeights &, float *, float *,
                                               float *, void *, size_t, float *,
                                               hipStream_t);
-template Status hyena_forward<uint16_t, uint16_t *>(int, const uint16_t *, size_t, size_t,
+template Status hyena_forward<uint16_t, uint16_t *>(int, const uint16_t *, size_t, size_t, bool,
                                                     const HyenaWeights &, float *, float *,
                                                     float *, void *, size_t, uint16_t *,
                                                     hipStream_t);
-template Status hyena_forward<uint16_t, SplitOut>(int, const uint16_t *, size_t, size_t,
+template Status hyena_forward<uint16_t, SplitOut>(int, const uint16_t *, size_t, size_t, bool,
                                                   const HyenaWeights &, float *, float *,
                                                   float *, void *, size_t, SplitOut,
                                                   hipStream_t);
-template Status hyena_forward<float, SplitOut>(int, const float *, size_t, size_t,
+template Status hyena_forward<float, SplitOut>(int, const float *, size_t, size_t, bool,
                                                const HyenaWeights &, float *, float *,
                                                float *, void *, size_t, SplitOut,
                                                hipStream_t);

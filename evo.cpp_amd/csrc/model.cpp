@@ -358,7 +358,9 @@ Status Context::initialize(std::shared_ptr<const Model> model, size_t capacity,
   EVO_TRY(hip_check(hipMemsetAsync(flag_.as<void>(), 0, sizeof(int), stream_), "flag reset"));
   EVO_TRY(hip_check(hipHostMalloc(reinterpret_cast<void **>(&host_flag_), sizeof(int),
                                   hipHostMallocDefault), "pinned flag"));
-  workspace_bytes_ = hyena_workspace_bytes(kHyenaHcl, R, w, c.state);
+  workspace_bytes_ = std::max({hyena_workspace_bytes(kHyenaHcl, R, w, c.state),
+                               hyena_workspace_bytes(kHyenaHcs, R, w, c.state),
+                               hyena_workspace_bytes(kHyenaHcm, R, w, c.state)});
   EVO_TRY(workspace_.allocate(std::max<size_t>(workspace_bytes_, 256), "hyena workspace"));
   EVO_TRY(hip_check(hipHostMalloc(reinterpret_cast<void **>(&host_logits_),
                                   R * std::max(c.vocab, w) * 4, hipHostMallocDefault),
@@ -455,13 +457,13 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
                        : L.type == Mixer::kHcm ? kHyenaHcm : kHyenaHcl;
       if (L.fp8)
         EVO_TRY((hyena_forward<uint16_t, SplitOut>(kind, projected_.as<uint16_t>(), rows, w,
-                                                   hw, k.short_history.as<float>(),
+                                                   false, hw, k.short_history.as<float>(),
                                                    k.inner_history.as<float>(),
                                                    k.modal_state.as<float>(),
                                                    workspace_.as<void>(), workspace_.bytes(),
                                                    mixed_out, stream_)));
       else
-        EVO_TRY((hyena_forward<float, SplitOut>(kind, projected, rows, w, hw,
+        EVO_TRY((hyena_forward<float, SplitOut>(kind, projected, rows, w, false, hw,
                                                 k.short_history.as<float>(),
                                                 k.inner_history.as<float>(),
                                                 k.modal_state.as<float>(),

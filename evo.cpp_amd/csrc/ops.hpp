@@ -107,9 +107,11 @@ struct HyenaWeights {
 size_t hyena_workspace_bytes(int kind, size_t length, size_t width,
                              size_t state);
 // O: float* (F32 out), uint16_t* (BF16 out) or SplitOut (GEMM planes).
+// The projection [L, 3W] holds stream s (x2, x1, v) of channel c at column
+// 3c + s (the reference layout) or, when planar_projection, at s * W + c.
 template <typename T, typename O>
 Status hyena_forward(int kind, const T *projection, size_t length,
-                     size_t width, const HyenaWeights &weights,
+                     size_t width, bool planar_projection, const HyenaWeights &weights,
                      float *short_history, float *inner_history,
                      float *modal_state, void *workspace,
                      size_t workspace_bytes, O out, hipStream_t stream);

@@ -41,11 +41,18 @@ EVO_API void *evo_hip_context_stream(const evo_context *context);
 
 /* Storage type of activation tensors passed to the Hyena operator. */
 /* EVO_HIP_SPLIT: F32 input, output as split BF16 planes [2][rows][cols]
- * (hi = bf16(y), lo = bf16(y - hi)), the GEMM activation layout. */
+ * (hi = bf16(y), lo = bf16(y - hi)), the GEMM activation layout.
+ * EVO_HIP_BF16_SPLIT: BF16 input (the FP8 projection's output), split
+ * output; Hyena operator only. */
 typedef enum evo_hip_dtype {
   EVO_HIP_F32 = 0,
   EVO_HIP_BF16 = 1,
-  EVO_HIP_SPLIT = 2
+  EVO_HIP_SPLIT = 2,
+  EVO_HIP_BF16_SPLIT = 3,
+  /* OR-ed into the Hyena operator's dtype: the projection holds stream s
+   * (x2, x1, v) of channel c at column s*W + c instead of the reference's
+   * 3c + s (the library permutes its projection weights this way). */
+  EVO_HIP_PLANAR = 0x100
 } evo_hip_dtype;
 typedef enum evo_hip_hyena_kind {
   EVO_HIP_HYENA_HCS = 0,

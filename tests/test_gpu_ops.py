@@ -242,8 +242,18 @@ def hyena_oracle(kind, case, projection=None):
                          case.get("state", 0))
 
 
-def hyena_gpu(kind, case, dtype=N.DTYPE_F32, rows=None, caches=None, projection=None):
+def planar(proj):
+    """Interleaved projection columns (3c + s) -> planar (s * W + c)."""
+    rows, cols = proj.shape
+    return np.ascontiguousarray(proj.reshape(rows, cols // 3, 3).transpose(0, 2, 1)
+                                .reshape(rows, cols))
+
+
+def hyena_gpu(kind, case, dtype=N.DTYPE_F32, rows=None, caches=None, projection=None,
+              planar_layout=False):
     proj = case["projection"] if projection is None else projection
+    if planar_layout:
+        proj = planar(proj)
     length = proj.shape[0] if rows is None else rows
     width = case["width"]
     state = case.get("state", 0)
@@ -256,11 +266,15 @@ def hyena_gpu(kind, case, dtype=N.DTYPE_F32, rows=None, caches=None, projection=
     elif dtype == N.DTYPE_SPLIT:
         proj_d = dev(proj)
         out = empty((2, length, width), np.uint16)
+    elif dtype == N.DTYPE_BF16_SPLIT:
+        proj_d = dev(bf16_bits(proj))
+        out = empty((2, length, width), np.uint16)
     else:
         proj_d = dev(proj)
         out = empty((length, width))
     caches = caches or {}
-    N.call("evo_hip_hyena_forward", kind, dtype, p(proj_d), length, width,
+    N.call("evo_hip_hyena_forward", kind, dtype | (N.DTYPE_PLANAR if planar_layout else 0),
+           p(proj_d), length, width,
            p(dev(case["short"])), 3, p(dev(case["inner"]) if "inner" in case else None),
            case.get("groups", 1), case.get("inner_len", 0),
            p(dev(case["direct"]) if "direct" in case else None),
@@ -269,7 +283,7 @@ def hyena_gpu(kind, case, dtype=N.DTYPE_F32, rows=None, caches=None, projection=
            p(caches.get("short")), p(caches.get("inner")), p(caches.get("modal")),
            p(ws), ws_bytes, p(out), stream())
     result = host(out)
-    if dtype == N.DTYPE_SPLIT:
+    if dtype in (N.DTYPE_SPLIT, N.DTYPE_BF16_SPLIT):
         planes = bf16_to_f32(result.view(np.uint16))
         return planes[0].astype(np.float64) + planes[1]
     return bf16_to_f32(result.view(np.uint16)) if dtype == N.DTYPE_BF16 else result
@@ -285,6 +299,26 @@ def test_hyena_f32_matches_oracle(kind, inner_len, length, width):
                       inner_len=inner_len or 7)
     expected = hyena_oracle(kind, case)
     assert rel_err(hyena_gpu(kind, case), expected) < 1e-5
+
+
+@pytest.mark.parametrize("kind,inner_len", [(N.HYENA_HCS, 7), (N.HYENA_HCS, 5),
+                                             (N.HYENA_HCM, 128), (N.HYENA_HCM, 33)])
+@pytest.mark.parametrize("length,width,groups", [(1, 256, 16), (300, 256, 16),
+                                                 (1000, 128, 4), (777, 512, 16)])
+def test_hyena_fir_mfma_matches_oracle(kind, inner_len, length, width, groups):
+    """Filter groups of 16k channels run the Toeplitz-MFMA FIR; F32 taps that
+    are not BF16 numbers exercise the split-tap pass."""
+    case = hyena_case(length + width + groups + inner_len, kind, length, width,
+                      groups=groups, inner_len=inner_len)
+    expected = hyena_oracle(kind, case)
+    assert rel_err(hyena_gpu(kind, case), expected) < 1e-5
+    proj = bf16_to_f32(bf16_bits(case["projection"]))
+    expected = hyena_oracle(kind, case, projection=proj)
+    actual = hyena_gpu(kind, case, dtype=N.DTYPE_BF16_SPLIT, projection=proj)
+    assert rel_err(actual, expected) < 2e-5
+    actual = hyena_gpu(kind, case, dtype=N.DTYPE_BF16_SPLIT, projection=proj,
+                       planar_layout=True)
+    assert rel_err(actual, expected) < 2e-5
 
 
 @pytest.mark.parametrize("kind,inner_len", KINDS)
@@ -307,18 +341,38 @@ def test_hyena_bf16_io(kind, inner_len):
 
 
 @pytest.mark.parametrize("kind,inner_len", KINDS)
+@pytest.mark.parametrize("groups", [16, 8])
+def test_hyena_bf16_split_io(kind, inner_len, groups):
+    """The model's FP8-projection path: BF16 projection in, split planes out."""
+    case = hyena_case(55 + kind + groups, kind, 1029, 128, groups=groups,
+                      inner_len=inner_len or 7)
+    proj = bf16_to_f32(bf16_bits(case["projection"]))
+    expected = hyena_oracle(kind, case, projection=proj)
+    actual = hyena_gpu(kind, case, dtype=N.DTYPE_BF16_SPLIT, projection=proj)
+    assert rel_err(actual, expected) < 2e-5
+    actual = hyena_gpu(kind, case, dtype=N.DTYPE_BF16_SPLIT, projection=proj,
+                       planar_layout=True)
+    assert rel_err(actual, expected) < 2e-5
+
+
+@pytest.mark.parametrize("kind,inner_len", KINDS)
 @pytest.mark.parametrize("split", [1, 5, 130, 299])
-def test_hyena_continuation_equals_one_pass(kind, inner_len, split):
-    """Two calls sharing the FIR histories / modal state equal one call."""
-    case = hyena_case(5 + kind, kind, 300, 64, inner_len=inner_len or 7)
+@pytest.mark.parametrize("groups,layout", [(16, False), (4, False), (4, True)])
+def test_hyena_continuation_equals_one_pass(kind, inner_len, split, groups, layout):
+    """Two calls sharing the FIR histories / modal state equal one call
+    (groups=4 gives 16-channel filter groups: the MFMA FIR; layout=True feeds
+    the planar projection, whose short-FIR history is planar too)."""
+    case = hyena_case(5 + kind, kind, 300, 64, groups=groups, inner_len=inner_len or 7)
     width = 64
     whole = hyena_gpu(kind, case)
     hist = inner_len - 1 if inner_len else 0
     caches = {"short": zeros((2, 3 * width)),
               "inner": zeros((max(hist, 1), width)) if hist else None,
               "modal": zeros((width, 16)) if kind == N.HYENA_HCL else None}
-    first = hyena_gpu(kind, case, projection=case["projection"][:split], caches=caches)
-    second = hyena_gpu(kind, case, projection=case["projection"][split:], caches=caches)
+    first = hyena_gpu(kind, case, projection=case["projection"][:split], caches=caches,
+                      planar_layout=layout)
+    second = hyena_gpu(kind, case, projection=case["projection"][split:], caches=caches,
+                       planar_layout=layout)
     joined = np.concatenate([first, second])
     assert rel_err(joined, whole) < 1e-5
 
