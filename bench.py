@@ -93,24 +93,33 @@ def kernel_rooflines(split):
     out["gemm"] = dict(kernel="gemm_kernel<%s>" % ("true" if split else "false"),
                        ms=ms, flops=flops, tflops=flops / ms / 1e9)
     del x, w, y, planes
-    # config 2: fused Hyena HCL operator, BF16 [8192, 12288] in, [8192, 4096] out
-    length, width, state = 8192, 4096, 16
+    # Hyena operators on the model's path: BF16 projection [8192, 12288] in
+    # (the FP8 projection's output), split BF16 planes [2, 8192, 4096] out,
+    # 7B filter groups (256) and tap counts (HCS 7, HCM 128, HCL 16 states).
+    length, width, state, groups = 8192, 4096, 16, 256
     proj = torch.randn(length, 3 * width, device="cuda", generator=g).to(torch.bfloat16)
-    short = (torch.randn(3 * width, 3, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    short = (torch.randn(3 * width, 3, device="cuda", generator=g) * 0.3).to(torch.bfloat16)
     poles = torch.rand(width, state, device="cuda", generator=g) * 0.49 + 0.5
     residues = torch.randn(width, state, device="cuda", generator=g) * 0.02
     direct = torch.randn(width, device="cuda", generator=g) * 0.02
-    ws_bytes = native.call("evo_hip_hyena_workspace_bytes", 2, length, width, state)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
-    yb = torch.empty(length, width, dtype=torch.bfloat16, device="cuda")
-    ms = event_time(lambda: native.call(
-        "evo_hip_hyena_forward", 2, 1, proj.data_ptr(), length, width, short.data_ptr(), 3,
-        None, 1, 0, direct.data_ptr(), poles.data_ptr(), residues.data_ptr(), state, None,
-        None, None, ws.data_ptr(), ws_bytes, yb.data_ptr(), stream), 10)
-    hbm_bytes = length * 3 * width * 2 + length * width * 2
-    out["hyena"] = dict(kernel="hcl operator (chunk_state + carry + output)", ms=ms,
-                        bytes=hbm_bytes, gbs=hbm_bytes / ms / 1e6)
-    del proj, yb, ws
+    planes_out = torch.empty(2, length, width, dtype=torch.int16, device="cuda")
+    hbm_bytes = length * 3 * width * 2 + length * width * 4
+    out["hyena"] = []
+    for kind, name, taps in ((1, "HCM FIR (128 taps)", 128), (0, "HCS FIR (7 taps)", 7),
+                             (2, "HCL (16 modal states)", 0)):
+        filt = (torch.randn(groups, max(taps, 1), device="cuda", generator=g)
+                / max(taps, 1) ** 0.5).to(torch.bfloat16).float()
+        st = state if kind == 2 else 0
+        ws_bytes = native.call("evo_hip_hyena_workspace_bytes", kind, length, width, st)
+        ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device="cuda")
+        ms = event_time(lambda: native.call(
+            "evo_hip_hyena_forward", kind, native.DTYPE_BF16_SPLIT, proj.data_ptr(), length,
+            width, short.data_ptr(), 3, filt.data_ptr(), groups, taps, direct.data_ptr(),
+            poles.data_ptr(), residues.data_ptr(), st, None, None, None, ws.data_ptr(),
+            ws_bytes, planes_out.data_ptr(), stream), 10)
+        out["hyena"].append(dict(kernel=name, ms=ms, bytes=hbm_bytes,
+                                 gbs=hbm_bytes / ms / 1e6))
+    del proj, planes_out
     # config 3: FP8 projection GEMM M=1024 K=4096 N=12288 (promotion every 32 K)
     m, k, n = 1024, 4096, 12288
     a8 = torch.randint(0, 0x7e, (m, k), dtype=torch.uint8, device="cuda", generator=g)
@@ -233,12 +242,14 @@ def main():
                               "unit": "TFLOP/s", "frac": round(g["tflops"] / BF16_PEAK_TFLOPS, 4),
                               "traffic": None, "ms": round(g["ms"], 4),
                               "per_launch": "2*8192*22528*4096 flop (MLP l1/l2 of one block)"}
-        h = kernels["hyena"]
-        result["hyena_roofline"] = {"bound": "hbm", "kernel": h["kernel"],
-                                    "achieved": round(h["gbs"], 1), "peak": HBM_PEAK_GBS,
-                                    "unit": "GB/s", "frac": round(h["gbs"] / HBM_PEAK_GBS, 4),
-                                    "ms": round(h["ms"], 4),
-                                    "per_launch": "268435456 B (read [8192,12288] + write [8192,4096] BF16)"}
+        hyena = [{"kernel": h["kernel"], "achieved": round(h["gbs"], 1),
+                  "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                  "frac": round(h["gbs"] / HBM_PEAK_GBS, 4), "ms": round(h["ms"], 4)}
+                 for h in kernels["hyena"]]
+        per_launch = ("335544320 B: read BF16 [8192, 12288] projection, write split "
+                      "BF16 planes [2, 8192, 4096]")
+        result["hyena_roofline"] = dict(hyena[0], bound="hbm", per_launch=per_launch)
+        result["hyena_kernels"] = hyena
         for name in ("fp8_k32", "fp8_k128"):
             f = kernels[name]
             result[name + "_roofline"] = {"bound": "mfma", "kernel": f["kernel"],
