@@ -4,7 +4,11 @@
 // qkv_rope: splits the Wqkv projection (head-major `column_split` layout
 // [h][q,k,v][d], or component-major [q,k,v][h][d]), applies GPT-NeoX
 // half-pair RoPE at position (prefix + row) / rope_scale and writes Q and the
-// appended K/V rows as split BF16 planes (hi = bf16(x), lo = bf16(x - hi)).
+// appended K rows as split BF16 planes (hi = bf16(x), lo = bf16(x - hi)).
+// v_transpose appends V to the transposed value cache V^T [W][capacity]
+// (row h*d_head + d), keys permuted inside every 16-key block by swapping
+// bits 2 and 3 of the position, the order in which one MFMA lane holds the
+// probabilities of a 16-key step (see below).
 // Reference: evo.cpp `src/cpu/model.cpp:455-509`.
 //
 // causal_attention: softmax(q.k / sqrt(d)) v over keys [0, position].
@@ -12,13 +16,15 @@
 // form below equals it up to F32 rounding).
 //
 // MFMA kernel (head_dim 32/64/128): one 256-thread block = 4 waves x 32
-// queries of one head; K and V^T tiles of 64 keys are staged in LDS as BF16
-// planes. Each wave computes S^T = K Q^T (keys x queries) with
-// v_mfma_f32_32x32x16_bf16, so every lane owns one query: the running max
-// and sum stay in-lane (plus one exchange with the lane holding the other
-// half of the keys), and P^T is already in the B-operand layout of
-// O^T += V^T P^T. Products use three BF16 passes (hi*hi + hi*lo + lo*hi),
-// about 16 significant bits per operand, with F32 accumulation.
+// queries of one head. K [64 keys][d] and V^T [d][64 keys] tiles of both
+// planes are DMA'd (global_load_lds) into XOR-swizzled LDS, double buffered,
+// so the next tile streams in while this one computes. Each wave computes
+// S^T = K Q^T (keys x queries) with v_mfma_f32_32x32x16_bf16, so every lane
+// owns one query: the running max and sum stay in-lane (plus one exchange
+// with the lane holding the other half of the keys), and P^T is already in
+// the B-operand layout of O^T += V^T P^T. Products use three BF16 passes
+// (hi*hi + hi*lo + lo*hi), about 16 significant bits per operand, with F32
+// accumulation; the exponential is exp2 of log2(e)-prescaled scores.
 // head_dim 16 uses a VALU kernel (four lanes per query).
 #include "common.hpp"
 #include "ops.hpp"
@@ -36,12 +42,23 @@ __device__ inline float get_split(const uint16_t *hi, const uint16_t *lo, size_t
   return bf16_to_f32(hi[i]) + bf16_to_f32(lo[i]);
 }
 
+// Position of key `pos` inside the transposed value cache.
+__host__ __device__ inline size_t vt_column(size_t pos) {
+  return (pos & ~static_cast<size_t>(15)) | (pos & 3) | ((pos & 4) << 1) | ((pos & 8) >> 1);
+}
+
+__device__ inline size_t qkv_column(int column_split, size_t width, size_t head,
+                                    size_t head_dim, size_t component, size_t dim) {
+  return column_split ? head * 3 * head_dim + component * head_dim + dim
+                      : component * width + head * head_dim + dim;
+}
+
 __global__ void qkv_rope_kernel(const float *__restrict__ projected, size_t rows,
                                 size_t width, size_t heads, size_t head_dim,
                                 int column_split, const float *__restrict__ inv_freq,
                                 float rope_scale, size_t prefix, uint16_t *__restrict__ q,
                                 size_t q_plane, uint16_t *__restrict__ k_cache,
-                                uint16_t *__restrict__ v_cache, size_t cache_plane) {
+                                size_t cache_plane) {
   const size_t half = head_dim / 2;
   const size_t n = rows * heads * half;
   for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
@@ -50,27 +67,52 @@ __global__ void qkv_rope_kernel(const float *__restrict__ projected, size_t rows
     const size_t head = (i / half) % heads;
     const size_t row = i / (half * heads);
     const float *src = projected + row * width * 3;
-    auto source = [&](size_t component, size_t dim) {
-      return column_split ? head * 3 * head_dim + component * head_dim + dim
-                          : component * width + head * head_dim + dim;
-    };
     const float position = static_cast<float>(prefix + row) / rope_scale;
     const float angle = position * inv_freq[pair];
     const float cosine = cosf(angle), sine = sinf(angle);
     const size_t qi = row * width + head * head_dim;
     const size_t ki = (prefix + row) * width + head * head_dim;
     {
-      const float first = src[source(0, pair)], second = src[source(0, half + pair)];
+      const float first = src[qkv_column(column_split, width, head, head_dim, 0, pair)];
+      const float second = src[qkv_column(column_split, width, head, head_dim, 0, half + pair)];
       put_split(q, q + q_plane, qi + pair, first * cosine - second * sine);
       put_split(q, q + q_plane, qi + half + pair, second * cosine + first * sine);
     }
     {
-      const float first = src[source(1, pair)], second = src[source(1, half + pair)];
+      const float first = src[qkv_column(column_split, width, head, head_dim, 1, pair)];
+      const float second = src[qkv_column(column_split, width, head, head_dim, 1, half + pair)];
       put_split(k_cache, k_cache + cache_plane, ki + pair, first * cosine - second * sine);
       put_split(k_cache, k_cache + cache_plane, ki + half + pair, second * cosine + first * sine);
     }
-    put_split(v_cache, v_cache + cache_plane, ki + pair, src[source(2, pair)]);
-    put_split(v_cache, v_cache + cache_plane, ki + half + pair, src[source(2, half + pair)]);
+  }
+}
+
+// V rows [rows, W] of the projection -> V^T planes at positions prefix..:
+// a 64-position x 64-channel tile is read row-wise, transposed through LDS
+// and written position-contiguous.
+__global__ __launch_bounds__(256) void v_transpose_kernel(
+    const float *__restrict__ projected, size_t rows, size_t width, size_t head_dim,
+    int column_split, size_t prefix, uint16_t *__restrict__ vt_cache, size_t cache_plane,
+    size_t capacity) {
+  __shared__ float tile[64][65];
+  const int tid = threadIdx.x;
+  const size_t r0 = blockIdx.x * 64ULL, c0 = blockIdx.y * 64ULL;
+  const size_t channel = c0 + (tid & 63);
+  for (int i = tid >> 6; i < 64; i += 4) {
+    const size_t row = r0 + i;
+    float value = 0.0F;
+    if (row < rows && channel < width)
+      value = projected[row * width * 3 +
+                        qkv_column(column_split, width, channel / head_dim, head_dim, 2,
+                                   channel % head_dim)];
+    tile[tid & 63][i] = value;
+  }
+  __syncthreads();
+  for (int i = tid >> 6; i < 64; i += 4) {
+    const size_t ch = c0 + i, row = r0 + (tid & 63);
+    if (row < rows && ch < width)
+      put_split(vt_cache, vt_cache + cache_plane, ch * capacity + vt_column(prefix + row),
+                tile[i][tid & 63]);
   }
 }
 
@@ -78,27 +120,72 @@ __global__ void qkv_rope_kernel(const float *__restrict__ projected, size_t rows
 constexpr int kQueriesPerWave = 32;
 constexpr int kKeys = 64;
 
+typedef __attribute__((address_space(3))) void lds_void;
+
+// 16 bytes per lane global -> LDS DMA (lane l lands at lds + 16 l; lds must be
+// wave-uniform). Completion is tracked with explicit s_waitcnt vmcnt.
+__device__ inline void dma16(const void *global, const uint16_t *lds) {
+  const unsigned address = __builtin_amdgcn_readfirstlane(
+      static_cast<unsigned>(reinterpret_cast<size_t>((const lds_void *)(lds))));
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(global), "s"(address) : "memory");
+}
+
+template <int kPending>
+__device__ inline void wait_dma() {
+  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(kPending) : "memory");
+}
+
+// Swizzle of a row of kUnits 16-byte units: 8 consecutive rows read at one
+// logical unit hit 8 distinct 16-byte bank groups.
+template <int kUnits>
+__device__ inline int swizzle(int row, int unit) {
+  return unit ^ ((row * kUnits / 16) & (kUnits - 1));
+}
+
+template <int kD>
+struct FlashShape {
+  static constexpr int kKUnits = kD / 8;             // 16-byte units per K row
+  static constexpr int kKPlane = kKeys * kD;         // BF16 per K plane
+  static constexpr int kVPlane = kD * kKeys;         // BF16 per V^T plane
+  static constexpr int kStage = 2 * kKPlane + 2 * kVPlane;
+  static constexpr size_t kLdsBytes = 2 * kStage * sizeof(uint16_t);
+  static constexpr int kDmaPerWave = kD / 8;         // 1 KB DMA ops per wave per tile
+};
+
 template <int kD, typename O>
 __global__ __launch_bounds__(256) void flash_attention_kernel(
     const uint16_t *__restrict__ q, size_t q_plane, const uint16_t *__restrict__ k_cache,
-    const uint16_t *__restrict__ v_cache, size_t cache_plane, size_t rows, size_t prefix,
-    size_t heads, O out) {
-  constexpr int kKStride = kD + 8;     // K tile row (BF16), padded
-  constexpr int kVStride = kKeys + 8;  // V^T tile row (BF16), padded
-  constexpr int kDSteps = kD / 16;     // K-steps of S^T over head_dim
-  constexpr int kDTiles = kD / 32;     // 32-row tiles of O^T
-  __shared__ __attribute__((aligned(16))) uint16_t k_s[2][kKeys * kKStride];
-  __shared__ __attribute__((aligned(16))) uint16_t v_s[2][kD * kVStride];
+    const uint16_t *__restrict__ vt_cache, size_t cache_plane, size_t capacity, size_t rows,
+    size_t prefix, size_t heads, O out) {
+  using Shape = FlashShape<kD>;
+  constexpr int kDSteps = kD / 16;  // K-steps of S^T over head_dim
+  constexpr int kDTiles = kD / 32;  // 32-row tiles of O^T
+  extern __shared__ __attribute__((aligned(16))) uint16_t flash_lds[];
 
   const size_t width = heads * kD;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int half = lane >> 5, col = lane & 31;
-  const size_t head = blockIdx.y;
-  const size_t block_row = blockIdx.x * static_cast<size_t>(4 * kQueriesPerWave);
+  // Block -> (head, query block): heaviest (latest) query blocks first; with
+  // heads % 8 == 0 the blocks of a head share an XCD (blocks are dealt to
+  // the 8 XCDs round-robin), so its K/V tiles are reused from one L2.
+  const size_t query_blocks = (rows + 4 * kQueriesPerWave - 1) / (4 * kQueriesPerWave);
+  const size_t b = blockIdx.x;
+  size_t head, qb;
+  if (heads % 8 == 0) {
+    const size_t per_xcd = heads / 8, idx = b / 8;
+    head = (b % 8) + 8 * (idx % per_xcd);
+    qb = query_blocks - 1 - idx / per_xcd;
+  } else {
+    head = b % heads;
+    qb = query_blocks - 1 - b / heads;
+  }
+  const size_t block_row = qb * (4 * kQueriesPerWave);
   const size_t row = block_row + wave * kQueriesPerWave + col;  // this lane's query
   const bool active = row < rows;
   const size_t position = prefix + row;
-  const float scale = 1.0F / sqrtf(static_cast<float>(kD));
+  // exp(x * scale) = exp2(x * scale * log2(e))
+  const float scale2 = 1.4426950408889634F / sqrtf(static_cast<float>(kD));
 
   // Q^T operand fragments: for d-step s, 8 consecutive dims s*16 + half*8.
   bf16x8 qh[kDSteps], ql[kDSteps];
@@ -115,6 +202,39 @@ __global__ __launch_bounds__(256) void flash_attention_kernel(
       }
     }
   }
+
+  // Per-lane DMA sources of tile 0 (op g of this wave: part g / kDmaPerWave
+  // of {K hi, K lo, V hi, V lo}, 1 KB chunk g % kDmaPerWave of that plane).
+  const uint16_t *src[Shape::kDmaPerWave];
+  int dst[Shape::kDmaPerWave];
+#pragma unroll
+  for (int i = 0; i < Shape::kDmaPerWave; ++i) {
+    const int g = wave * Shape::kDmaPerWave + i;
+    const int part = g / Shape::kDmaPerWave, chunk = g % Shape::kDmaPerWave;
+    const int flat = chunk * 64 + lane;  // 16-byte unit within the plane
+    if (part < 2) {
+      const int key = flat / Shape::kKUnits, unit = swizzle<Shape::kKUnits>(key, flat % Shape::kKUnits);
+      src[i] = k_cache + (part == 1 ? cache_plane : 0) + static_cast<size_t>(key) * width +
+               head * kD + unit * 8;
+      dst[i] = part * Shape::kKPlane + chunk * 512;
+    } else {
+      const int d = flat / 8, unit = swizzle<8>(d, flat % 8);
+      src[i] = vt_cache + (part == 3 ? cache_plane : 0) +
+               (head * kD + d) * capacity + unit * 8;
+      dst[i] = 2 * Shape::kKPlane + (part - 2) * Shape::kVPlane + chunk * 512;
+    }
+  }
+  auto issue = [&](size_t tile) {
+    uint16_t *stage = flash_lds + (tile & 1) * Shape::kStage;
+    const size_t k0 = tile * kKeys;
+#pragma unroll
+    for (int i = 0; i < Shape::kDmaPerWave; ++i) {
+      const int g = wave * Shape::kDmaPerWave + i;
+      const bool is_k = g / Shape::kDmaPerWave < 2;
+      dma16(src[i] + (is_k ? k0 * width : k0), stage + dst[i]);
+    }
+  };
+
   f32x16 o_acc[kDTiles];
 #pragma unroll
   for (int t = 0; t < kDTiles; ++t)
@@ -124,31 +244,23 @@ __global__ __launch_bounds__(256) void flash_attention_kernel(
   float running_max = -INFINITY, partial_sum = 0.0F;
 
   const size_t last_row = min(rows, block_row + 4 * kQueriesPerWave) - 1;
-  const size_t keys_needed = prefix + last_row + 1;
-  for (size_t k0 = 0; k0 < keys_needed; k0 += kKeys) {
+  const size_t tiles = (prefix + last_row + 1 + kKeys - 1) / kKeys;
+  const size_t wave_first = prefix + block_row + wave * kQueriesPerWave;  // lowest position
+  issue(0);
+  for (size_t tile = 0; tile < tiles; ++tile) {
+    // Every wave has left buffer (tile+1)&1 (tile-1's) once it passes here.
     __syncthreads();
-    // K tile [key][d] and V^T tile [d][key], both planes.
-    for (int c = tid; c < kKeys * kD / 8; c += 256) {
-      const int key = c / (kD / 8), d0 = (c % (kD / 8)) * 8;
-      const size_t g = (k0 + key) * width + head * kD + d0;
-      uint4 kh = make_uint4(0, 0, 0, 0), kl = kh, vh = kh, vl = kh;
-      if (k0 + key < keys_needed) {
-        kh = *reinterpret_cast<const uint4 *>(k_cache + g);
-        kl = *reinterpret_cast<const uint4 *>(k_cache + cache_plane + g);
-        vh = *reinterpret_cast<const uint4 *>(v_cache + g);
-        vl = *reinterpret_cast<const uint4 *>(v_cache + cache_plane + g);
-      }
-      *reinterpret_cast<uint4 *>(&k_s[0][key * kKStride + d0]) = kh;
-      *reinterpret_cast<uint4 *>(&k_s[1][key * kKStride + d0]) = kl;
-      const uint16_t *vhs = reinterpret_cast<const uint16_t *>(&vh);
-      const uint16_t *vls = reinterpret_cast<const uint16_t *>(&vl);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        v_s[0][(d0 + e) * kVStride + key] = vhs[e];
-        v_s[1][(d0 + e) * kVStride + key] = vls[e];
-      }
+    if (tile + 1 < tiles) {
+      issue(tile + 1);
+      wait_dma<Shape::kDmaPerWave>();
+    } else {
+      wait_dma<0>();
     }
     __syncthreads();
+    const uint16_t *stage = flash_lds + (tile & 1) * Shape::kStage;
+    const uint16_t *k_hi = stage, *k_lo = stage + Shape::kKPlane;
+    const uint16_t *v_hi = stage + 2 * Shape::kKPlane, *v_lo = v_hi + Shape::kVPlane;
+    const size_t k0 = tile * kKeys;
 
     // S^T tiles: st[kt] holds keys kt*32 + (e/4)*8 + half*4 + e%4 for query col.
     f32x16 st[2];
@@ -157,67 +269,68 @@ __global__ __launch_bounds__(256) void flash_attention_kernel(
 #pragma unroll
       for (int e = 0; e < 16; ++e)
         st[kt][e] = 0.0F;
+      const int key = kt * 32 + col;
 #pragma unroll
       for (int s = 0; s < kDSteps; ++s) {
-        const int off = (kt * 32 + col) * kKStride + s * 16 + half * 8;
-        const bf16x8 kh = *reinterpret_cast<const bf16x8 *>(&k_s[0][off]);
-        const bf16x8 kl = *reinterpret_cast<const bf16x8 *>(&k_s[1][off]);
+        const int off = (key * Shape::kKUnits + swizzle<Shape::kKUnits>(key, 2 * s + half)) * 8;
+        const bf16x8 kh = *reinterpret_cast<const bf16x8 *>(k_hi + off);
+        const bf16x8 kl = *reinterpret_cast<const bf16x8 *>(k_lo + off);
         st[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, qh[s], st[kt], 0, 0, 0);
         st[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, ql[s], st[kt], 0, 0, 0);
         st[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kl, qh[s], st[kt], 0, 0, 0);
       }
     }
-    // Scale, causal mask, tile maximum.
+    // Scale (log2 domain), causal mask on the diagonal tiles, tile maximum.
     float tile_max = -INFINITY;
+    const bool diagonal = k0 + kKeys - 1 > wave_first;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const size_t key = k0 + kt * 32 + (e >> 2) * 8 + half * 4 + (e & 3);
-        const float value = key <= position ? st[kt][e] * scale : -INFINITY;
+        float value = st[kt][e] * scale2;
+        if (diagonal) {
+          const size_t key = k0 + kt * 32 + (e >> 2) * 8 + half * 4 + (e & 3);
+          value = key <= position ? value : -INFINITY;
+        }
         st[kt][e] = value;
         tile_max = fmaxf(tile_max, value);
       }
     tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32, 64));
     const float new_max = fmaxf(running_max, tile_max);
-    // A query with no visible key yet keeps new_max = -inf: nothing to scale.
-    const float correction = new_max == -INFINITY ? 1.0F : expf(running_max - new_max);
-    running_max = new_max;
-    partial_sum *= correction;
+    if (__any(new_max != running_max)) {
+      // A query with no visible key yet keeps new_max = -inf: nothing to scale.
+      const float correction =
+          new_max == -INFINITY ? 1.0F : __builtin_amdgcn_exp2f(running_max - new_max);
+      partial_sum *= correction;
 #pragma unroll
-    for (int t = 0; t < kDTiles; ++t)
+      for (int t = 0; t < kDTiles; ++t)
 #pragma unroll
-      for (int e = 0; e < 16; ++e)
-        o_acc[t][e] *= correction;
-    // P = exp(S - max) as B operands (P^T slots = this lane's key entries).
+        for (int e = 0; e < 16; ++e)
+          o_acc[t][e] *= correction;
+      running_max = new_max;
+    }
+    const float base = new_max == -INFINITY ? 0.0F : new_max;
+    // P = exp2(S - max) as B operands; with the permuted V^T key order, the
+    // 8 entries e0..e0+7 of this lane are the 8 consecutive V^T columns of
+    // 16-key step kk at half*8.
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       const int kt = kk >> 1, e0 = (kk & 1) * 8;
       bf16x8 ph, pl;
 #pragma unroll
       for (int slot = 0; slot < 8; ++slot) {
-        const float s_value = st[kt][e0 + slot];
-        const float p = s_value == -INFINITY ? 0.0F : expf(s_value - new_max);
+        const float p = __builtin_amdgcn_exp2f(st[kt][e0 + slot] - base);
         partial_sum += p;
         const __bf16 h = static_cast<__bf16>(p);
         ph[slot] = h;
         pl[slot] = static_cast<__bf16>(p - static_cast<float>(h));
       }
-      // keys of this k-step for this lane: base + {0..3} and base + 8 + {0..3}
-      const int key_base = kt * 32 + (e0 >> 2) * 8 + half * 4;
 #pragma unroll
       for (int t = 0; t < kDTiles; ++t) {
         const int d = t * 32 + col;
-        const uint16_t *vh_row = &v_s[0][d * kVStride + key_base];
-        const uint16_t *vl_row = &v_s[1][d * kVStride + key_base];
-        const uint2 h0 = *reinterpret_cast<const uint2 *>(vh_row);
-        const uint2 h1 = *reinterpret_cast<const uint2 *>(vh_row + 8);
-        const uint2 l0 = *reinterpret_cast<const uint2 *>(vl_row);
-        const uint2 l1 = *reinterpret_cast<const uint2 *>(vl_row + 8);
-        const uint4 hv = make_uint4(h0.x, h0.y, h1.x, h1.y);
-        const uint4 lv = make_uint4(l0.x, l0.y, l1.x, l1.y);
-        const bf16x8 vh = __builtin_bit_cast(bf16x8, hv);
-        const bf16x8 vl = __builtin_bit_cast(bf16x8, lv);
+        const int off = (d * 8 + swizzle<8>(d, 2 * kk + half)) * 8;
+        const bf16x8 vh = *reinterpret_cast<const bf16x8 *>(v_hi + off);
+        const bf16x8 vl = *reinterpret_cast<const bf16x8 *>(v_lo + off);
         o_acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vh, ph, o_acc[t], 0, 0, 0);
         o_acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vh, pl, o_acc[t], 0, 0, 0);
         o_acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vl, ph, o_acc[t], 0, 0, 0);
@@ -241,8 +354,8 @@ __global__ __launch_bounds__(256) void flash_attention_kernel(
 template <int kDim, typename O>  // head_dim, output type
 __global__ __launch_bounds__(256) void attention_kernel(
     const uint16_t *__restrict__ q, size_t q_plane, const uint16_t *__restrict__ k_cache,
-    const uint16_t *__restrict__ v_cache, size_t cache_plane, size_t rows, size_t prefix,
-    size_t heads, O out) {
+    const uint16_t *__restrict__ v_cache, size_t cache_plane, size_t capacity, size_t rows,
+    size_t prefix, size_t heads, O out) {
   constexpr int kQ = 64, kTile = 64, kPart = kDim / 4;
   __shared__ float k_s[kTile * kDim];
   __shared__ float v_s[kTile * kDim];
@@ -271,7 +384,9 @@ __global__ __launch_bounds__(256) void attention_kernel(
       const size_t g = (k0 + key) * width + head * kDim + d;
       const bool ok = k0 + key < keys_needed;
       k_s[i] = ok ? get_split(k_cache, k_cache + cache_plane, g) : 0.0F;
-      v_s[i] = ok ? get_split(v_cache, v_cache + cache_plane, g) : 0.0F;
+      v_s[i] = ok ? get_split(v_cache, v_cache + cache_plane,
+                              (head * kDim + d) * capacity + vt_column(k0 + key))
+                  : 0.0F;
     }
     __syncthreads();
     float scores[kTile];
@@ -312,35 +427,47 @@ __global__ __launch_bounds__(256) void attention_kernel(
   }
 }
 
+template <int kD, typename O>
+Status launch_flash(const uint16_t *q, size_t q_plane, const uint16_t *k_cache,
+                    const uint16_t *v_cache, size_t cache_plane, size_t capacity, size_t rows,
+                    size_t prefix, size_t heads, O out, hipStream_t stream) {
+  constexpr size_t lds = FlashShape<kD>::kLdsBytes;
+  static_assert(lds <= 160 * 1024, "LDS");
+  auto kernel = flash_attention_kernel<kD, O>;
+  EVO_TRY(hip_status(hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         static_cast<int>(lds)),
+                     "flash_attention_kernel LDS opt-in"));
+  const size_t blocks = ceil_div(rows, 4 * kQueriesPerWave) * heads;
+  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), lds, stream, q,
+                     q_plane, k_cache, v_cache, cache_plane, capacity, rows, prefix, heads, out);
+  return launch_status("flash_attention_kernel");
+}
+
 template <typename O>
 Status launch_attention(const uint16_t *q, size_t q_plane, const uint16_t *k_cache,
-                        const uint16_t *v_cache, size_t cache_plane, size_t rows,
-                        size_t prefix, size_t heads, size_t head_dim, O out,
+                        const uint16_t *v_cache, size_t cache_plane, size_t capacity,
+                        size_t rows, size_t prefix, size_t heads, size_t head_dim, O out,
                         hipStream_t stream) {
-  const dim3 mfma_grid(ceil_div(rows, 4 * kQueriesPerWave), static_cast<unsigned>(heads));
   switch (head_dim) {
   case 16:
     hipLaunchKernelGGL((attention_kernel<16, O>), dim3(ceil_div(rows, 64), heads), dim3(256),
-                       0, stream, q, q_plane, k_cache, v_cache, cache_plane, rows, prefix,
-                       heads, out);
+                       0, stream, q, q_plane, k_cache, v_cache, cache_plane, capacity, rows,
+                       prefix, heads, out);
     return launch_status("attention_kernel");
   case 32:
-    hipLaunchKernelGGL((flash_attention_kernel<32, O>), mfma_grid, dim3(256), 0, stream, q,
-                       q_plane, k_cache, v_cache, cache_plane, rows, prefix, heads, out);
-    break;
+    return launch_flash<32, O>(q, q_plane, k_cache, v_cache, cache_plane, capacity, rows,
+                               prefix, heads, out, stream);
   case 64:
-    hipLaunchKernelGGL((flash_attention_kernel<64, O>), mfma_grid, dim3(256), 0, stream, q,
-                       q_plane, k_cache, v_cache, cache_plane, rows, prefix, heads, out);
-    break;
+    return launch_flash<64, O>(q, q_plane, k_cache, v_cache, cache_plane, capacity, rows,
+                               prefix, heads, out, stream);
   case 128:
-    hipLaunchKernelGGL((flash_attention_kernel<128, O>), mfma_grid, dim3(256), 0, stream, q,
-                       q_plane, k_cache, v_cache, cache_plane, rows, prefix, heads, out);
-    break;
+    return launch_flash<128, O>(q, q_plane, k_cache, v_cache, cache_plane, capacity, rows,
+                                prefix, heads, out, stream);
   default:
     return {ErrorCode::kUnsupported,
             "causal_attention: head_dim must be 16, 32, 64 or 128"};
   }
-  return launch_status("flash_attention_kernel");
 }
 
 }  // namespace
@@ -348,34 +475,40 @@ Status launch_attention(const uint16_t *q, size_t q_plane, const uint16_t *k_cac
 Status qkv_rope(const float *projected, size_t rows, size_t width, size_t heads,
                 bool column_split, const float *inv_freq, float rope_scale,
                 size_t prefix, uint16_t *q, size_t q_plane, uint16_t *k_cache,
-                uint16_t *v_cache, size_t cache_plane, hipStream_t stream) {
+                uint16_t *v_cache, size_t cache_plane, size_t capacity, hipStream_t stream) {
   if (projected == nullptr || inv_freq == nullptr || q == nullptr ||
       k_cache == nullptr || v_cache == nullptr || rows == 0 || heads == 0 ||
       width % heads != 0 || (width / heads) % 2 != 0 || !(rope_scale > 0.0F) ||
-      q_plane < rows * width || cache_plane < (prefix + rows) * width)
+      q_plane < rows * width || capacity % kKeys != 0 || prefix + rows > capacity ||
+      cache_plane < capacity * width)
     return {ErrorCode::kInvalidArgument, "qkv_rope: invalid arguments"};
   const size_t n = rows * heads * (width / heads / 2);
   const unsigned grid = static_cast<unsigned>(std::min<size_t>((n + 255) / 256, 16384));
   hipLaunchKernelGGL(qkv_rope_kernel, dim3(grid), dim3(256), 0, stream, projected, rows,
                      width, heads, width / heads, column_split ? 1 : 0, inv_freq,
-                     rope_scale, prefix, q, q_plane, k_cache, v_cache, cache_plane);
-  return launch_status("qkv_rope_kernel");
+                     rope_scale, prefix, q, q_plane, k_cache, cache_plane);
+  EVO_TRY(launch_status("qkv_rope_kernel"));
+  hipLaunchKernelGGL(v_transpose_kernel, dim3(ceil_div(rows, 64), ceil_div(width, 64)),
+                     dim3(256), 0, stream, projected, rows, width, width / heads,
+                     column_split ? 1 : 0, prefix, v_cache, cache_plane, capacity);
+  return launch_status("v_transpose_kernel");
 }
 
 Status causal_attention(const uint16_t *q, size_t q_plane, const uint16_t *k_cache,
-                        const uint16_t *v_cache, size_t cache_plane, size_t rows,
-                        size_t prefix, size_t heads, size_t head_dim, float *out_f32,
-                        uint16_t *out_hi, uint16_t *out_lo, hipStream_t stream) {
+                        const uint16_t *v_cache, size_t cache_plane, size_t capacity,
+                        size_t rows, size_t prefix, size_t heads, size_t head_dim,
+                        float *out_f32, uint16_t *out_hi, uint16_t *out_lo,
+                        hipStream_t stream) {
   if (q == nullptr || k_cache == nullptr || v_cache == nullptr ||
       (out_f32 == nullptr && out_hi == nullptr) || rows == 0 || heads == 0 ||
-      heads > 65535 || q_plane < rows * heads * head_dim ||
-      cache_plane < (prefix + rows) * heads * head_dim)
+      heads > 65535 || q_plane < rows * heads * head_dim || capacity % kKeys != 0 ||
+      prefix + rows > capacity || cache_plane < capacity * heads * head_dim)
     return {ErrorCode::kInvalidArgument, "causal_attention: invalid arguments"};
   if (out_f32 != nullptr)
-    return launch_attention(q, q_plane, k_cache, v_cache, cache_plane, rows, prefix, heads,
-                            head_dim, out_f32, stream);
-  return launch_attention(q, q_plane, k_cache, v_cache, cache_plane, rows, prefix, heads,
-                          head_dim, SplitOut{out_hi, out_lo}, stream);
+    return launch_attention(q, q_plane, k_cache, v_cache, cache_plane, capacity, rows, prefix,
+                            heads, head_dim, out_f32, stream);
+  return launch_attention(q, q_plane, k_cache, v_cache, cache_plane, capacity, rows, prefix,
+                          heads, head_dim, SplitOut{out_hi, out_lo}, stream);
 }
 
 }  // namespace evo::hip

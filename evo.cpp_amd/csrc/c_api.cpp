@@ -708,16 +708,17 @@ evo_status evo_hip_attention(const float *projected, size_t rows, size_t width, 
                              void *stream) {
   return protect([&]() -> evo_status {
     const auto s = static_cast<hipStream_t>(stream);
-    if (prefix + rows > capacity)
+    if (prefix + rows > capacity || capacity % 64 != 0)
       return publish(EVO_STATUS_INVALID_ARGUMENT,
-                     "invalid_argument: attention rows exceed the cache capacity");
+                     "invalid_argument: attention rows exceed the cache capacity, or the "
+                     "capacity is not a multiple of 64");
     auto status = evo::hip::qkv_rope(projected, rows, width, heads, column_split != 0,
                                      inv_freq, rope_scale, prefix, query, rows * width,
-                                     key_cache, value_cache, capacity * width, s);
+                                     key_cache, value_cache, capacity * width, capacity, s);
     if (!status.ok())
       return publish(status);
     return publish(evo::hip::causal_attention(query, rows * width, key_cache, value_cache,
-                                              capacity * width, rows, prefix, heads,
+                                              capacity * width, capacity, rows, prefix, heads,
                                               heads == 0 ? 0 : width / heads, out, nullptr,
                                               nullptr, s));
   });

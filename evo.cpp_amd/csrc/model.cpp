@@ -331,6 +331,7 @@ Status Context::initialize(std::shared_ptr<const Model> model, size_t capacity,
     return {ErrorCode::kInvalidArgument,
             "invalid_argument: context requires a valid capacity"};
   capacity_ = capacity;
+  cache_capacity_ = (capacity + 63) / 64 * 64;
   arena_rows_ = std::min(capacity, kArenaRows);
   // Test hook: a smaller activation arena forces multi-chunk prefill.
   if (const char *rows = std::getenv("EVO_HIP_ARENA_ROWS")) {
@@ -371,9 +372,15 @@ Status Context::initialize(std::shared_ptr<const Model> model, size_t capacity,
     const Layer &L = model_->layer[i];
     Cache &k = cache_[i];
     if (L.type == Mixer::kAttention) {
-      // split BF16 planes [2][capacity][W]
-      EVO_TRY(k.keys.allocate(capacity * w * 4, "key cache"));
-      EVO_TRY(k.values.allocate(capacity * w * 4, "value cache"));
+      // split BF16 planes: K [2][capacity][W], V^T [2][W][capacity] with the
+      // capacity rounded up to whole 64-key tiles; zeroed once so that tile
+      // entries past the last written key are finite.
+      EVO_TRY(k.keys.allocate(cache_capacity_ * w * 4, "key cache"));
+      EVO_TRY(k.values.allocate(cache_capacity_ * w * 4, "value cache"));
+      EVO_TRY(hip_check(hipMemsetAsync(k.keys.as<void>(), 0, k.keys.bytes(), stream_),
+                        "key cache"));
+      EVO_TRY(hip_check(hipMemsetAsync(k.values.as<void>(), 0, k.values.bytes(), stream_),
+                        "value cache"));
       continue;
     }
     EVO_TRY(k.short_history.allocate((c.short_len - 1) * 3 * w * 4, "short FIR cache"));
@@ -434,12 +441,13 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
     }
     if (L.type == Mixer::kAttention) {
       uint16_t *query = query_.as<uint16_t>();
-      const size_t cache_plane = capacity_ * w;
+      const size_t cache_plane = cache_capacity_ * w;
       EVO_TRY(qkv_rope(projected, rows, w, c.heads, c.column_split, L.inv_freq.as<float>(),
                        c.rope_scale, position_, query, rows * w, k.keys.as<uint16_t>(),
-                       k.values.as<uint16_t>(), cache_plane, stream_));
+                       k.values.as<uint16_t>(), cache_plane, cache_capacity_, stream_));
       EVO_TRY(causal_attention(query, rows * w, k.keys.as<uint16_t>(),
-                               k.values.as<uint16_t>(), cache_plane, rows, position_,
+                               k.values.as<uint16_t>(), cache_plane, cache_capacity_, rows,
+                               position_,
                                c.heads, c.head_dim(), nullptr, mixed_out.hi, mixed_out.lo,
                                stream_));
     } else {

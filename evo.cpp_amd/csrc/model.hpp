@@ -138,7 +138,7 @@ private:
   ContextOptions options_;
   std::string profile_;
   hipStream_t stream_{nullptr};
-  size_t capacity_{0}, arena_rows_{0}, position_{0};
+  size_t capacity_{0}, cache_capacity_{0}, arena_rows_{0}, position_{0};
   bool valid_{false};
   DeviceBuffer tokens_, hidden_, residual_, normed_, projected_, mixed_, query_,
       gated_, logits_, codes_, workspace_, flag_;

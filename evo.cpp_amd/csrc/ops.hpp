@@ -118,18 +118,23 @@ Status hyena_forward(int kind, const T *projection, size_t length,
 
 // ---- Attention (attention.hip). Q and the K/V caches are split BF16 planes:
 // plane 0 (hi) at the pointer, plane 1 (lo) `*_plane` elements further.
+// The key cache is [capacity][W]; the value cache is transposed, V^T
+// [W][capacity], each 16-position block stored in the order 0-3, 8-11, 4-7,
+// 12-15 (bits 2 and 3 of the position swapped). capacity is a multiple of
+// 64 and cache rows never written must hold finite values (zero them once).
 // qkv_rope splits the QKV projection [rows, 3W] into rotated Q, rotated K and
-// V, appending K/V rows at position `prefix` of the caches [capacity, W].
+// V, appending K/V at position `prefix` of the caches.
 Status qkv_rope(const float *projected, size_t rows, size_t width, size_t heads,
                 bool column_split, const float *inv_freq, float rope_scale,
                 size_t prefix, uint16_t *q, size_t q_plane, uint16_t *k_cache,
-                uint16_t *v_cache, size_t cache_plane, hipStream_t stream);
+                uint16_t *v_cache, size_t cache_plane, size_t capacity, hipStream_t stream);
 // Causal attention of `rows` queries at positions prefix.. against keys
 // [0, prefix + rows). Layout [time, heads, head_dim] = [time, W]. Output F32
 // (out_f32) or split planes (out_hi, out_lo).
 Status causal_attention(const uint16_t *q, size_t q_plane, const uint16_t *k_cache,
-                        const uint16_t *v_cache, size_t cache_plane, size_t rows,
-                        size_t prefix, size_t heads, size_t head_dim, float *out_f32,
-                        uint16_t *out_hi, uint16_t *out_lo, hipStream_t stream);
+                        const uint16_t *v_cache, size_t cache_plane, size_t capacity,
+                        size_t rows, size_t prefix, size_t heads, size_t head_dim,
+                        float *out_f32, uint16_t *out_hi, uint16_t *out_lo,
+                        hipStream_t stream);
 
 }  // namespace evo::hip

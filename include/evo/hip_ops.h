@@ -146,7 +146,10 @@ EVO_API evo_status evo_hip_rms_norm(const float *x, size_t rows, size_t width,
 /* Attention block body: split the Wqkv output [rows, 3W], apply RoPE at
  * positions prefix.., append K/V at `prefix` of the caches, causal softmax
  * attention into out [rows, W] F32. query is workspace of 2*rows*W uint16;
- * key_cache / value_cache hold split BF16 planes [2][capacity][W] uint16.
+ * key_cache holds split BF16 planes [2][capacity][W] uint16 and value_cache
+ * the transposed planes [2][W][capacity], each 16-position block stored in
+ * the order 0-3, 8-11, 4-7, 12-15. capacity must be a multiple of 64, and
+ * cache entries never written must hold finite values (zero the caches once).
  * Replaces `bf16_split_qkv` + `bf16_apply_rope` + `bf16_kv_append` +
  * `bf16_online_causal_attention` (`include/evo/cuda/attention.hpp:100-133`). */
 EVO_API evo_status evo_hip_attention(const float *projected, size_t rows,

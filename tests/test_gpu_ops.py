@@ -400,11 +400,30 @@ def test_attention_matches_oracle(oracle, rows, heads, head_dim, prefix):
     O.check(oracle.oracle_causal_attention(O.ptr(q), O.ptr(k), O.ptr(v), total, heads,
                                            head_dim, O.ptr(expected)))
     expected = expected.reshape(total, width)[prefix:]
-    kc, vc = zeros((2, total, width), np.uint16), zeros((2, total, width), np.uint16)
+    capacity = (total + 63) // 64 * 64  # whole 64-key tiles
+    kc, vc = zeros((2, capacity, width), np.uint16), zeros((2, width, capacity), np.uint16)
     query, out = empty((2, total, width), np.uint16), empty((total, width))
     if prefix:
         N.call("evo_hip_attention", p(dev(proj[:prefix])), prefix, width, heads, 1,
-               p(dev(inv_freq)), 8.0, 0, p(query), p(kc), p(vc), total, p(out), stream())
+               p(dev(inv_freq)), 8.0, 0, p(query), p(kc), p(vc), capacity, p(out), stream())
     N.call("evo_hip_attention", p(dev(proj[prefix:])), rows, width, heads, 1,
-           p(dev(inv_freq)), 8.0, prefix, p(query), p(kc), p(vc), total, p(out), stream())
+           p(dev(inv_freq)), 8.0, prefix, p(query), p(kc), p(vc), capacity, p(out), stream())
     assert rel_err(host(out)[:rows], expected) < 1e-5
+    # value cache layout: V^T planes, positions permuted inside 16-blocks
+    vt = bf16_to_f32(host(vc))
+    v_rows = v.reshape(total, width)
+    pos = np.arange(total)
+    column = (pos & ~15) | (pos & 3) | ((pos & 4) << 1) | ((pos & 8) >> 1)
+    stored = vt[0][:, column].T + vt[1][:, column].T
+    assert np.abs(stored - v_rows).max() <= 2.0 ** -16 * np.abs(v_rows).max()
+
+
+def test_attention_rejects_unaligned_capacity():
+    width, heads = 64, 2
+    proj = zeros((4, 3 * width))
+    inv = dev(np.ones(16, np.float32))
+    kc, vc = zeros((2, 70, width), np.uint16), zeros((2, width, 70), np.uint16)
+    query, out = empty((2, 4, width), np.uint16), empty((4, width))
+    with pytest.raises(N.OpError, match="multiple of 64"):
+        N.call("evo_hip_attention", p(proj), 4, width, heads, 1, p(inv), 1.0, 0, p(query),
+               p(kc), p(vc), 70, p(out), stream())
