@@ -13,16 +13,13 @@
 // product carries ~16 significant bits of the activation (relative error
 // ~2^-17) for twice the MFMA work; without lo (profile hip-bf16) one pass.
 //
-// Tiling for CDNA4: 256 threads = 4 waves as 2 (M) x 2 (N); block tile
-// 256 x 256, K step 32; each wave owns 128 x 128 = 4 x 4 MFMA 32x32x16 tiles
-// (256 F32 accumulators per lane, held in AGPRs at one wave per SIMD). The
-// large wave tile keeps LDS traffic at 12 KB per 32 MFMAs per wave, well
-// under the CU's LDS bandwidth (a 64 x 128 wave tile needs twice that and
-// saturates it). Operands are staged through LDS with 16-byte loads into
-// rows padded to 40 BF16 (80 B), double-buffered so one barrier per K step
-// separates the prefetch of step k+1 from the MFMAs of step k; within a K
-// step the hi-plane sweep and the lo-plane sweep each issue 16 independent
-// MFMAs.
+// Tiling for CDNA4: block tile 256 x 256, K step 32. The main kernel runs
+// 512 threads = 8 waves as 2 (M) x 4 (N), each owning 128 x 64 = 4 x 2 MFMA
+// 32x32x16 tiles (128 F32 accumulators per lane), two waves per SIMD so one
+// wave's MFMAs cover the other's LDS reads and barrier waits. Operands reach
+// LDS by DMA (global_load_lds_dwordx4) into XOR-swizzled, unpadded rows,
+// triple-buffered. The fallback kernel (K % 32 != 0) runs 4 waves of
+// 128 x 128 with register-staged, padded LDS rows.
 // Tiles are renumbered so that each of the 8 XCDs (own L2) receives a
 // contiguous band of the tile grid, walked in groups of 8 tile-rows.
 #include "common.hpp"
@@ -301,7 +298,7 @@ __device__ inline int swizzled_unit(int row, int seg) {
 }
 
 template <bool kSplit>
-__global__ __launch_bounds__(kThreads) void gemm_kernel(
+__global__ __launch_bounds__(512) void gemm_kernel(
     const uint16_t *__restrict__ a_hi, const uint16_t *__restrict__ a_lo, int lda,
     const uint16_t *__restrict__ W, int M, int N, int K, float *__restrict__ C,
     uint16_t *__restrict__ c_hi, uint16_t *__restrict__ c_lo, int ldc,
@@ -313,18 +310,18 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wave_m = wave >> 1;  // 0..1
-  const int wave_n = wave & 1;   // 0..1
+  const int wave_m = wave >> 2;  // 0..1
+  const int wave_n = wave & 3;   // 0..3
   const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
   int tm, tn;
   tile_of(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
   const int block_m = tm * kBM, block_n = tn * kBN;
 
   // This lane's four DMA rows (instructions t = wave*4 + i) and segments.
-  const uint16_t *src_a_hi[4], *src_a_lo[4], *src_w[4];
+  const uint16_t *src_a_hi[2], *src_a_lo[2], *src_w[2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int t = wave * 4 + i;
+  for (int i = 0; i < 2; ++i) {
+    const int t = wave * 2 + i;
     const int r = 16 * t + (lane >> 2);
     const int seg = (lane & 3) ^ ((r >> 2) & 3);
     const int ar = min(block_m + r, M - 1), wr = min(block_n + r, N - 1);
@@ -336,8 +333,8 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(
     uint16_t *stage = lds + (step % kStages) * kStage;
     const int k0 = step * kBK;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int unit0 = (wave * 4 + i) * 64;  // first unit of this instruction
+    for (int i = 0; i < 2; ++i) {
+      const int unit0 = (wave * 2 + i) * 64;  // first unit of this instruction
       dma16(src_a_hi[i] + k0, stage + unit0 * 8);
       if (kSplit)
         dma16(src_a_lo[i] + k0, stage + kPlane + unit0 * 8);
@@ -345,11 +342,11 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(
     }
   };
 
-  f32x16 acc[4][4];
+  f32x16 acc[4][2];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e)
         acc[i][j][e] = 0.0F;
@@ -363,9 +360,9 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(
     // flight), then for every wave's.
     if (s + 1 < steps) {
       if (kSplit)
-        asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+        asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
       else
-        asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
     } else {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
@@ -378,13 +375,13 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(
     const uint16_t *sw = stage + (kPlanes - 1) * kPlane;
     // Fragments of both 16-wide K halves; the reads of half 1 are issued
     // before the MFMAs of half 0 so their latency hides behind them.
-    bf16x8 b[2][4], ah[2][4], al[2][4];
+    bf16x8 b[2][2], ah[2][4], al[2][4];
     auto read = [&](int ks) {
       const int seg = 2 * ks + (lane >> 5);
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < 2; ++j)
         b[ks][j] = *reinterpret_cast<const bf16x8 *>(
-            sw + swizzled_unit(wave_n * 128 + j * 32 + (lane & 31), seg) * 8);
+            sw + swizzled_unit(wave_n * 64 + j * 32 + (lane & 31), seg) * 8);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         ah[ks][i] = *reinterpret_cast<const bf16x8 *>(
@@ -400,13 +397,13 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < 2; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[ks][i], b[ks][j], acc[i][j], 0, 0, 0);
       if (kSplit) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
+          for (int j = 0; j < 2; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[ks][i], b[ks][j], acc[i][j], 0, 0, 0);
       }
     };
@@ -419,20 +416,20 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(
     multiply(1);
   }
 
-  const int wave_col = block_n + wave_n * 128;
+  const int wave_col = block_n + wave_n * 64;
   const int wave_row = block_m + wave_m * 128 + (lane >> 5) * 4;
   if (epi.mode == kGemmGated) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int pair = 0; pair < 2; ++pair)
+      for (int pair = 0; pair < 1; ++pair)
         store_gated(acc[i][2 * pair], acc[i][2 * pair + 1], wave_row + i * 32,
                     wave_col / 2 + pair * 32 + (lane & 31), M, ldc, epi, c_hi, c_lo);
   } else {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < 2; ++j)
         store_tile(acc[i][j], wave_row + i * 32, wave_col + j * 32 + (lane & 31), M, N, ldc,
                    epi, C);
   }
@@ -491,10 +488,10 @@ Status gemm_bf16w(const Activation &a, const uint16_t *W, const GemmOutput &out,
   const int lda = static_cast<int>(a.ld), ldc = static_cast<int>(out.ld);
   if (K % kBK == 0) {
     if (split)
-      hipLaunchKernelGGL(gemm_kernel<true>, grid, dim3(kThreads), 0, stream, a.hi, a.lo, lda,
+      hipLaunchKernelGGL(gemm_kernel<true>, grid, dim3(512), 0, stream, a.hi, a.lo, lda,
                          W, m, n, k, out.f32, out.hi, out.lo, ldc, epi);
     else
-      hipLaunchKernelGGL(gemm_kernel<false>, grid, dim3(kThreads), 0, stream, a.hi, a.lo, lda,
+      hipLaunchKernelGGL(gemm_kernel<false>, grid, dim3(512), 0, stream, a.hi, a.lo, lda,
                          W, m, n, k, out.f32, out.hi, out.lo, ldc, epi);
     return launch_status("gemm_kernel");
   }
