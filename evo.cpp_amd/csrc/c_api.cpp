@@ -370,13 +370,37 @@ evo_status evo_context_prefill(evo_context *context, const evo_batch *batch,
   });
 }
 
-evo_status evo_context_decode(evo_context *context, uint32_t, evo_logits_callback,
-                              void *) {
+// One cached step: the token at position `offset` runs through every block
+// as a one-row continuation (FIR histories, HCL modal state and K/V caches
+// advance), and its logits go to the callback (`src/c_api.cpp:1000-1082`,
+// StripedHyena2 decode = forward({token}) on the caches,
+// `src/cpu/model.cpp:3475-3483`).
+evo_status evo_context_decode(evo_context *context, uint32_t token,
+                              evo_logits_callback callback, void *user_data) {
   return protect([&]() -> evo_status {
-    if (context == nullptr)
+    if (context == nullptr || callback == nullptr)
       return publish(EVO_STATUS_INVALID_ARGUMENT, "invalid_argument: decode argument is null");
-    return publish(EVO_STATUS_UNSUPPORTED,
-                   "unsupported: the HIP prefill library does not implement decode");
+    if (context->failed)
+      return publish(EVO_STATUS_INVALID_ARGUMENT,
+                     "invalid_argument: context is invalid after a prior failure");
+    const size_t offset = context->hip->position();
+    const auto &config = context->hip->config();
+    if (offset == 0 || offset >= context->hip->capacity() || token >= config.vocab)
+      return publish(EVO_STATUS_INVALID_ARGUMENT,
+                     "invalid_argument: decode token/context is invalid");
+    context->failed = true;
+    std::vector<float> logits(config.vocab);
+    const auto status = context->hip->forward(&token, 1, false, logits.data(),
+                                              std::numeric_limits<size_t>::max(), nullptr);
+    if (!status.ok())
+      return publish(status);
+    const evo_status callback_status = callback(logits.data(), 1, config.vocab, offset,
+                                                user_data);
+    if (callback_status != EVO_STATUS_OK)
+      return publish(valid_status(callback_status) ? callback_status : EVO_STATUS_INTERNAL,
+                     "callback: logits consumer aborted HIP decode");
+    context->failed = false;
+    return publish(evo::Status::Ok());
   });
 }
 

@@ -89,6 +89,8 @@ class EvoLibrary:
         lib.evo_context_profile.restype = ctypes.c_char_p
         lib.evo_context_prefill.argtypes = [ctypes.c_void_p, ctypes.c_void_p,
                                             LOGITS_CALLBACK, ctypes.c_void_p]
+        lib.evo_context_decode.argtypes = [ctypes.c_void_p, ctypes.c_uint32,
+                                           LOGITS_CALLBACK, ctypes.c_void_p]
         lib.evo_batch_create.argtypes = [ctypes.c_size_t,
                                          ctypes.POINTER(ctypes.c_void_p)]
         lib.evo_batch_free.argtypes = [ctypes.c_void_p]
@@ -192,3 +194,17 @@ class Context:
         if not chunks:
             return np.zeros((0, self.model.vocab), dtype=np.float32)
         return np.concatenate(chunks, axis=0)
+
+    def decode(self, token: int) -> np.ndarray:
+        """One cached decode step; returns the [vocab] F32 logits of `token`
+        at the current position."""
+        lib = self.model.library.lib
+        rows: List[np.ndarray] = []
+
+        def callback(logits, count, columns, offset, _user):
+            rows.append(np.ctypeslib.as_array(logits, shape=(count, columns)).copy())
+            return 0
+
+        c_callback = LOGITS_CALLBACK(callback)
+        self.model.library.check(lib.evo_context_decode(self.handle, token, c_callback, None))
+        return rows[0][0]

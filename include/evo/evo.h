@@ -197,7 +197,9 @@ EVO_API evo_status evo_context_prefill(evo_context *context,
                                        const evo_batch *batch,
                                        evo_logits_callback callback,
                                        void *user_data);
-/* Decode is outside this library's hot path: returns EVO_STATUS_UNSUPPORTED. */
+/* One cached decode step after a prefill: the token at position
+ * evo_context_position() advances every cache and its [1, vocab] logits go
+ * to the callback (reference `include/evo/evo.h:183-186`). */
 EVO_API evo_status evo_context_decode(evo_context *context, uint32_t token,
                                       evo_logits_callback callback,
                                       void *user_data);

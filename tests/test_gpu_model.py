@@ -136,3 +136,74 @@ def test_evo2_1b_shape_config1(hip, tmp_path):
     actual, _ = run_hip(hip, path, tokens)
     assert relmax(actual, expected) <= TOL
     assert np.array_equal(actual.argmax(1), expected.argmax(1))
+
+
+def open_context(hip, path, capacity, flags=0):
+    import ctypes
+    model = hip.load(path, capi.BACKEND_HIP)
+    params = hip.lib.evo_context_default_params()
+    params.context_size = capacity
+    params.flags = flags
+    handle = ctypes.c_void_p()
+    hip.check(hip.lib.evo_context_create(model.handle, ctypes.byref(params),
+                                         ctypes.byref(handle)))
+    return capi.Context(model, handle)
+
+
+@pytest.mark.parametrize("groups,heads", [(16, 2), (4, 2), (16, 4)])
+def test_decode_matches_prefill_logits(hip, tmp_path, groups, heads):
+    """Prefill n tokens, then decode the rest one at a time: each decode row
+    equals the oracle's full-sequence prefill row at that position (groups=4
+    gives 16-channel filter groups, the MFMA FIR; heads 2/4 the MFMA/VALU
+    attention)."""
+    shape = A.tiny_shape(width=64, layers=8, heads=heads, inner=96, groups=groups, attn=(3,))
+    path = make(tmp_path, shape, seed=31 + groups)
+    tokens = A.acgt_tokens(96, seed=groups)
+    expected = O.OracleModel(path).prefill(tokens)
+    ctx = open_context(hip, path, capacity=100)
+    first = 80
+    logits = ctx.prefill(tokens[:first].astype(np.uint8).tobytes())
+    assert relmax(logits, expected[:first]) <= TOL
+    for t in range(first, len(tokens)):
+        row = ctx.decode(int(tokens[t]))
+        assert ctx.position == t + 1
+        assert relmax(row, expected[t]) <= TOL
+        assert row.argmax() == expected[t].argmax()
+
+
+def test_greedy_generation_matches_oracle(hip, tmp_path):
+    """Greedy loop (argmax, lowest index on ties) through decode: the
+    generated bytes equal the oracle's greedy continuation."""
+    shape = A.tiny_shape(width=64, layers=8, heads=2, inner=96, groups=4, attn=(3,))
+    path = make(tmp_path, shape, seed=41)
+    prompt = A.acgt_tokens(40, seed=9)
+    oracle = O.OracleModel(path)
+    sequence = list(prompt)
+    for _ in range(12):
+        sequence.append(int(oracle.prefill(np.array(sequence, np.uint32))[-1].argmax()))
+    ctx = open_context(hip, path, capacity=64)
+    generated = list(prompt)
+    nxt = int(ctx.prefill(prompt.astype(np.uint8).tobytes())[-1].argmax())
+    for _ in range(12):
+        generated.append(nxt)
+        nxt = int(ctx.decode(nxt).argmax())
+    assert generated == sequence
+
+
+def test_decode_argument_errors(hip, tmp_path):
+    shape = A.tiny_shape(width=64, layers=8, heads=2, inner=96, groups=4, attn=(3,))
+    path = make(tmp_path, shape, seed=43)
+    ctx = open_context(hip, path, capacity=8)
+    with pytest.raises(capi.EvoError) as fresh:
+        ctx.decode(65)  # nothing prefilled yet
+    assert fresh.value.status == 2
+    ctx.prefill(bytes(A.acgt_tokens(8, seed=1).astype(np.uint8)))
+    with pytest.raises(capi.EvoError) as full:
+        ctx.decode(65)  # capacity reached
+    assert full.value.status == 2
+    ctx = open_context(hip, path, capacity=16)
+    ctx.prefill(bytes(A.acgt_tokens(4, seed=1).astype(np.uint8)))
+    with pytest.raises(capi.EvoError) as vocab:
+        ctx.decode(512)
+    assert vocab.value.status == 2
+    assert ctx.decode(71).shape == (512,)  # a rejected call leaves the context usable
