@@ -165,6 +165,9 @@ def main():
     parser.add_argument("--cpu-sample", type=int, default=16)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-kernels", action="store_true")
+    parser.add_argument("--long-tokens", type=int, default=131072,
+                        help="config 5: one chunked prefill of this many tokens (0 = skip)")
+    parser.add_argument("--decode-steps", type=int, default=32)
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build runs on one "
@@ -218,6 +221,49 @@ def main():
     cabi_rate = args.tokens / (time.perf_counter() - start)
     ctx2.close()
 
+    # Cached decode after a 1024-token prefill (C ABI, host logits per step).
+    decode_rate = None
+    if args.decode_steps > 0:
+        log(f"timing {args.decode_steps} decode steps after a 1024-token prefill")
+        ctx3 = model.context(1024 + args.decode_steps + 8)
+        token = int(ctx3.prefill(A.acgt_tokens(1024, seed=3).astype(np.uint8)
+                                 .tobytes())[-1].argmax())
+        for _ in range(4):
+            token = int(ctx3.decode(token).argmax())
+        start = time.perf_counter()
+        for _ in range(args.decode_steps):
+            token = int(ctx3.decode(token).argmax())
+        decode_rate = args.decode_steps / (time.perf_counter() - start)
+        ctx3.close()
+
+    # Config 5: one long prefill, chunked through the 8192-row arena.
+    long_result = None
+    if args.long_tokens > 0:
+        log(f"timing one chunked prefill of {args.long_tokens} tokens")
+        lparams = hip.lib.evo_context_default_params()
+        lparams.context_size = args.long_tokens
+        lparams.flags = params.flags
+        lhandle = ctypes.c_void_p()
+        hip.check(hip.lib.evo_context_create(model.handle, ctypes.byref(lparams),
+                                             ctypes.byref(lhandle)))
+        lctx = capi.Context(model, lhandle)
+        ltokens = torch.from_numpy(A.acgt_tokens(args.long_tokens, seed=5)
+                                   .astype(np.int32)).cuda()
+        llogits = torch.empty(args.long_tokens, shape.vocab, device="cuda")
+        torch.cuda.synchronize()
+        start = time.perf_counter()
+        status = lib.evo_hip_context_prefill_resident(lhandle, ltokens.data_ptr(),
+                                                     args.long_tokens, llogits.data_ptr())
+        torch.cuda.synchronize()
+        seconds = time.perf_counter() - start
+        if status != 0:
+            raise RuntimeError(lib.evo_last_error().decode())
+        long_result = {"tokens": args.long_tokens, "seconds": round(seconds, 3),
+                       "tok_s": round(args.long_tokens / seconds, 1),
+                       "chunk_rows": 8192, "finite": bool(torch.isfinite(llogits).all())}
+        lctx.close()
+        del ltokens, llogits
+
     result = {
         "metric": METRIC, "value": round(value, 1), "unit": "tok/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 3),
@@ -231,7 +277,9 @@ def main():
                    "heads": shape.heads, "ffn": shape.inner,
                    "profile": context.profile, "tok_s_1k": round(rate_1k, 1),
                    "ms_per_step_1k": round(ms_1k, 3),
-                   "c_abi_host_logits_tok_s": round(cabi_rate, 1)},
+                   "c_abi_host_logits_tok_s": round(cabi_rate, 1),
+                   "decode_tok_s_after_1k": round(decode_rate, 1) if decode_rate else None,
+                   "long_context_prefill": long_result},
     }
     if not args.no_kernels:
         log("kernel rooflines")
