@@ -120,22 +120,6 @@ __global__ __launch_bounds__(256) void v_transpose_kernel(
 constexpr int kQueriesPerWave = 32;
 constexpr int kKeys = 64;
 
-typedef __attribute__((address_space(3))) void lds_void;
-
-// 16 bytes per lane global -> LDS DMA (lane l lands at lds + 16 l; lds must be
-// wave-uniform). Completion is tracked with explicit s_waitcnt vmcnt.
-__device__ inline void dma16(const void *global, const uint16_t *lds) {
-  const unsigned address = __builtin_amdgcn_readfirstlane(
-      static_cast<unsigned>(reinterpret_cast<size_t>((const lds_void *)(lds))));
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-               :: "v"(global), "s"(address) : "memory");
-}
-
-template <int kPending>
-__device__ inline void wait_dma() {
-  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(kPending) : "memory");
-}
-
 // Swizzle of a row of kUnits 16-byte units: 8 consecutive rows read at one
 // logical unit hit 8 distinct 16-byte bank groups.
 template <int kUnits>

@@ -38,6 +38,46 @@ __host__ __device__ inline float round_bf16(const float value) {
   return bf16_to_f32(f32_to_bf16(value));
 }
 
+// ---- Global -> LDS DMA (global_load_lds_dwordx4): lane l's 16 bytes land at
+// LDS byte address lds + 16 l (lds must be wave-uniform). Issued through
+// inline asm so the compiler does not serialise it with LDS reads of other
+// stage buffers (it cannot tell them apart and would wait for every DMA);
+// kernels account for completion themselves with s_waitcnt vmcnt. M0 is
+// written here and is not live across this asm in the kernels that use it.
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ inline void dma16(const void *global, const void *lds) {
+  const unsigned address = __builtin_amdgcn_readfirstlane(
+      static_cast<unsigned>(reinterpret_cast<size_t>((const lds_void *)(lds))));
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(global), "s"(address) : "memory");
+}
+
+template <int kPending>
+__device__ inline void wait_dma() {
+  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(kPending) : "memory");
+}
+
+// ---- GEMM tile order.
+// Maps the hardware block id to a (tile_m, tile_n) pair: consecutive ids go
+// to different XCDs, so id -> (xcd, slot) -> contiguous band per XCD.
+// XCD x receives total/8 tiles (+1 for the first total%8 XCDs), so the map
+// from hardware id to linear tile is a bijection for every grid size.
+template <int kGroupRows = 8>
+__device__ inline void tile_of(int id, int tiles_m, int tiles_n, int *tm, int *tn) {
+  const int total = tiles_m * tiles_n;
+  const int q = total / 8, r = total % 8;
+  const int xcd = id % 8;
+  const int linear = xcd * q + min(xcd, r) + id / 8;
+  const int group_size = kGroupRows * tiles_n;
+  const int group = linear / group_size;
+  const int first_m = group * kGroupRows;
+  const int rows = min(tiles_m - first_m, kGroupRows);
+  const int in_group = linear % group_size;
+  *tm = first_m + in_group % rows;
+  *tn = in_group / rows;
+}
+
 // ---- Activation storage type of the inter-kernel tensors.
 enum class IoType : int { kF32 = 0, kBF16 = 1 };
 

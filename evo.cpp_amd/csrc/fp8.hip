@@ -16,11 +16,11 @@
 //    products, every term aligned to 13 fractional bits and truncated, one
 //    integer sum, E8M13 truncation of the normalised result;
 //  * mfma-k32 / mfma-k128: OCP-E4M3 MFMA (v_mfma_f32_32x32x16_fp8_fp8 or
-//    v_mfma_scale_f32_32x32x64_f8f6f4 with unit scales) computes each K chunk
-//    exactly-rounded in F32; the chunk is then promoted into the running
-//    accumulator, which is truncated to E8M13 after every promotion like the
-//    reference's. Per-term truncation inside a chunk is not reproduced, so
-//    results differ from exact mode by a few E8M13 ulps.
+//    v_mfma_scale_f32_32x32x64_f8f6f4 with unit scales) adds each K chunk's
+//    products onto the running accumulator in F32, which is then truncated
+//    to E8M13 like the reference's after every group. Per-term truncation
+//    inside a chunk is not reproduced, so results differ from exact mode by
+//    a few E8M13 ulps.
 // All modes finish with bf16(acc * output_scale).
 #include "common.hpp"
 #include "ops.hpp"
@@ -150,134 +150,164 @@ __global__ __launch_bounds__(256) void qgmma_exact_kernel(
     put(out, static_cast<size_t>(row) * N + col, round_bf16(acc * output_scale));
 }
 
-// MFMA path. Block 128x128 outputs, 4 waves of 64x64 (2x2 tiles 32x32),
-// K staged 128 bytes per step through LDS rows padded to 144 B.
-constexpr int kBM = 128, kBN = 128, kBK = 128, kStride = kBK + 16;
+// MFMA path. Block 256 (M) x 128 (N) outputs, 4 waves as 2 x 2 of 128 x 64
+// (4 x 2 MFMA 32x32 tiles): 128 accumulators per lane stay in VGPRs, so the
+// E8M13 truncation after each promotion is one VALU op per value. The
+// accumulator is the MFMA's C operand: a chunk's products are summed onto it
+// inside the matrix core and the sum is truncated (the reference also adds
+// the aligned accumulator into each group's integer sum). K is staged 128
+// codes (one 128-byte line per row) per step by DMA into LDS rows of eight
+// 16-byte units, unit u of row r at r*8 + (u ^ ((r >> 1) & 7)) so that the
+// fragment reads of 8 consecutive rows hit 8 distinct bank groups; three
+// stages rotate. Rows beyond M or N load a clamped valid row and are never
+// stored.
+constexpr int kBM = 256, kBN = 128, kBK = 128, kStages = 3;
+constexpr int kStageBytes = (kBM + kBN) * kBK;   // 48 KB
+constexpr int kDmaPerWave = kStageBytes / 1024 / 4;  // 12
+constexpr size_t kMfmaLds = static_cast<size_t>(kStages) * kStageBytes;
+
+__device__ inline int fp8_unit(int row, int unit) { return row * 8 + (unit ^ ((row >> 1) & 7)); }
 
 template <int kChunk, typename Out>
 __global__ __launch_bounds__(256) void fp8_mfma_kernel(
     const uint8_t *__restrict__ a, const uint8_t *__restrict__ w,
     Out *__restrict__ out, int M, int N, int K, float output_scale) {
-  __shared__ __attribute__((aligned(16))) uint8_t a_s[kBM * kStride];
-  __shared__ __attribute__((aligned(16))) uint8_t w_s[kBN * kStride];
+  extern __shared__ __attribute__((aligned(16))) uint8_t fp8_lds[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5, col = lane & 31;
   const int wave_m = wave >> 1, wave_n = wave & 1;
-  const int block_m = blockIdx.y * kBM, block_n = blockIdx.x * kBN;
-  // loader: 128 rows x 128 bytes per operand = 1024 uint4; 4 per thread.
-  uint4 a_reg[4], w_reg[4];
-  auto fetch = [&](int k0) {
+  const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
+  int tm, tn;
+  tile_of(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
+  const int block_m = tm * kBM, block_n = tn * kBN;
+
+  // DMA op g = wave*12 + i: 1 KB chunk g of the stage (chunks 0..31 = A rows
+  // 8g.., 32..47 = W rows 8(g-32)..); lane l fills unit 64 g' + l.
+  const uint8_t *src[kDmaPerWave];
+  int dst[kDmaPerWave];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int idx = tid + v * 256;
-      const int r = idx >> 3, seg = (idx & 7) * 16;
-      const int ar = block_m + r, wr = block_n + r;
-      a_reg[v] = ar < M ? *reinterpret_cast<const uint4 *>(a + static_cast<size_t>(ar) * K + k0 + seg)
-                        : make_uint4(0, 0, 0, 0);
-      w_reg[v] = wr < N ? *reinterpret_cast<const uint4 *>(w + static_cast<size_t>(wr) * K + k0 + seg)
-                        : make_uint4(0, 0, 0, 0);
-    }
+  for (int i = 0; i < kDmaPerWave; ++i) {
+    const int g = wave * kDmaPerWave + i;
+    const bool is_a = g < kBM / 8;
+    const int chunk = is_a ? g : g - kBM / 8;
+    const int flat = chunk * 64 + lane;
+    const int row = flat >> 3, unit = (flat & 7) ^ ((row >> 1) & 7);
+    if (is_a)
+      src[i] = a + static_cast<size_t>(min(block_m + row, M - 1)) * K + unit * 16;
+    else
+      src[i] = w + static_cast<size_t>(min(block_n + row, N - 1)) * K + unit * 16;
+    dst[i] = (is_a ? 0 : kBM * kBK) + chunk * 1024;
+  }
+  auto issue = [&](int step) {
+    uint8_t *stage = fp8_lds + (step % kStages) * kStageBytes;
+    const int k0 = step * kBK;
+#pragma unroll
+    for (int i = 0; i < kDmaPerWave; ++i)
+      dma16(src[i] + k0, stage + dst[i]);
   };
-  auto stash = [&]() {
+
+  f32x16 acc[4][2];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int idx = tid + v * 256;
-      const int r = idx >> 3, seg = (idx & 7) * 16;
-      *reinterpret_cast<uint4 *>(a_s + r * kStride + seg) = a_reg[v];
-      *reinterpret_cast<uint4 *>(w_s + r * kStride + seg) = w_reg[v];
-    }
-  };
-  f32x16 acc[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e)
         acc[i][j][e] = 0.0F;
+  auto truncate_all = [&]() {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          acc[i][j][e] = truncate_e8m13(acc[i][j][e]);
+  };
 
-  fetch(0);
-  for (int k0 = 0; k0 < K; k0 += kBK) {
+  const int steps = K / kBK;
+  issue(0);
+  if (steps > 1)
+    issue(1);
+  for (int s = 0; s < steps; ++s) {
+    if (s + 1 < steps)
+      wait_dma<kDmaPerWave>();
+    else
+      wait_dma<0>();
     __syncthreads();
-    stash();
-    __syncthreads();
-    if (k0 + kBK < K)
-      fetch(k0 + kBK);
+    if (s + 2 < steps)
+      issue(s + 2);  // into the buffer of step s-1, which every wave has left
+    const uint8_t *a_s = fp8_lds + (s % kStages) * kStageBytes;
+    const uint8_t *w_s = a_s + kBM * kBK;
+    if constexpr (kChunk == 128) {
+      // Two K=64 MFMAs per tile, then one promotion (truncation) per 128 K.
 #pragma unroll
-    for (int c0 = 0; c0 < kBK; c0 += kChunk) {
-      f32x16 part[2][2];
+      for (int ks = 0; ks < 2; ++ks) {
+        i32x8 bv[2], av[4];
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+        for (int j = 0; j < 2; ++j) {
+          const int row = wave_n * 64 + j * 32 + col;
+          const uint4 lo = *reinterpret_cast<const uint4 *>(w_s + fp8_unit(row, ks * 4 + half * 2) * 16);
+          const uint4 hi = *reinterpret_cast<const uint4 *>(w_s + fp8_unit(row, ks * 4 + half * 2 + 1) * 16);
+          bv[j] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
+                        (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+        }
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int i = 0; i < 4; ++i) {
+          const int row = wave_m * 128 + i * 32 + col;
+          const uint4 lo = *reinterpret_cast<const uint4 *>(a_s + fp8_unit(row, ks * 4 + half * 2) * 16);
+          const uint4 hi = *reinterpret_cast<const uint4 *>(a_s + fp8_unit(row, ks * 4 + half * 2 + 1) * 16);
+          av[i] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
+                        (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+        }
 #pragma unroll
-          for (int e = 0; e < 16; ++e)
-            part[i][j][e] = 0.0F;
-      if constexpr (kChunk == 32) {
-#pragma unroll
-        for (int ks = 0; ks < 32; ks += 16) {
-          const int koff = c0 + ks + (lane >> 5) * 8;
-          long bv[2];
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
           for (int j = 0; j < 2; ++j)
-            bv[j] = *reinterpret_cast<const long *>(
-                w_s + (wave_n * 64 + j * 32 + (lane & 31)) * kStride + koff);
+            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                av[i], bv[j], acc[i][j], 0, 0, 0, 127, 0, 127);
+      }
+      truncate_all();
+    } else {
+      // Four 32-K chunks, each two K=16 MFMAs then a promotion.
 #pragma unroll
-          for (int i = 0; i < 2; ++i) {
-            const long av = *reinterpret_cast<const long *>(
-                a_s + (wave_m * 64 + i * 32 + (lane & 31)) * kStride + koff);
+      for (int c = 0; c < kBK / 32; ++c) {
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-              part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(av, bv[j], part[i][j], 0, 0, 0);
-          }
-        }
-      } else {
-#pragma unroll
-        for (int ks = 0; ks < kChunk; ks += 64) {
-          const int koff = c0 + ks + (lane >> 5) * 32;
-          i32x8 bv[2];
+        for (int ks = 2 * c; ks < 2 * c + 2; ++ks) {
+          long bv[2], av[4];
 #pragma unroll
           for (int j = 0; j < 2; ++j) {
-            const uint8_t *p = w_s + (wave_n * 64 + j * 32 + (lane & 31)) * kStride + koff;
-            const uint4 lo = *reinterpret_cast<const uint4 *>(p);
-            const uint4 hi = *reinterpret_cast<const uint4 *>(p + 16);
-            bv[j] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
-                          (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+            const int row = wave_n * 64 + j * 32 + col;
+            bv[j] = *reinterpret_cast<const long *>(w_s + fp8_unit(row, ks) * 16 + half * 8);
           }
 #pragma unroll
-          for (int i = 0; i < 2; ++i) {
-            const uint8_t *p = a_s + (wave_m * 64 + i * 32 + (lane & 31)) * kStride + koff;
-            const uint4 lo = *reinterpret_cast<const uint4 *>(p);
-            const uint4 hi = *reinterpret_cast<const uint4 *>(p + 16);
-            const i32x8 av{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
-                           (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+          for (int i = 0; i < 4; ++i) {
+            const int row = wave_m * 128 + i * 32 + col;
+            av[i] = *reinterpret_cast<const long *>(a_s + fp8_unit(row, ks) * 16 + half * 8);
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int j = 0; j < 2; ++j)
-              part[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                  av, bv[j], part[i][j], 0, 0, 0, 127, 0, 127);
-          }
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(av[i], bv[j], acc[i][j],
+                                                                     0, 0, 0);
         }
+        truncate_all();
       }
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int e = 0; e < 16; ++e)
-            acc[i][j][e] = truncate_e8m13(acc[i][j][e] + part[i][j][e]);
     }
   }
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const int row = block_m + wave_m * 64 + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+      const int row = block_m + wave_m * 128 + i * 32 + (e >> 2) * 8 + half * 4 + (e & 3);
       if (row >= M)
         continue;
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const int col = block_n + wave_n * 64 + j * 32 + (lane & 31);
-        if (col < N)
-          put(out, static_cast<size_t>(row) * N + col, round_bf16(acc[i][j][e] * output_scale));
+        const int column = block_n + wave_n * 64 + j * 32 + col;
+        if (column < N)
+          put(out, static_cast<size_t>(row) * N + column,
+              round_bf16(acc[i][j][e] * output_scale));
       }
     }
 }
@@ -328,15 +358,17 @@ Status fp8_linear_impl(const uint8_t *in_codes, const uint8_t *w_codes, Out *out
   }
   if (K % kBK != 0)
     return {ErrorCode::kInvalidArgument, "fp8_linear: MFMA modes need K % 128 == 0"};
-  const dim3 grid(ceil_div(N, kBN), ceil_div(M, kBM));
-  if (mode == kFp8MfmaK32)
-    hipLaunchKernelGGL((fp8_mfma_kernel<32, Out>), grid, dim3(256), 0, stream, in_codes,
-                       w_codes, out, m, n, k, output_scale);
-  else if (mode == kFp8MfmaK128)
-    hipLaunchKernelGGL((fp8_mfma_kernel<128, Out>), grid, dim3(256), 0, stream, in_codes,
-                       w_codes, out, m, n, k, output_scale);
-  else
+  if (mode != kFp8MfmaK32 && mode != kFp8MfmaK128)
     return {ErrorCode::kInvalidArgument, "fp8_linear: unknown mode"};
+  const auto kernel = mode == kFp8MfmaK32 ? fp8_mfma_kernel<32, Out> : fp8_mfma_kernel<128, Out>;
+  // 144 KB of the CU's 160 KB LDS: opt in above the 64 KB default.
+  EVO_TRY(hip_status(hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         static_cast<int>(kMfmaLds)),
+                     "fp8_mfma_kernel LDS opt-in"));
+  const unsigned blocks = static_cast<unsigned>(ceil_div(M, kBM) * ceil_div(N, kBN));
+  hipLaunchKernelGGL(kernel, dim3(blocks), dim3(256), kMfmaLds, stream, in_codes, w_codes, out,
+                     m, n, k, output_scale);
   return launch_status("fp8_mfma_kernel");
 }
 

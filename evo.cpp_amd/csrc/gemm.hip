@@ -33,8 +33,6 @@ constexpr int kBN = 256;
 constexpr int kBK = 32;
 constexpr int kThreads = 256;
 constexpr int kStride = kBK + 8;  // BF16 per LDS row
-constexpr int kXcds = 8;
-constexpr int kGroupM = 8;
 
 struct Epilogue {
   int mode;              // GemmEpilogue
@@ -94,23 +92,6 @@ __device__ __forceinline__ void store_gated(const f32x16 &first, const f32x16 &s
   }
 }
 
-// Maps the hardware block id to a (tile_m, tile_n) pair: consecutive ids go
-// to different XCDs, so id -> (xcd, slot) -> contiguous band per XCD.
-// XCD x receives total/8 tiles (+1 for the first total%8 XCDs), so the map
-// from hardware id to linear tile is a bijection for every grid size.
-__device__ inline void tile_of(int id, int tiles_m, int tiles_n, int *tm, int *tn) {
-  const int total = tiles_m * tiles_n;
-  const int q = total / kXcds, r = total % kXcds;
-  const int xcd = id % kXcds;
-  const int linear = xcd * q + min(xcd, r) + id / kXcds;
-  const int group_size = kGroupM * tiles_n;
-  const int group = linear / group_size;
-  const int first_m = group * kGroupM;
-  const int rows = min(tiles_m - first_m, kGroupM);
-  const int in_group = linear % group_size;
-  *tm = first_m + in_group % rows;
-  *tn = in_group / rows;
-}
 
 template <bool kSplit>
 __global__ __launch_bounds__(kThreads) void gemm_staged_kernel(
@@ -277,21 +258,6 @@ __global__ __launch_bounds__(kThreads) void gemm_staged_kernel(
 // row; their results are never stored. Requires K % 32 == 0.
 constexpr int kStages = 3;
 constexpr int kPlane = kBM * kBK;  // BF16 per plane (no padding)
-
-typedef __attribute__((address_space(3))) void lds_void;
-
-// One 16-byte-per-lane global -> LDS DMA: lane l's 16 bytes land at LDS byte
-// address lds + 16 l (lds must be wave-uniform). Issued through inline asm so
-// the compiler does not serialise it with the LDS reads of other stage
-// buffers (it cannot tell them apart and would wait for every DMA); the
-// kernel accounts for completion itself with s_waitcnt vmcnt. M0 is written
-// here and is not live across this asm in the kernels that use it.
-__device__ inline void dma16(const void *global, const uint16_t *lds) {
-  const unsigned address = __builtin_amdgcn_readfirstlane(
-      static_cast<unsigned>(reinterpret_cast<size_t>((const lds_void *)(lds))));
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-               :: "v"(global), "s"(address) : "memory");
-}
 
 __device__ inline int swizzled_unit(int row, int seg) {
   return row * 4 + (seg ^ ((row >> 2) & 3));
