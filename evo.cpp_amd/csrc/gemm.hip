@@ -375,9 +375,15 @@ __global__ __launch_bounds__(512) void gemm_kernel(
     };
     read(0);
     __builtin_amdgcn_sched_barrier(0);
+    // The K-half-1 reads are interleaved with the K-half-0 MFMAs (one LDS
+    // read, then two MFMAs) instead of being issued as one burst.
     read(1);
-    __builtin_amdgcn_sched_barrier(0);
     multiply(0);
+#pragma unroll
+    for (int q = 0; q < 10; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+    }
     __builtin_amdgcn_sched_barrier(0);
     multiply(1);
   }
