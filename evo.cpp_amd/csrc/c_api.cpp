@@ -725,6 +725,17 @@ evo_status evo_hip_rms_norm(const float *x, size_t rows, size_t width, const flo
   });
 }
 
+evo_status evo_hip_rms_norm_e4m3(const float *x, size_t rows, size_t width,
+                                 const float *scale, float eps, float code_scale,
+                                 uint8_t *codes, void *stream) {
+  return protect([&]() -> evo_status {
+    if (codes == nullptr)
+      return publish(EVO_STATUS_INVALID_ARGUMENT, "invalid_argument: codes are null");
+    return publish(evo::hip::rms_norm(x, rows, width, scale, eps, nullptr, nullptr, nullptr,
+                                      static_cast<hipStream_t>(stream), codes, code_scale));
+  });
+}
+
 evo_status evo_hip_attention(const float *projected, size_t rows, size_t width, size_t heads,
                              int column_split, const float *inv_freq, float rope_scale,
                              size_t prefix, uint16_t *query, uint16_t *key_cache,

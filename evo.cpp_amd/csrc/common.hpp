@@ -78,6 +78,29 @@ __device__ inline void tile_of(int id, int tiles_m, int tiles_n, int *tm, int *t
   *tn = in_group / rows;
 }
 
+// ---- E4M3FN encoder: round to nearest even, saturating finite overflow and
+// infinities to +-448, NaN -> 0x7f|sign, sign kept on values rounding to
+// zero (the code set of evo.cpp `src/fp8.cpp:26-58`), computed from the
+// binade: subnormals as rint(m * 2^9), normals as rint(m * 2^(3-e)) offset
+// by the exponent field.
+__host__ __device__ inline uint8_t encode_e4m3(const float value) {
+  const uint32_t bits = __builtin_bit_cast(uint32_t, value);
+  const uint8_t sign = (bits >> 24U) & 0x80U;
+  const uint32_t abs_bits = bits & 0x7fffffffU;
+  if (abs_bits > 0x7f800000U)
+    return sign | 0x7fU;
+  const float magnitude = __builtin_bit_cast(float, abs_bits);
+  if (magnitude >= 448.0F)
+    return sign | 0x7eU;
+  if (magnitude < 0.015625F) {  // below 2^-6: subnormal step 2^-9
+    return sign | static_cast<uint8_t>(rintf(magnitude * 512.0F));
+  }
+  const int exponent = static_cast<int>(abs_bits >> 23U) - 127;  // -6..8
+  const float scaled = ldexpf(magnitude, 3 - exponent);          // [8, 16)
+  const int q = static_cast<int>(rintf(scaled));                 // 8..16
+  return sign | static_cast<uint8_t>(((exponent + 7) << 3) + (q - 8));
+}
+
 // ---- Activation storage type of the inter-kernel tensors.
 enum class IoType : int { kF32 = 0, kBF16 = 1 };
 

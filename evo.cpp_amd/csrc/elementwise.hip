@@ -41,7 +41,7 @@ __device__ inline float wave_sum(float v) {
 __global__ __launch_bounds__(256) void rms_norm_kernel(
     const float *__restrict__ x, size_t width, const float *__restrict__ scale,
     float eps, float *__restrict__ out, uint16_t *__restrict__ out_hi,
-    uint16_t *__restrict__ out_lo) {
+    uint16_t *__restrict__ out_lo, uint8_t *__restrict__ codes, float code_scale) {
   __shared__ float partial[4];
   const size_t row = blockIdx.x;
   const float *src = x + row * width;
@@ -62,6 +62,34 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(
   __syncthreads();
   const float total = partial[0] + partial[1] + partial[2] + partial[3];
   const float denominator = sqrtf(total / static_cast<float>(width)) + eps;
+  if (vec) {
+    // Four values per thread per pass: 16-byte F32 and 8-byte plane stores,
+    // 4-byte code stores.
+    for (size_t c = threadIdx.x * 4; c < width; c += 256 * 4) {
+      const float4 v = *reinterpret_cast<const float4 *>(src + c);
+      const float4 g = *reinterpret_cast<const float4 *>(scale + c);
+      const float y[4] = {v.x / denominator * g.x, v.y / denominator * g.y,
+                          v.z / denominator * g.z, v.w / denominator * g.w};
+      const size_t index = row * width + c;
+      if (out != nullptr)
+        *reinterpret_cast<float4 *>(out + index) = make_float4(y[0], y[1], y[2], y[3]);
+      uint16_t hi[4], lo[4];
+      uint8_t code[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        hi[e] = f32_to_bf16(y[e]);
+        lo[e] = f32_to_bf16(y[e] - bf16_to_f32(hi[e]));
+        code[e] = encode_e4m3(bf16_to_f32(hi[e]) * code_scale);
+      }
+      if (out_hi != nullptr)
+        *reinterpret_cast<uint2 *>(out_hi + index) = __builtin_bit_cast(uint2, hi);
+      if (out_lo != nullptr)
+        *reinterpret_cast<uint2 *>(out_lo + index) = __builtin_bit_cast(uint2, lo);
+      if (codes != nullptr)
+        *reinterpret_cast<uint32_t *>(codes + index) = __builtin_bit_cast(uint32_t, code);
+    }
+    return;
+  }
   const SplitOut planes{out_hi, out_lo};
   for (size_t c = threadIdx.x; c < width; c += 256) {
     const float value = src[c] / denominator * scale[c];
@@ -70,6 +98,8 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(
       out[index] = value;
     if (out_hi != nullptr)
       put(planes, index, value);
+    if (codes != nullptr)
+      codes[index] = encode_e4m3(round_bf16(value) * code_scale);
   }
 }
 
@@ -107,12 +137,14 @@ Status embed_tokens(const uint32_t *tokens, size_t rows, const uint16_t *table,
 
 Status rms_norm(const float *x, size_t rows, size_t width, const float *scale,
                 float eps, float *out, uint16_t *out_hi, uint16_t *out_lo,
-                hipStream_t stream) {
-  if (x == nullptr || scale == nullptr || (out == nullptr && out_hi == nullptr) ||
-      rows == 0 || width == 0 || rows > (1U << 31))
+                hipStream_t stream, uint8_t *codes, float code_scale) {
+  if (x == nullptr || scale == nullptr ||
+      (out == nullptr && out_hi == nullptr && codes == nullptr) || rows == 0 ||
+      width == 0 || rows > (1U << 31) ||
+      (codes != nullptr && !(code_scale > 0.0F && __builtin_isfinite(code_scale))))
     return {ErrorCode::kInvalidArgument, "rms_norm: invalid arguments"};
   hipLaunchKernelGGL(rms_norm_kernel, dim3(static_cast<unsigned>(rows)), dim3(256),
-                     0, stream, x, width, scale, eps, out, out_hi, out_lo);
+                     0, stream, x, width, scale, eps, out, out_hi, out_lo, codes, code_scale);
   return launch_status("rms_norm_kernel");
 }
 

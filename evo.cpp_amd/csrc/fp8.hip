@@ -28,23 +28,6 @@
 namespace evo::hip {
 namespace {
 
-__host__ __device__ inline uint8_t encode_e4m3(const float value) {
-  const uint32_t bits = __builtin_bit_cast(uint32_t, value);
-  const uint8_t sign = (bits >> 24U) & 0x80U;
-  const uint32_t abs_bits = bits & 0x7fffffffU;
-  if (abs_bits > 0x7f800000U)
-    return sign | 0x7fU;
-  const float magnitude = __builtin_bit_cast(float, abs_bits);
-  if (magnitude >= 448.0F)
-    return sign | 0x7eU;
-  if (magnitude < 0.015625F) {  // below 2^-6: subnormal step 2^-9
-    return sign | static_cast<uint8_t>(rintf(magnitude * 512.0F));
-  }
-  const int exponent = static_cast<int>(abs_bits >> 23U) - 127;  // -6..8
-  const float scaled = ldexpf(magnitude, 3 - exponent);          // [8, 16)
-  const int q = static_cast<int>(rintf(scaled));                 // 8..16
-  return sign | static_cast<uint8_t>(((exponent + 7) << 3) + (q - 8));
-}
 
 __global__ void quantize_f32_kernel(const float *__restrict__ x, size_t n,
                                     float scale, uint8_t *__restrict__ codes) {

@@ -422,12 +422,16 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
   for (size_t i = 0; i < c.layers; ++i) {
     const Layer &L = model_->layer[i];
     Cache &k = cache_[i];
-    EVO_TRY(rms_norm(hidden, rows, w, L.pre_norm.as<float>(), c.eps, nullptr, normed_hi,
-                     split ? normed_lo : nullptr, stream_));
     if (L.fp8) {
-      // codes of bf16(x) * input_scale: the hi plane is bf16(x) exactly.
-      EVO_TRY(e4m3_quantize_bf16(normed.hi, rows * w, L.fp8_input_scale,
-                                 codes_.as<uint8_t>(), stream_));
+      // The norm writes only the E4M3 codes of bf16(x) * input_scale: the
+      // projection is the sole consumer of this normed activation.
+      EVO_TRY(rms_norm(hidden, rows, w, L.pre_norm.as<float>(), c.eps, nullptr, nullptr,
+                       nullptr, stream_, codes_.as<uint8_t>(), L.fp8_input_scale));
+    } else {
+      EVO_TRY(rms_norm(hidden, rows, w, L.pre_norm.as<float>(), c.eps, nullptr, normed_hi,
+                       split ? normed_lo : nullptr, stream_));
+    }
+    if (L.fp8) {
       const Fp8Mode mode = (w % 128 != 0) ? kFp8Exact : options_.fp8_mode;
       // The product is BF16 by definition: store it as BF16 and halve the
       // projection's HBM traffic for the Hyena kernels that read it.

@@ -79,9 +79,11 @@ Status embed_tokens(const uint32_t *tokens, size_t rows, const uint16_t *table,
                     size_t vocab, size_t width, float *out, int *invalid,
                     hipStream_t stream);
 // Writes the F32 result to out_f32 and/or split planes (out_hi, out_lo).
+// With codes, also E4M3 codes of bf16(y) * code_scale (the FP8 projection's
+// input quantisation fused into the norm).
 Status rms_norm(const float *x, size_t rows, size_t width, const float *scale,
                 float eps, float *out_f32, uint16_t *out_hi, uint16_t *out_lo,
-                hipStream_t stream);
+                hipStream_t stream, uint8_t *codes = nullptr, float code_scale = 1.0F);
 // Copies the last `history` rows of the sequence [old_history ; x] into
 // history (F32 [history, channels]), keeping continuation caches.
 Status update_history(const float *x, size_t rows, size_t channels,

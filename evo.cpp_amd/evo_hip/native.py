@@ -36,6 +36,8 @@ _OPS = {
     "evo_hip_pack_mlp": (c_int, [c_void, c_void, c_size, c_size, c_void, c_void]),
     "evo_hip_gated_mlp": (c_int, [c_void, c_void, c_void, c_void, c_size, c_size, c_size,
                                   c_int, c_void, c_void, c_void, c_void]),
+    "evo_hip_rms_norm_e4m3": (c_int, [c_void, c_size, c_size, c_void, c_float, c_float,
+                                      c_void, c_void]),
     "evo_hip_rms_norm": (c_int, [c_void, c_size, c_size, c_void, c_float, c_void, c_void,
                                  c_void, c_void]),
     "evo_hip_context_prefill_resident": (c_int, [c_void, c_void, c_size, c_void]),

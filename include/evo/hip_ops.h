@@ -143,6 +143,14 @@ EVO_API evo_status evo_hip_rms_norm(const float *x, size_t rows, size_t width,
                                     uint16_t *out_hi, uint16_t *out_lo,
                                     void *stream);
 
+/* RMSNorm fused with the FP8 projection's input quantisation: codes =
+ * E4M3FN(bf16(y) * code_scale) of the normed rows, without writing y
+ * (the sequence `bf16_rms_norm` + `quantize_bf16_e4m3` of the reference's
+ * FP8 projection path, `src/cuda/ops.cu:72-113, 250-262`). */
+EVO_API evo_status evo_hip_rms_norm_e4m3(const float *x, size_t rows, size_t width,
+                                         const float *scale, float eps, float code_scale,
+                                         uint8_t *codes, void *stream);
+
 /* Attention block body: split the Wqkv output [rows, 3W], apply RoPE at
  * positions prefix.., append K/V at `prefix` of the caches, causal softmax
  * attention into out [rows, W] F32. query is workspace of 2*rows*W uint16;

@@ -215,6 +215,27 @@ def test_rms_norm(oracle):
                               bf16_bits(got - bf16_to_f32(bf16_bits(got))))
 
 
+@pytest.mark.parametrize("rows,width,code_scale", [(64, 4096, 448.0 / 8.0), (5, 1920, 17.5),
+                                                  (3, 257, 3.0)])
+def test_rms_norm_e4m3_codes(rows, width, code_scale):
+    """The norm fused with the FP8 input quantisation: codes are bit-exact
+    E4M3(bf16(y) * scale) of the norm's own F32 output (oracle encoder)."""
+    r = rng(rows + width)
+    x = r.standard_normal((rows, width)).astype(np.float32) * 2
+    scale = (1 + 0.1 * r.standard_normal(width)).astype(np.float32)
+    out = empty((rows, width))
+    N.call("evo_hip_rms_norm", p(dev(x)), rows, width, p(dev(scale)), 1e-6, p(out),
+           None, None, stream())
+    y = host(out)
+    codes = empty((rows * width,), np.uint8)
+    N.call("evo_hip_rms_norm_e4m3", p(dev(x)), rows, width, p(dev(scale)), 1e-6, code_scale,
+           p(codes), stream())
+    expected = np.zeros(rows * width, np.uint8)
+    bits = np.ascontiguousarray(bf16_bits(y).ravel())
+    O.lib().oracle_e4m3_quantize_bf16(O.ptr(bits), bits.size, code_scale, O.ptr(expected))
+    assert np.array_equal(host(codes), expected)
+
+
 # --------------------------------------------------------------- Hyena
 def hyena_case(seed, kind, length, width, groups=16, inner_len=7, state=16):
     r = rng(seed)
