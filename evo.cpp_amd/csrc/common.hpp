@@ -104,6 +104,26 @@ __host__ __device__ inline uint8_t encode_e4m3(const float value) {
 // ---- Activation storage type of the inter-kernel tensors.
 enum class IoType : int { kF32 = 0, kBF16 = 1 };
 
+// Raw buffer loads: a wave-uniform resource (base, byte bound) plus a 32-bit
+// per-lane byte offset and a wave-uniform scalar byte offset, one
+// buffer_load per element with no per-lane address arithmetic. Offsets at
+// or past the bound read 0.
+__device__ inline __amdgpu_buffer_rsrc_t buffer_resource(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, static_cast<int>(bytes),
+                                           0x00020000);
+}
+
+template <typename T>
+__device__ inline float buffer_act(__amdgpu_buffer_rsrc_t resource, uint32_t lane_offset,
+                                   uint32_t uniform_offset) {
+  if constexpr (sizeof(T) == 2)
+    return bf16_to_f32(static_cast<uint16_t>(__builtin_amdgcn_raw_buffer_load_b16(
+        resource, static_cast<int>(lane_offset), static_cast<int>(uniform_offset), 0)));
+  else
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+        resource, static_cast<int>(lane_offset), static_cast<int>(uniform_offset), 0));
+}
+
 template <typename T> __device__ inline float load_act(const T *p, size_t i);
 template <> __device__ inline float load_act<float>(const float *p, size_t i) {
   return p[i];

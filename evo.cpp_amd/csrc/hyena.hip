@@ -140,11 +140,18 @@ struct RowStream {
 template <typename T, int kB>
 __device__ inline void load_batch(const T *P, size_t cols3, size_t planar, size_t t,
                                   size_t t1, size_t c, float (&rows)[kB][3]) {
+  // Rows at or past t1 lie beyond the resource bound and read 0.
+  const uint32_t row_bytes = static_cast<uint32_t>(cols3 * sizeof(T));
+  const auto resource = buffer_resource(P + t * cols3, static_cast<uint32_t>(t1 - t) * row_bytes);
+  uint32_t column[3];
+#pragma unroll
+  for (int s = 0; s < 3; ++s)
+    column[s] = static_cast<uint32_t>(pcol(c, s, planar) * sizeof(T));
 #pragma unroll
   for (int b = 0; b < kB; ++b)
 #pragma unroll
     for (int s = 0; s < 3; ++s)
-      rows[b][s] = t + b < t1 ? load_act(P, (t + b) * cols3 + pcol(c, s, planar)) : 0.0F;
+      rows[b][s] = buffer_act<T>(resource, column[s], b * row_bytes);
 }
 
 // ---- HCL phase 1: final local state of every chunk from a zero start.
@@ -431,15 +438,21 @@ __global__ __launch_bounds__(kFirThreads) void hyena_fir_mfma_kernel(
     if (interior) {
       float taps[3][kWin];
       load_window_taps(short_filter, short_len, c, taps);
+      // Wave-uniform row pointers plus a 32-bit per-lane column offset
+      // (scalar-base addressing, no per-lane 64-bit address arithmetic).
       const T *base = P + static_cast<size_t>(tw - (kWin - 1)) * cols3;
+      const uint32_t row_bytes = static_cast<uint32_t>(cols3 * sizeof(T));
+      const auto resource = buffer_resource(base, (kRows + kWin - 1) * row_bytes);
+      uint32_t column[3];
+#pragma unroll
+      for (int s = 0; s < 3; ++s)
+        column[s] = static_cast<uint32_t>(pcol(c, s, planar) * sizeof(T));
       float v[kRows + kWin - 1][3];
 #pragma unroll
-      for (int s = 0; s < 3; ++s) {
-        const T *column = base + pcol(c, s, planar);
+      for (int b = 0; b < kRows + kWin - 1; ++b)
 #pragma unroll
-        for (int b = 0; b < kRows + kWin - 1; ++b)
-          v[b][s] = load_act(column, static_cast<size_t>(b) * cols3);
-      }
+        for (int s = 0; s < 3; ++s)
+          v[b][s] = buffer_act<T>(resource, column[s], b * row_bytes);
       uint32_t *hi_pairs = reinterpret_cast<uint32_t *>(u_hi + lane * Shape::kStride + i0);
       uint32_t *lo_pairs = reinterpret_cast<uint32_t *>(u_lo + lane * Shape::kStride + i0);
 #pragma unroll
