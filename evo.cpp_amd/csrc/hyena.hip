@@ -211,18 +211,29 @@ __global__ void hcl_carry_kernel(float *__restrict__ chunk_state, size_t G,
   for (int e = 1; e < kChunk; e <<= 1)
     full *= full;
   float state = modal_state != nullptr ? modal_state[c * S + m] : 0.0F;
-  for (size_t g = 0; g < G; ++g) {
-    const size_t index = (g * S + m) * W + c;
-    const float local = chunk_state[index];
-    chunk_state[index] = state;
-    const size_t len = min(L - g * kChunk, static_cast<size_t>(kChunk));
-    float power = full;
-    if (len != static_cast<size_t>(kChunk)) {
-      power = 1.0F;
-      for (size_t e = 0; e < len; ++e)
-        power *= p;
+  // Chunk states are loaded 16 at a time ahead of the serial combine, so
+  // the loads overlap instead of forming a load -> store chain per chunk.
+  constexpr int kAhead = 16;
+  for (size_t g0 = 0; g0 < G; g0 += kAhead) {
+    float local[kAhead];
+#pragma unroll
+    for (int q = 0; q < kAhead; ++q)
+      local[q] = g0 + q < G ? chunk_state[((g0 + q) * S + m) * W + c] : 0.0F;
+#pragma unroll
+    for (int q = 0; q < kAhead; ++q) {
+      const size_t g = g0 + q;
+      if (g >= G)
+        break;
+      chunk_state[(g * S + m) * W + c] = state;
+      const size_t len = min(L - g * kChunk, static_cast<size_t>(kChunk));
+      float power = full;
+      if (len != static_cast<size_t>(kChunk)) {
+        power = 1.0F;
+        for (size_t e = 0; e < len; ++e)
+          power *= p;
+      }
+      state = power * state + local[q];
     }
-    state = power * state + local;
   }
   if (modal_state != nullptr)
     modal_state[c * S + m] = state;
