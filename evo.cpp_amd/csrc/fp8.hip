@@ -133,39 +133,41 @@ __global__ __launch_bounds__(256) void qgmma_exact_kernel(
     put(out, static_cast<size_t>(row) * N + col, round_bf16(acc * output_scale));
 }
 
-// MFMA path. Block 256 (M) x 128 (N) outputs, 4 waves as 2 x 2 of 128 x 64
-// (4 x 2 MFMA 32x32 tiles): 128 accumulators per lane stay in VGPRs, so the
-// E8M13 truncation after each promotion is one VALU op per value. The
-// accumulator is the MFMA's C operand: a chunk's products are summed onto it
-// inside the matrix core and the sum is truncated (the reference also adds
-// the aligned accumulator into each group's integer sum). K is staged 128
-// codes (one 128-byte line per row) per step by DMA into LDS rows of eight
-// 16-byte units, unit u of row r at r*8 + (u ^ ((r >> 1) & 7)) so that the
-// fragment reads of 8 consecutive rows hit 8 distinct bank groups; three
-// stages rotate. Rows beyond M or N load a clamped valid row and are never
-// stored.
-constexpr int kBM = 256, kBN = 128, kBK = 128, kStages = 3;
-constexpr int kStageBytes = (kBM + kBN) * kBK;   // 48 KB
-constexpr int kDmaPerWave = kStageBytes / 1024 / 4;  // 12
+// MFMA path. Block 256 (M) x 192 (N) outputs, 8 waves as 4 (M) x 2 (N) of
+// 64 x 96 (2 x 3 MFMA 32x32 tiles), two waves per SIMD; the 96 accumulators
+// per lane stay in VGPRs, so the E8M13 truncation after each promotion is
+// one VALU op per value. The accumulator is the MFMA's C operand: a chunk's
+// products are summed onto it inside the matrix core and the sum is
+// truncated (the reference also adds the aligned accumulator into each
+// group's integer sum). K is staged 128 codes (one 128-byte line per row)
+// per step by DMA into LDS rows of eight 16-byte units, unit u of row r at
+// r*8 + (u ^ ((r >> 1) & 7)) so that the fragment reads of 8 consecutive rows
+// hit 8 distinct bank groups; two stages alternate. A 1024-row projection
+// is 4 x 64 = 256 tiles: one per CU. Rows beyond M or N load a clamped
+// valid row and are never stored.
+constexpr int kBM = 256, kBN = 192, kBK = 128, kStages = 2;
+constexpr int kWaves = 8;
+constexpr int kStageBytes = (kBM + kBN) * kBK;            // 56 KB
+constexpr int kDmaPerWave = kStageBytes / 1024 / kWaves;  // 7
 constexpr size_t kMfmaLds = static_cast<size_t>(kStages) * kStageBytes;
 
 __device__ inline int fp8_unit(int row, int unit) { return row * 8 + (unit ^ ((row >> 1) & 7)); }
 
 template <int kChunk, typename Out>
-__global__ __launch_bounds__(256) void fp8_mfma_kernel(
+__global__ __launch_bounds__(kWaves * 64) void fp8_mfma_kernel(
     const uint8_t *__restrict__ a, const uint8_t *__restrict__ w,
     Out *__restrict__ out, int M, int N, int K, float output_scale) {
   extern __shared__ __attribute__((aligned(16))) uint8_t fp8_lds[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int half = lane >> 5, col = lane & 31;
-  const int wave_m = wave >> 1, wave_n = wave & 1;
+  const int wave_m = wave >> 1, wave_n = wave & 1;  // 4 x 2
   const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
   int tm, tn;
   tile_of(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
   const int block_m = tm * kBM, block_n = tn * kBN;
 
-  // DMA op g = wave*12 + i: 1 KB chunk g of the stage (chunks 0..31 = A rows
-  // 8g.., 32..47 = W rows 8(g-32)..); lane l fills unit 64 g' + l.
+  // DMA op g = wave*7 + i: 1 KB chunk g of the stage (chunks 0..31 = A rows
+  // 8g.., 32..55 = W rows 8(g-32)..); lane l fills unit 64 g' + l.
   const uint8_t *src[kDmaPerWave];
   int dst[kDmaPerWave];
 #pragma unroll
@@ -189,66 +191,61 @@ __global__ __launch_bounds__(256) void fp8_mfma_kernel(
       dma16(src[i] + k0, stage + dst[i]);
   };
 
-  f32x16 acc[4][2];
+  f32x16 acc[2][3];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 3; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e)
         acc[i][j][e] = 0.0F;
   auto truncate_all = [&]() {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < 3; ++j)
 #pragma unroll
         for (int e = 0; e < 16; ++e)
           acc[i][j][e] = truncate_e8m13(acc[i][j][e]);
   };
+  auto frag32 = [&](const uint8_t *base, int row, int unit) {
+    const uint4 lo = *reinterpret_cast<const uint4 *>(base + fp8_unit(row, unit) * 16);
+    const uint4 hi = *reinterpret_cast<const uint4 *>(base + fp8_unit(row, unit + 1) * 16);
+    return i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
+                 (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+  };
 
   const int steps = K / kBK;
   issue(0);
-  if (steps > 1)
-    issue(1);
   for (int s = 0; s < steps; ++s) {
-    if (s + 1 < steps)
-      wait_dma<kDmaPerWave>();
-    else
-      wait_dma<0>();
+    wait_dma<0>();
+    // Every wave's DMA of step s has landed and every wave has left the
+    // buffer of step s-1, which the next issue overwrites.
     __syncthreads();
-    if (s + 2 < steps)
-      issue(s + 2);  // into the buffer of step s-1, which every wave has left
+    if (s + 1 < steps)
+      issue(s + 1);
     const uint8_t *a_s = fp8_lds + (s % kStages) * kStageBytes;
     const uint8_t *w_s = a_s + kBM * kBK;
     if constexpr (kChunk == 128) {
       // Two K=64 MFMAs per tile, then one promotion (truncation) per 128 K.
+      i32x8 av[2][2], bv[2][3];
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        i32x8 bv[2], av[4];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int row = wave_n * 64 + j * 32 + col;
-          const uint4 lo = *reinterpret_cast<const uint4 *>(w_s + fp8_unit(row, ks * 4 + half * 2) * 16);
-          const uint4 hi = *reinterpret_cast<const uint4 *>(w_s + fp8_unit(row, ks * 4 + half * 2 + 1) * 16);
-          bv[j] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
-                        (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-        }
+        for (int j = 0; j < 3; ++j)
+          bv[ks][j] = frag32(w_s, wave_n * 96 + j * 32 + col, ks * 4 + half * 2);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int row = wave_m * 128 + i * 32 + col;
-          const uint4 lo = *reinterpret_cast<const uint4 *>(a_s + fp8_unit(row, ks * 4 + half * 2) * 16);
-          const uint4 hi = *reinterpret_cast<const uint4 *>(a_s + fp8_unit(row, ks * 4 + half * 2 + 1) * 16);
-          av[i] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
-                        (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int j = 0; j < 2; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                av[i], bv[j], acc[i][j], 0, 0, 0, 127, 0, 127);
+        for (int i = 0; i < 2; ++i)
+          av[ks][i] = frag32(a_s, wave_m * 64 + i * 32 + col, ks * 4 + half * 2);
       }
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 3; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                av[ks][i], bv[ks][j], acc[i][j], 0, 0, 0, 127, 0, 127);
       truncate_all();
     } else {
       // Four 32-K chunks, each two K=16 MFMAs then a promotion.
@@ -256,21 +253,21 @@ __global__ __launch_bounds__(256) void fp8_mfma_kernel(
       for (int c = 0; c < kBK / 32; ++c) {
 #pragma unroll
         for (int ks = 2 * c; ks < 2 * c + 2; ++ks) {
-          long bv[2], av[4];
+          long bv[3], av[2];
 #pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            const int row = wave_n * 64 + j * 32 + col;
+          for (int j = 0; j < 3; ++j) {
+            const int row = wave_n * 96 + j * 32 + col;
             bv[j] = *reinterpret_cast<const long *>(w_s + fp8_unit(row, ks) * 16 + half * 8);
           }
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int row = wave_m * 128 + i * 32 + col;
+          for (int i = 0; i < 2; ++i) {
+            const int row = wave_m * 64 + i * 32 + col;
             av[i] = *reinterpret_cast<const long *>(a_s + fp8_unit(row, ks) * 16 + half * 8);
           }
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
+          for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < 3; ++j)
               acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(av[i], bv[j], acc[i][j],
                                                                      0, 0, 0);
         }
@@ -279,15 +276,15 @@ __global__ __launch_bounds__(256) void fp8_mfma_kernel(
     }
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const int row = block_m + wave_m * 128 + i * 32 + (e >> 2) * 8 + half * 4 + (e & 3);
+      const int row = block_m + wave_m * 64 + i * 32 + (e >> 2) * 8 + half * 4 + (e & 3);
       if (row >= M)
         continue;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int column = block_n + wave_n * 64 + j * 32 + col;
+      for (int j = 0; j < 3; ++j) {
+        const int column = block_n + wave_n * 96 + j * 32 + col;
         if (column < N)
           put(out, static_cast<size_t>(row) * N + column,
               round_bf16(acc[i][j][e] * output_scale));
@@ -344,13 +341,13 @@ Status fp8_linear_impl(const uint8_t *in_codes, const uint8_t *w_codes, Out *out
   if (mode != kFp8MfmaK32 && mode != kFp8MfmaK128)
     return {ErrorCode::kInvalidArgument, "fp8_linear: unknown mode"};
   const auto kernel = mode == kFp8MfmaK32 ? fp8_mfma_kernel<32, Out> : fp8_mfma_kernel<128, Out>;
-  // 144 KB of the CU's 160 KB LDS: opt in above the 64 KB default.
+  // 112 KB of the CU's 160 KB LDS: opt in above the 64 KB default.
   EVO_TRY(hip_status(hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
                                          hipFuncAttributeMaxDynamicSharedMemorySize,
                                          static_cast<int>(kMfmaLds)),
                      "fp8_mfma_kernel LDS opt-in"));
   const unsigned blocks = static_cast<unsigned>(ceil_div(M, kBM) * ceil_div(N, kBN));
-  hipLaunchKernelGGL(kernel, dim3(blocks), dim3(256), kMfmaLds, stream, in_codes, w_codes, out,
+  hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kWaves * 64), kMfmaLds, stream, in_codes, w_codes, out,
                      m, n, k, output_scale);
   return launch_status("fp8_mfma_kernel");
 }
