@@ -148,9 +148,11 @@ def kernel_rooflines(split):
     m, k, n = 1024, 4096, 12288
     a8 = torch.randint(0, 0x7e, (m, k), dtype=torch.uint8, device="cuda", generator=g)
     w8 = torch.randint(0, 0x7e, (n, k), dtype=torch.uint8, device="cuda", generator=g)
-    y8 = torch.empty(m, n, device="cuda")
+    # BF16 output, the projection's own output type (each value is
+    # bf16(acc * output_scale)), as the model writes it.
+    y8 = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
     for mode, name in ((0, "fp8_k32"), (1, "fp8_k128")):
-        ms = event_time(lambda: native.call("evo_hip_fp8_linear", a8.data_ptr(),
+        ms = event_time(lambda: native.call("evo_hip_fp8_linear_bf16", a8.data_ptr(),
                                             w8.data_ptr(), y8.data_ptr(), m, n, k, 1e-3,
                                             mode, stream), 10)
         flops = 2.0 * m * n * k

@@ -648,6 +648,18 @@ evo_status evo_hip_fp8_linear(const uint8_t *in_codes, const uint8_t *w_codes, f
   });
 }
 
+evo_status evo_hip_fp8_linear_bf16(const uint8_t *in_codes, const uint8_t *w_codes,
+                                   uint16_t *out, size_t m, size_t n, size_t k,
+                                   float output_scale, int mode, void *stream) {
+  return protect([&]() -> evo_status {
+    if (mode < 0 || mode > 2)
+      return publish(EVO_STATUS_INVALID_ARGUMENT, "invalid_argument: unknown FP8 mode");
+    return publish(evo::hip::fp8_linear(in_codes, w_codes, out, m, n, k, output_scale,
+                                        static_cast<evo::hip::Fp8Mode>(mode),
+                                        static_cast<hipStream_t>(stream)));
+  });
+}
+
 evo_status evo_hip_split_f32(const float *x, size_t count, uint16_t *hi, uint16_t *lo,
                             void *stream) {
   return protect([&]() -> evo_status {

@@ -30,6 +30,8 @@ _OPS = {
     "evo_hip_e4m3_quantize": (c_int, [c_int, c_void, c_size, c_float, c_void, c_void]),
     "evo_hip_fp8_linear": (c_int, [c_void, c_void, c_void, c_size, c_size, c_size,
                                    c_float, c_int, c_void]),
+    "evo_hip_fp8_linear_bf16": (c_int, [c_void, c_void, c_void, c_size, c_size, c_size,
+                                   c_float, c_int, c_void]),
     "evo_hip_split_f32": (c_int, [c_void, c_size, c_void, c_void, c_void]),
     "evo_hip_linear": (c_int, [c_void, c_void, c_void, c_void, c_void, c_size, c_size,
                                c_size, c_void, c_void]),

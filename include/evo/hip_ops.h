@@ -105,6 +105,13 @@ EVO_API evo_status evo_hip_fp8_linear(const uint8_t *in_codes,
                                       float output_scale, int mode,
                                       void *stream);
 
+/* The same product stored as BF16 [M,N] (the projection's own output type:
+ * each value already is bf16(acc * output_scale)). */
+EVO_API evo_status evo_hip_fp8_linear_bf16(const uint8_t *in_codes,
+                                           const uint8_t *w_codes, uint16_t *out,
+                                           size_t m, size_t n, size_t k,
+                                           float output_scale, int mode, void *stream);
+
 /* GEMM activation layout: hi[i] = bf16(x[i]), lo[i] = bf16(x[i] - hi[i])
  * (lo may be NULL for BF16-only activations). */
 EVO_API evo_status evo_hip_split_f32(const float *x, size_t count, uint16_t *hi,

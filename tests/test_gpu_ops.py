@@ -107,6 +107,19 @@ def test_fp8_mfma_close_to_qgmma(mode, m, k, n):
     assert np.abs(actual - expected).max() <= 2.0 ** -6 * np.abs(expected).max()
 
 
+@pytest.mark.parametrize("mode", [N.FP8_MFMA_K32, N.FP8_MFMA_K128, N.FP8_EXACT])
+def test_fp8_linear_bf16_output_equals_f32_output(mode):
+    """BF16-output variant: bit-identical to the F32 output (every value is
+    already a BF16 number)."""
+    a, w = fp8_case(23, 300, 512, 200)
+    f32 = fp8_gpu(a, w, 0.03125, mode)
+    out = empty((300, 200), np.uint16)
+    N.call("evo_hip_fp8_linear_bf16", p(dev(a)), p(dev(w)), p(out), 300, 200, 512, 0.03125,
+           mode, stream())
+    assert np.array_equal(host(out).view(np.uint16), bf16_bits(f32))
+    assert np.array_equal(bf16_to_f32(bf16_bits(f32)), f32)
+
+
 def test_fp8_mfma_exact_on_representable_sums():
     """Codes restricted to +-{1, 1.5, 2}: every QGMMA term and partial sum is
     exact, so all three modes must agree bit for bit."""
