@@ -407,6 +407,119 @@ __global__ __launch_bounds__(512) void gemm_kernel(
   }
 }
 
+// ---- Few-row product (decode, M <= 4): each wave owns 8 weight rows and
+// streams them with 1 KB coalesced loads (lane l reads K elements
+// [k + 8 l, k + 8 l + 8)); the activation row is hi + lo in F32 and the dot
+// runs in F32 FMAs, then a wave reduction. The weights are read once, so the
+// product runs at the HBM rate that the 256 x 256 tile kernel cannot reach
+// with one row (it would fill N/256 CUs). Gated mode: the 8 rows are the l1
+// and l2 rows of 4 gated columns (32-row blocks alternate l1 / l2).
+constexpr int kGemvRows = 8;
+constexpr int kGemvMaxM = 4;
+
+template <bool kSplit>
+__global__ __launch_bounds__(256) void gemv_kernel(
+    const uint16_t *__restrict__ a_hi, const uint16_t *__restrict__ a_lo, int lda,
+    const uint16_t *__restrict__ W, int M, int N, int K, float *__restrict__ C,
+    uint16_t *__restrict__ c_hi, uint16_t *__restrict__ c_lo, int ldc,
+    const Epilogue epi) {
+  const int lane = threadIdx.x & 63;
+  const int unit = blockIdx.x * 4 + (threadIdx.x >> 6);  // this wave's 8 rows
+  const bool gated = epi.mode == kGemmGated;
+  int rows[kGemvRows];
+#pragma unroll
+  for (int r = 0; r < kGemvRows; ++r) {
+    if (gated) {
+      const int column = unit * 4 + (r & 3);  // gated column
+      rows[r] = (column / 32) * 64 + (r >= 4 ? 32 : 0) + column % 32;
+    } else {
+      rows[r] = unit * kGemvRows + r;
+    }
+  }
+  float acc[kGemvRows][kGemvMaxM];
+#pragma unroll
+  for (int r = 0; r < kGemvRows; ++r)
+#pragma unroll
+    for (int m = 0; m < kGemvMaxM; ++m)
+      acc[r][m] = 0.0F;
+  for (int k = lane * 8; k < K; k += 512) {
+    float x[kGemvMaxM][8];
+#pragma unroll
+    for (int m = 0; m < kGemvMaxM; ++m) {
+      if (m >= M)
+        break;
+      const uint4 h = *reinterpret_cast<const uint4 *>(a_hi + static_cast<size_t>(m) * lda + k);
+      const uint16_t *hs = reinterpret_cast<const uint16_t *>(&h);
+      uint4 l = make_uint4(0, 0, 0, 0);
+      if (kSplit)
+        l = *reinterpret_cast<const uint4 *>(a_lo + static_cast<size_t>(m) * lda + k);
+      const uint16_t *ls = reinterpret_cast<const uint16_t *>(&l);
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        x[m][e] = bf16_to_f32(hs[e]) + (kSplit ? bf16_to_f32(ls[e]) : 0.0F);
+    }
+#pragma unroll
+    for (int r = 0; r < kGemvRows; ++r) {
+      if (rows[r] >= N)
+        continue;
+      const uint4 wv = *reinterpret_cast<const uint4 *>(W + static_cast<size_t>(rows[r]) * K + k);
+      const uint16_t *ws = reinterpret_cast<const uint16_t *>(&wv);
+#pragma unroll
+      for (int m = 0; m < kGemvMaxM; ++m) {
+        if (m >= M)
+          break;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          acc[r][m] = fmaf(x[m][e], bf16_to_f32(ws[e]), acc[r][m]);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kGemvRows; ++r)
+#pragma unroll
+    for (int m = 0; m < kGemvMaxM; ++m) {
+      float v = acc[r][m];
+#pragma unroll
+      for (int offset = 32; offset > 0; offset >>= 1)
+        v += __shfl_xor(v, offset, 64);
+      acc[r][m] = v;
+    }
+  if (lane >= kGemvMaxM)
+    return;
+  const int m = lane;
+  if (m >= M)
+    return;
+  if (gated) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int column = unit * 4 + j;
+      if (column >= epi.gated_width || rows[j + 4] >= N)
+        continue;
+      const float first = acc[j][m], second = acc[j + 4][m];
+      const float value = (epi.gelu ? gelu_erf(first) : first) * second;
+      const size_t index = static_cast<size_t>(m) * ldc + column;
+      const uint16_t hi = f32_to_bf16(value);
+      c_hi[index] = hi;
+      if (c_lo != nullptr)
+        c_lo[index] = f32_to_bf16(value - bf16_to_f32(hi));
+    }
+    return;
+  }
+#pragma unroll
+  for (int r = 0; r < kGemvRows; ++r) {
+    const int column = rows[r];
+    if (column >= N)
+      continue;
+    const size_t index = static_cast<size_t>(m) * ldc + column;
+    float value = acc[r][m];
+    if (epi.mode == kGemmBias || epi.mode == kGemmBiasResidual)
+      value = value + bf16_to_f32(epi.bias[column]);
+    if (epi.mode == kGemmResidual || epi.mode == kGemmBiasResidual)
+      value = value + epi.residual[index];
+    C[index] = value;
+  }
+}
+
 __global__ void split_kernel(const float *__restrict__ x, size_t n,
                              uint16_t *__restrict__ hi, uint16_t *__restrict__ lo) {
   for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
@@ -458,6 +571,16 @@ Status gemm_bf16w(const Activation &a, const uint16_t *W, const GemmOutput &out,
   const dim3 grid(static_cast<unsigned>(tiles));
   const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
   const int lda = static_cast<int>(a.ld), ldc = static_cast<int>(out.ld);
+  if (M <= static_cast<size_t>(kGemvMaxM)) {
+    const dim3 gemv_grid(static_cast<unsigned>(ceil_div(N, 4 * kGemvRows)));
+    if (split)
+      hipLaunchKernelGGL(gemv_kernel<true>, gemv_grid, dim3(256), 0, stream, a.hi, a.lo, lda,
+                         W, m, n, k, out.f32, out.hi, out.lo, ldc, epi);
+    else
+      hipLaunchKernelGGL(gemv_kernel<false>, gemv_grid, dim3(256), 0, stream, a.hi, a.lo,
+                         lda, W, m, n, k, out.f32, out.hi, out.lo, ldc, epi);
+    return launch_status("gemv_kernel");
+  }
   if (K % kBK == 0) {
     if (split)
       hipLaunchKernelGGL(gemm_kernel<true>, grid, dim3(512), 0, stream, a.hi, a.lo, lda,

@@ -138,9 +138,12 @@ def test_fp8_mfma_exact_on_representable_sums():
 
 
 # ---------------------------------------------------------------- GEMM
-@pytest.mark.parametrize("m,n,k", [(1, 40, 64), (130, 200, 72), (256, 384, 1024)])
+@pytest.mark.parametrize("m,n,k", [(1, 40, 64), (130, 200, 72), (256, 384, 1024),
+                                   (2, 4096, 4096), (3, 77, 11264), (4, 520, 1920),
+                                   (5, 96, 256)])
 @pytest.mark.parametrize("bias,residual", [(False, False), (True, True), (False, True)])
 def test_linear_split_matches_oracle(m, n, k, bias, residual):
+    """m <= 4 runs the few-row (decode) kernel, m >= 5 the MFMA tile kernel."""
     r = rng(m + n + k)
     x = r.standard_normal((m, k)).astype(np.float32)
     w = bf16_bits(r.standard_normal((n, k)).astype(np.float32) / np.sqrt(k))
@@ -186,10 +189,12 @@ def test_linear_bf16_profile_is_bf16_accurate():
 
 
 @pytest.mark.parametrize("gelu", [1, 0])
-def test_gated_mlp(gelu):
+@pytest.mark.parametrize("m", [70, 1, 3])
+def test_gated_mlp(gelu, m):
+    """m = 70: MFMA tiles; m = 1, 3: the few-row kernel's gated epilogue."""
     from scipy.special import erf
-    r = rng(17 + gelu)
-    m, width, inner = 70, 96, 80  # inner not a multiple of 32: padded block
+    r = rng(17 + gelu + m)
+    width, inner = 96, 80  # inner not a multiple of 32: padded block
     x = r.standard_normal((m, width)).astype(np.float32)
     l1 = bf16_bits(r.standard_normal((inner, width)).astype(np.float32) / 10)
     l2 = bf16_bits(r.standard_normal((inner, width)).astype(np.float32) / 10)
