@@ -292,6 +292,89 @@ __global__ __launch_bounds__(kWaves * 64) void fp8_mfma_kernel(
     }
 }
 
+// ---- Few-row projection (decode, M <= 4, MFMA modes): each 256-thread
+// block owns 8 weight rows, wave w the rows 2w and 2w+1 over all of K; lane
+// l reads 16 codes of a row per 1024-K sweep. Codes decode to F32 (the
+// hardware OCP-E4M3 convert), products are exact, and the lanes of one
+// kChunk-K group sum their partials by shuffles; the group sums go to LDS
+// and one thread per (row, activation row) then promotes them in K order,
+// acc = trunc_E8M13(acc + chunk), finishing with bf16(acc * output_scale).
+// The activation codes of the block's rows are decoded into LDS once.
+constexpr int kGemv8Rows = 8;
+constexpr int kGemv8MaxM = 4;
+constexpr int kGemv8MaxK = 8192;
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+__device__ inline void decode16(const uint4 codes, float (&out)[16]) {
+  const unsigned words[4] = {codes.x, codes.y, codes.z, codes.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(words[q]), false);
+    const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(words[q]), true);
+    out[4 * q] = lo.x;
+    out[4 * q + 1] = lo.y;
+    out[4 * q + 2] = hi.x;
+    out[4 * q + 3] = hi.y;
+  }
+}
+
+template <int kChunk, typename Out>
+__global__ __launch_bounds__(256) void fp8_gemv_kernel(
+    const uint8_t *__restrict__ a, const uint8_t *__restrict__ w, Out *__restrict__ out,
+    int M, int N, int K, float output_scale) {
+  constexpr int kLanesPerChunk = kChunk / 16;
+  // LDS: decoded activation rows a_s[M][K], then chunk sums [8][M][K/kChunk].
+  extern __shared__ float gemv8_lds[];
+  float *a_s = gemv8_lds;
+  float *chunk_s = gemv8_lds + M * K;
+  const int chunks = K / kChunk;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int i = tid * 16; i < M * K; i += 256 * 16) {
+    float v[16];
+    decode16(*reinterpret_cast<const uint4 *>(a + (i / K) * static_cast<size_t>(K) + i % K), v);
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      a_s[i + e] = v[e];
+  }
+  __syncthreads();
+  const int row0 = blockIdx.x * kGemv8Rows + wave * 2;
+  for (int k = lane * 16; k < K; k += 1024) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int row = row0 + r;
+      float wv[16];
+      decode16(row < N ? *reinterpret_cast<const uint4 *>(w + static_cast<size_t>(row) * K + k)
+                       : make_uint4(0, 0, 0, 0), wv);
+#pragma unroll
+      for (int m = 0; m < kGemv8MaxM; ++m) {
+        if (m >= M)
+          break;
+        float sum = 0.0F;
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          sum = fmaf(a_s[m * K + k + e], wv[e], sum);
+#pragma unroll
+        for (int offset = 1; offset < kLanesPerChunk; offset <<= 1)
+          sum += __shfl_xor(sum, offset, 64);
+        if ((lane % kLanesPerChunk) == 0)
+          chunk_s[((wave * 2 + r) * M + m) * chunks + k / kChunk] = sum;
+      }
+    }
+  }
+  __syncthreads();
+  if (tid >= kGemv8Rows * kGemv8MaxM)
+    return;
+  const int r = tid / kGemv8MaxM, m = tid % kGemv8MaxM;
+  const int row = blockIdx.x * kGemv8Rows + r;
+  if (m >= M || row >= N)
+    return;
+  float acc = 0.0F;
+  for (int c = 0; c < chunks; ++c)
+    acc = truncate_e8m13(acc + chunk_s[(r * M + m) * chunks + c]);
+  put(out, static_cast<size_t>(m) * N + row, round_bf16(acc * output_scale));
+}
+
 unsigned elementwise_grid(size_t n) {
   const size_t blocks = (n + 255) / 256;
   return static_cast<unsigned>(blocks < 16384 ? blocks : 16384);
@@ -340,6 +423,21 @@ Status fp8_linear_impl(const uint8_t *in_codes, const uint8_t *w_codes, Out *out
     return {ErrorCode::kInvalidArgument, "fp8_linear: MFMA modes need K % 128 == 0"};
   if (mode != kFp8MfmaK32 && mode != kFp8MfmaK128)
     return {ErrorCode::kInvalidArgument, "fp8_linear: unknown mode"};
+  if (M <= static_cast<size_t>(kGemv8MaxM) && K <= static_cast<size_t>(kGemv8MaxK)) {
+    const dim3 grid(static_cast<unsigned>(ceil_div(N, kGemv8Rows)));
+    const int chunk = mode == kFp8MfmaK32 ? 32 : 128;
+    const size_t lds = (M * K + kGemv8Rows * M * (K / chunk)) * sizeof(float);
+    const auto kernel = mode == kFp8MfmaK32 ? fp8_gemv_kernel<32, Out>
+                                            : fp8_gemv_kernel<128, Out>;
+    if (lds > 64 * 1024)
+      EVO_TRY(hip_status(hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             static_cast<int>(lds)),
+                         "fp8_gemv_kernel LDS opt-in"));
+    hipLaunchKernelGGL(kernel, grid, dim3(256), lds, stream, in_codes, w_codes, out, m, n, k,
+                       output_scale);
+    return launch_status("fp8_gemv_kernel");
+  }
   const auto kernel = mode == kFp8MfmaK32 ? fp8_mfma_kernel<32, Out> : fp8_mfma_kernel<128, Out>;
   // 112 KB of the CU's 160 KB LDS: opt in above the 64 KB default.
   EVO_TRY(hip_status(hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),

@@ -407,13 +407,15 @@ __global__ __launch_bounds__(512) void gemm_kernel(
   }
 }
 
-// ---- Few-row product (decode, M <= 4): each wave owns 8 weight rows and
-// streams them with 1 KB coalesced loads (lane l reads K elements
-// [k + 8 l, k + 8 l + 8)); the activation row is hi + lo in F32 and the dot
-// runs in F32 FMAs, then a wave reduction. The weights are read once, so the
-// product runs at the HBM rate that the 256 x 256 tile kernel cannot reach
-// with one row (it would fill N/256 CUs). Gated mode: the 8 rows are the l1
-// and l2 rows of 4 gated columns (32-row blocks alternate l1 / l2).
+// ---- Few-row product (decode, M <= 4): each 256-thread block owns 8
+// weight rows and its 4 waves split K (wave w takes the 512-element K
+// chunks w, w+4, ...); lane l reads K elements [k + 8 l, k + 8 l + 8) of a
+// row, 1 KB coalesced per load. The activation row is hi + lo in F32 and
+// the dot runs in F32 FMAs; wave partials are reduced by shuffles, then
+// across the 4 waves through LDS. The weights are read once, so the
+// product runs at the HBM rate the 256 x 256 tile kernel cannot reach with
+// one row (it would fill N/256 CUs). Gated mode: the 8 rows are the l1 and
+// l2 rows of 4 gated columns (32-row blocks alternate l1 / l2).
 constexpr int kGemvRows = 8;
 constexpr int kGemvMaxM = 4;
 
@@ -423,8 +425,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(
     const uint16_t *__restrict__ W, int M, int N, int K, float *__restrict__ C,
     uint16_t *__restrict__ c_hi, uint16_t *__restrict__ c_lo, int ldc,
     const Epilogue epi) {
-  const int lane = threadIdx.x & 63;
-  const int unit = blockIdx.x * 4 + (threadIdx.x >> 6);  // this wave's 8 rows
+  __shared__ float partial[4][kGemvRows][kGemvMaxM];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int unit = blockIdx.x;  // this block's 8 rows
   const bool gated = epi.mode == kGemmGated;
   int rows[kGemvRows];
 #pragma unroll
@@ -442,7 +445,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(
 #pragma unroll
     for (int m = 0; m < kGemvMaxM; ++m)
       acc[r][m] = 0.0F;
-  for (int k = lane * 8; k < K; k += 512) {
+  for (int k = wave * 512 + lane * 8; k < K; k += 2048) {
     float x[kGemvMaxM][8];
 #pragma unroll
     for (int m = 0; m < kGemvMaxM; ++m) {
@@ -458,12 +461,15 @@ __global__ __launch_bounds__(256) void gemv_kernel(
       for (int e = 0; e < 8; ++e)
         x[m][e] = bf16_to_f32(hs[e]) + (kSplit ? bf16_to_f32(ls[e]) : 0.0F);
     }
+    uint4 wv[kGemvRows];
+#pragma unroll
+    for (int r = 0; r < kGemvRows; ++r)
+      wv[r] = rows[r] < N ? *reinterpret_cast<const uint4 *>(
+                                W + static_cast<size_t>(rows[r]) * K + k)
+                          : make_uint4(0, 0, 0, 0);
 #pragma unroll
     for (int r = 0; r < kGemvRows; ++r) {
-      if (rows[r] >= N)
-        continue;
-      const uint4 wv = *reinterpret_cast<const uint4 *>(W + static_cast<size_t>(rows[r]) * K + k);
-      const uint16_t *ws = reinterpret_cast<const uint16_t *>(&wv);
+      const uint16_t *ws = reinterpret_cast<const uint16_t *>(&wv[r]);
 #pragma unroll
       for (int m = 0; m < kGemvMaxM; ++m) {
         if (m >= M)
@@ -482,20 +488,26 @@ __global__ __launch_bounds__(256) void gemv_kernel(
 #pragma unroll
       for (int offset = 32; offset > 0; offset >>= 1)
         v += __shfl_xor(v, offset, 64);
-      acc[r][m] = v;
+      if (lane == 0)
+        partial[wave][r][m] = v;
     }
-  if (lane >= kGemvMaxM)
+  __syncthreads();
+  if (wave != 0 || lane >= kGemvMaxM)
     return;
   const int m = lane;
   if (m >= M)
     return;
+  float total[kGemvRows];
+#pragma unroll
+  for (int r = 0; r < kGemvRows; ++r)
+    total[r] = partial[0][r][m] + partial[1][r][m] + partial[2][r][m] + partial[3][r][m];
   if (gated) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int column = unit * 4 + j;
       if (column >= epi.gated_width || rows[j + 4] >= N)
         continue;
-      const float first = acc[j][m], second = acc[j + 4][m];
+      const float first = total[j], second = total[j + 4];
       const float value = (epi.gelu ? gelu_erf(first) : first) * second;
       const size_t index = static_cast<size_t>(m) * ldc + column;
       const uint16_t hi = f32_to_bf16(value);
@@ -511,7 +523,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(
     if (column >= N)
       continue;
     const size_t index = static_cast<size_t>(m) * ldc + column;
-    float value = acc[r][m];
+    float value = total[r];
     if (epi.mode == kGemmBias || epi.mode == kGemmBiasResidual)
       value = value + bf16_to_f32(epi.bias[column]);
     if (epi.mode == kGemmResidual || epi.mode == kGemmBiasResidual)
@@ -572,7 +584,7 @@ Status gemm_bf16w(const Activation &a, const uint16_t *W, const GemmOutput &out,
   const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
   const int lda = static_cast<int>(a.ld), ldc = static_cast<int>(out.ld);
   if (M <= static_cast<size_t>(kGemvMaxM)) {
-    const dim3 gemv_grid(static_cast<unsigned>(ceil_div(N, 4 * kGemvRows)));
+    const dim3 gemv_grid(static_cast<unsigned>(ceil_div(N, kGemvRows)));
     if (split)
       hipLaunchKernelGGL(gemv_kernel<true>, gemv_grid, dim3(256), 0, stream, a.hi, a.lo, lda,
                          W, m, n, k, out.f32, out.hi, out.lo, ldc, epi);

@@ -603,7 +603,36 @@ __global__ void inner_history_kernel(const T *__restrict__ P,
   load_short_taps(short_filter, short_len, c, taps);
   const size_t cols3 = 3 * W;
   // With L >= hist every new row comes from u and rows are independent: one
-  // block row per history row. Otherwise rows shift in place, oldest first.
+  // block row per history row. Otherwise rows shift in place, oldest first:
+  // the old rows of a 32-row batch are loaded before any of them is
+  // overwritten (they only move to lower indices).
+  if (gridDim.y == 1 && static_cast<long>(L) < hist) {
+    constexpr int kShift = 32;
+    for (int h0 = 0; h0 < hist; h0 += kShift) {
+      float moved[kShift];
+#pragma unroll
+      for (int j = 0; j < kShift; ++j) {
+        const long source = static_cast<long>(h0 + j) + static_cast<long>(L);
+        moved[j] = (h0 + j < hist && source < hist)
+                       ? inner_history[static_cast<size_t>(source) * W + c] : 0.0F;
+      }
+#pragma unroll
+      for (int j = 0; j < kShift; ++j) {
+        const int h = h0 + j;
+        if (h >= hist)
+          break;
+        const long source = static_cast<long>(h) + static_cast<long>(L);
+        float value = moved[j];
+        if (source >= hist) {
+          float x2, u;
+          gates(P, short_history, taps, short_len, cols3, planar, source - hist, c, &x2, &u);
+          value = u;
+        }
+        inner_history[static_cast<size_t>(h) * W + c] = value;
+      }
+    }
+    return;
+  }
   const int h_begin = gridDim.y > 1 ? static_cast<int>(blockIdx.y) : 0;
   const int h_end = gridDim.y > 1 ? h_begin + 1 : hist;
   for (int h = h_begin; h < h_end; ++h) {
