@@ -300,7 +300,7 @@ __global__ __launch_bounds__(kWaves * 64) void fp8_mfma_kernel(
 // and one thread per (row, activation row) then promotes them in K order,
 // acc = trunc_E8M13(acc + chunk), finishing with bf16(acc * output_scale).
 // The activation codes of the block's rows are decoded into LDS once.
-constexpr int kGemv8Rows = 8;
+constexpr int kGemv8Rows = 16;
 constexpr int kGemv8MaxM = 4;
 constexpr int kGemv8MaxK = 8192;
 
@@ -324,28 +324,30 @@ __global__ __launch_bounds__(256) void fp8_gemv_kernel(
     const uint8_t *__restrict__ a, const uint8_t *__restrict__ w, Out *__restrict__ out,
     int M, int N, int K, float output_scale) {
   constexpr int kLanesPerChunk = kChunk / 16;
-  // LDS: decoded activation rows a_s[M][K], then chunk sums [8][M][K/kChunk].
-  extern __shared__ float gemv8_lds[];
-  float *a_s = gemv8_lds;
-  float *chunk_s = gemv8_lds + M * K;
+  constexpr int kRowsPerWave = kGemv8Rows / 4;
+  // LDS: chunk sums [kGemv8Rows][M][K/kChunk].
+  extern __shared__ float chunk_s[];
   const int chunks = K / kChunk;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  for (int i = tid * 16; i < M * K; i += 256 * 16) {
-    float v[16];
-    decode16(*reinterpret_cast<const uint4 *>(a + (i / K) * static_cast<size_t>(K) + i % K), v);
-#pragma unroll
-    for (int e = 0; e < 16; ++e)
-      a_s[i + e] = v[e];
-  }
-  __syncthreads();
-  const int row0 = blockIdx.x * kGemv8Rows + wave * 2;
+  const int row0 = blockIdx.x * kGemv8Rows + wave * kRowsPerWave;
   for (int k = lane * 16; k < K; k += 1024) {
+    float av[kGemv8MaxM][16];
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int row = row0 + r;
+    for (int m = 0; m < kGemv8MaxM; ++m) {
+      if (m >= M)
+        break;
+      decode16(*reinterpret_cast<const uint4 *>(a + static_cast<size_t>(m) * K + k), av[m]);
+    }
+    uint4 codes[kRowsPerWave];
+#pragma unroll
+    for (int r = 0; r < kRowsPerWave; ++r)
+      codes[r] = row0 + r < N ? *reinterpret_cast<const uint4 *>(
+                                    w + static_cast<size_t>(row0 + r) * K + k)
+                              : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < kRowsPerWave; ++r) {
       float wv[16];
-      decode16(row < N ? *reinterpret_cast<const uint4 *>(w + static_cast<size_t>(row) * K + k)
-                       : make_uint4(0, 0, 0, 0), wv);
+      decode16(codes[r], wv);
 #pragma unroll
       for (int m = 0; m < kGemv8MaxM; ++m) {
         if (m >= M)
@@ -353,12 +355,12 @@ __global__ __launch_bounds__(256) void fp8_gemv_kernel(
         float sum = 0.0F;
 #pragma unroll
         for (int e = 0; e < 16; ++e)
-          sum = fmaf(a_s[m * K + k + e], wv[e], sum);
+          sum = fmaf(av[m][e], wv[e], sum);
 #pragma unroll
         for (int offset = 1; offset < kLanesPerChunk; offset <<= 1)
           sum += __shfl_xor(sum, offset, 64);
         if ((lane % kLanesPerChunk) == 0)
-          chunk_s[((wave * 2 + r) * M + m) * chunks + k / kChunk] = sum;
+          chunk_s[((wave * kRowsPerWave + r) * M + m) * chunks + k / kChunk] = sum;
       }
     }
   }
@@ -426,7 +428,7 @@ Status fp8_linear_impl(const uint8_t *in_codes, const uint8_t *w_codes, Out *out
   if (M <= static_cast<size_t>(kGemv8MaxM) && K <= static_cast<size_t>(kGemv8MaxK)) {
     const dim3 grid(static_cast<unsigned>(ceil_div(N, kGemv8Rows)));
     const int chunk = mode == kFp8MfmaK32 ? 32 : 128;
-    const size_t lds = (M * K + kGemv8Rows * M * (K / chunk)) * sizeof(float);
+    const size_t lds = kGemv8Rows * M * (K / chunk) * sizeof(float);
     const auto kernel = mode == kFp8MfmaK32 ? fp8_gemv_kernel<32, Out>
                                             : fp8_gemv_kernel<128, Out>;
     if (lds > 64 * 1024)

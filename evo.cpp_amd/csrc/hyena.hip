@@ -603,36 +603,7 @@ __global__ void inner_history_kernel(const T *__restrict__ P,
   load_short_taps(short_filter, short_len, c, taps);
   const size_t cols3 = 3 * W;
   // With L >= hist every new row comes from u and rows are independent: one
-  // block row per history row. Otherwise rows shift in place, oldest first:
-  // the old rows of a 32-row batch are loaded before any of them is
-  // overwritten (they only move to lower indices).
-  if (gridDim.y == 1 && static_cast<long>(L) < hist) {
-    constexpr int kShift = 32;
-    for (int h0 = 0; h0 < hist; h0 += kShift) {
-      float moved[kShift];
-#pragma unroll
-      for (int j = 0; j < kShift; ++j) {
-        const long source = static_cast<long>(h0 + j) + static_cast<long>(L);
-        moved[j] = (h0 + j < hist && source < hist)
-                       ? inner_history[static_cast<size_t>(source) * W + c] : 0.0F;
-      }
-#pragma unroll
-      for (int j = 0; j < kShift; ++j) {
-        const int h = h0 + j;
-        if (h >= hist)
-          break;
-        const long source = static_cast<long>(h) + static_cast<long>(L);
-        float value = moved[j];
-        if (source >= hist) {
-          float x2, u;
-          gates(P, short_history, taps, short_len, cols3, planar, source - hist, c, &x2, &u);
-          value = u;
-        }
-        inner_history[static_cast<size_t>(h) * W + c] = value;
-      }
-    }
-    return;
-  }
+  // block row per history row. Otherwise rows shift in place, oldest first.
   const int h_begin = gridDim.y > 1 ? static_cast<int>(blockIdx.y) : 0;
   const int h_end = gridDim.y > 1 ? h_begin + 1 : hist;
   for (int h = h_begin; h < h_end; ++h) {
@@ -645,6 +616,39 @@ __global__ void inner_history_kernel(const T *__restrict__ P,
       float x2, u;
       gates(P, short_history, taps, short_len, cols3, planar, t, c, &x2, &u);
       value = u;
+    }
+    inner_history[static_cast<size_t>(h) * W + c] = value;
+  }
+}
+
+// Short continuation (L < hist): history <- last hist rows of [history ; u]
+// for 64 channels per block. All old rows that survive are read into LDS
+// before any row is rewritten, so every (row, channel) runs in parallel.
+template <typename T>
+__global__ __launch_bounds__(256) void inner_history_shift_kernel(
+    const T *__restrict__ P, const float *__restrict__ short_history,
+    const uint16_t *__restrict__ short_filter, int short_len, size_t L, size_t W,
+    size_t planar, float *inner_history, int hist) {
+  extern __shared__ float shift_s[];  // [hist][64]
+  const int lane = threadIdx.x & 63;
+  const size_t c = blockIdx.x * 64ULL + lane;
+  const bool valid = c < W;
+  const int keep = hist - static_cast<int>(L);  // rows that move down by L
+  for (int h = threadIdx.x >> 6; h < keep; h += 4)
+    shift_s[h * 64 + lane] = valid ? inner_history[(h + L) * W + c] : 0.0F;
+  __syncthreads();
+  if (!valid)
+    return;
+  float taps[3][kMaxShort];
+  load_short_taps(short_filter, short_len, c, taps);
+  const size_t cols3 = 3 * W;
+  for (int h = threadIdx.x >> 6; h < hist; h += 4) {
+    float value;
+    if (h < keep) {
+      value = shift_s[h * 64 + lane];
+    } else {
+      float x2;
+      gates(P, short_history, taps, short_len, cols3, planar, h - keep, c, &x2, &value);
     }
     inner_history[static_cast<size_t>(h) * W + c] = value;
   }
@@ -817,10 +821,16 @@ Status hyena_forward(int kind, const T *projection, size_t length,
     }
     EVO_TRY(launch_status("hyena_fir_kernel"));
     if (inner_history != nullptr && k > 1) {
-      const unsigned rows = length >= static_cast<size_t>(k - 1) ? static_cast<unsigned>(k - 1) : 1;
-      hipLaunchKernelGGL(inner_history_kernel<T>, dim3(ceil_div(width, 256), rows), dim3(256), 0,
-                         stream, projection, short_history, wt.short_filter,
-                         short_len, length, width, planar, inner_history, k - 1);
+      if (length >= static_cast<size_t>(k - 1)) {
+        hipLaunchKernelGGL(inner_history_kernel<T>, dim3(ceil_div(width, 256), k - 1),
+                           dim3(256), 0, stream, projection, short_history, wt.short_filter,
+                           short_len, length, width, planar, inner_history, k - 1);
+      } else {
+        const size_t lds = static_cast<size_t>(k - 1) * 64 * sizeof(float);  // <= 32.5 KB
+        hipLaunchKernelGGL(inner_history_shift_kernel<T>, dim3(ceil_div(width, 64)), dim3(256),
+                           lds, stream, projection, short_history, wt.short_filter, short_len,
+                           length, width, planar, inner_history, k - 1);
+      }
       EVO_TRY(launch_status("inner_history_kernel"));
     }
   } else {
