@@ -142,6 +142,21 @@ __device__ inline void put(const SplitOut &out, size_t i, float v) {
     out.lo[i] = f32_to_bf16(v - bf16_to_f32(hi));
 }
 
+// Non-temporal variants for outputs no later part of the producing kernel
+// reads: the stores stream past the L2 instead of evicting its input lines.
+__device__ inline void put_nt(float *out, size_t i, float v) {
+  __builtin_nontemporal_store(v, out + i);
+}
+__device__ inline void put_nt(uint16_t *out, size_t i, float v) {
+  __builtin_nontemporal_store(f32_to_bf16(v), out + i);
+}
+__device__ inline void put_nt(const SplitOut &out, size_t i, float v) {
+  const uint16_t hi = f32_to_bf16(v);
+  __builtin_nontemporal_store(hi, out.hi + i);
+  if (out.lo != nullptr)
+    __builtin_nontemporal_store(f32_to_bf16(v - bf16_to_f32(hi)), out.lo + i);
+}
+
 inline Status hip_status(const hipError_t error, const char *what) {
   if (error == hipSuccess)
     return Status::Ok();

@@ -280,7 +280,7 @@ __global__ __launch_bounds__(kChannels) void hcl_output_kernel(
         s[m] = p[m] * s[m] + u;
         modal += r[m] * s[m];
       }
-      put(out, (t + b) * W + c, x2 * (modal + d * u));
+      put_nt(out, (t + b) * W + c, x2 * (modal + d * u));
     }
   }
 }
@@ -350,6 +350,261 @@ __global__ __launch_bounds__(256) void hyena_fir_kernel(
     if (direct != nullptr)
       total += d * current;
     put(out, static_cast<size_t>(t) * W + c, x2_s[r * 64 + lane] * total);
+  }
+}
+
+// ---- Short grouped FIR (k <= 8, HCS) as a row stream on the VALU.
+// Each lane owns two adjacent channels: their six interleaved projection
+// columns are 12 (BF16) or 24 (F32) contiguous bytes of a row, and the two
+// outputs are one packed 32-bit store per plane. A wave streams a segment of
+// kStreamRows rows; it starts kLead rows early so that its short-FIR window
+// and its FIR window of u are full when the segment begins (the lead rows are
+// recomputed, not stored). Both windows hold their taps right-aligned with
+// zeros in front, so every sum runs oldest first as in the reference; with
+// kWin == short_len and kTaps == k there are no zero taps. Rows are fetched
+// in batches of kStreamBatch with the next batch in flight while the current
+// one is evaluated. Stores go through a buffer resource bounded to the
+// segment, so rows past the sequence end are dropped by the hardware, and
+// are non-temporal: the outputs are never re-read here, and streaming them
+// past the L2 keeps it for the projection rows (-23 % kernel time on the 7B
+// shape).
+constexpr int kStreamRows = 64;
+constexpr int kStreamBatch = 4;
+constexpr int kStreamWaves = 4;              // waves per block
+constexpr int kStreamChannels = kStreamWaves * 64 * 2;
+constexpr int kStreamStore = 2;              // buffer store cache policy: nt
+
+// Six projection values (channel c: x2, x1, v; channel c + 1: x2, x1, v) of
+// one row as 32-bit words (three for BF16, six for F32); rows past the
+// resource bound read 0.
+template <typename T> struct PairRow {
+  static constexpr int kWords = 3 * static_cast<int>(sizeof(T)) / 2;
+  uint32_t word[kWords];
+  __device__ void load(__amdgpu_buffer_rsrc_t resource, uint32_t lane, uint32_t row) {
+#pragma unroll
+    for (int i = 0; i < kWords; ++i)
+      word[i] = __builtin_amdgcn_raw_buffer_load_b32(resource, static_cast<int>(lane + 4 * i),
+                                                     static_cast<int>(row), 0);
+  }
+  __device__ float at(int i) const {
+    if constexpr (sizeof(T) == 2)
+      return __builtin_bit_cast(float, (i & 1) != 0 ? word[i >> 1] & 0xffff0000U
+                                                    : word[i >> 1] << 16);
+    else
+      return __builtin_bit_cast(float, word[i]);
+  }
+};
+
+__device__ inline uint32_t pack_bf16(float a, float b) {
+  return static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
+}
+
+// Output of a channel pair through segment-bounded buffer resources:
+// `lane` is the pair's byte offset within a row of one plane, `row` the
+// row's byte offset from the segment start.
+template <typename O> struct PairOut;
+template <> struct PairOut<float *> {
+  __amdgpu_buffer_rsrc_t out;
+  __device__ PairOut(float *o, size_t first, size_t rows, size_t W) {
+    out = buffer_resource(o + first * W, static_cast<uint32_t>(rows * W * 4));
+  }
+  __device__ void put(uint32_t lane, uint32_t row, float a, float b) const {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, a), out,
+                                          static_cast<int>(2 * lane), static_cast<int>(2 * row),
+                                          kStreamStore);
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, b), out,
+                                          static_cast<int>(2 * lane + 4), static_cast<int>(2 * row),
+                                          kStreamStore);
+  }
+};
+template <> struct PairOut<uint16_t *> {
+  __amdgpu_buffer_rsrc_t out;
+  __device__ PairOut(uint16_t *o, size_t first, size_t rows, size_t W) {
+    out = buffer_resource(o + first * W, static_cast<uint32_t>(rows * W * 2));
+  }
+  __device__ void put(uint32_t lane, uint32_t row, float a, float b) const {
+    __builtin_amdgcn_raw_buffer_store_b32(pack_bf16(a, b), out, static_cast<int>(lane),
+                                          static_cast<int>(row), kStreamStore);
+  }
+};
+template <> struct PairOut<SplitOut> {
+  __amdgpu_buffer_rsrc_t hi, lo;
+  bool has_lo;
+  __device__ PairOut(const SplitOut &o, size_t first, size_t rows, size_t W) {
+    hi = buffer_resource(o.hi + first * W, static_cast<uint32_t>(rows * W * 2));
+    has_lo = o.lo != nullptr;
+    lo = buffer_resource(has_lo ? o.lo + first * W : o.hi, has_lo ? static_cast<uint32_t>(rows * W * 2) : 0);
+  }
+  __device__ void put(uint32_t lane, uint32_t row, float a, float b) const {
+    const uint32_t h = pack_bf16(a, b);
+    __builtin_amdgcn_raw_buffer_store_b32(h, hi, static_cast<int>(lane), static_cast<int>(row),
+                                          kStreamStore);
+    // With no lo plane the resource has zero size and the store is dropped.
+    __builtin_amdgcn_raw_buffer_store_b32(
+        pack_bf16(a - __builtin_bit_cast(float, h << 16),
+                  b - __builtin_bit_cast(float, h & 0xffff0000U)),
+        lo, static_cast<int>(lane), static_cast<int>(row), kStreamStore);
+  }
+};
+
+template <typename T, int kWin, int kTaps, bool kDirect>
+struct PairFir {
+  float stap[6][kWin], ftap[kTaps], d[2];
+  float swin[6][kWin], uwin[2][kTaps];  // slot kWin-1 / kTaps-1 is the newest
+
+  // One row: shifts the six projection values and u into the windows and
+  // returns the pair's outputs y = x2 * (FIR(u) [+ d * u]).
+  __device__ void step(const PairRow<T> &row, float (&y)[2]) {
+    float fir[6];
+#pragma unroll
+    for (int col = 0; col < 6; ++col) {
+#pragma unroll
+      for (int i = 0; i < kWin - 1; ++i)
+        swin[col][i] = swin[col][i + 1];
+      swin[col][kWin - 1] = row.at(col);
+      float total = 0.0F;
+#pragma unroll
+      for (int i = 0; i < kWin; ++i)
+        total += swin[col][i] * stap[col][i];
+      fir[col] = total;
+    }
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) {
+      const float u = fir[3 * ch + 1] * fir[3 * ch + 2];
+#pragma unroll
+      for (int i = 0; i < kTaps - 1; ++i)
+        uwin[ch][i] = uwin[ch][i + 1];
+      uwin[ch][kTaps - 1] = u;
+      float total = 0.0F;
+#pragma unroll
+      for (int i = 0; i < kTaps; ++i)
+        total += uwin[ch][i] * ftap[i];
+      if constexpr (kDirect)
+        total += d[ch] * u;
+      y[ch] = fir[3 * ch] * total;
+    }
+  }
+};
+
+template <typename T, typename O, int kWin, int kTaps, bool kDirect>
+__global__ __launch_bounds__(kStreamWaves * 64) void hyena_fir_stream_kernel(
+    const T *__restrict__ P, const float *__restrict__ short_history,
+    const uint16_t *__restrict__ short_filter, int short_len,
+    const float *__restrict__ inner_history, const float *__restrict__ filter,
+    size_t group_size, int k, int causal, const float *__restrict__ direct,
+    size_t L, size_t W, unsigned channel_blocks, unsigned segments, O out) {
+  constexpr int kLead = (kTaps - 1) + (kWin - 1);
+  // XCD-aware order: consecutive hardware ids go to different XCDs, so each
+  // XCD takes a contiguous band of segments (neighbouring segments share
+  // their lead rows through that XCD's L2).
+  const unsigned total = channel_blocks * segments;
+  const unsigned xcd = blockIdx.x % 8, q = total / 8, r = total % 8;
+  const unsigned linear = xcd * q + min(xcd, r) + blockIdx.x / 8;
+  const unsigned segment = linear / channel_blocks;
+  const unsigned cblock = linear % channel_blocks;
+  const int lane = threadIdx.x & 63;
+  const size_t c = cblock * static_cast<size_t>(kStreamChannels) +
+                   (threadIdx.x >> 6) * 128 + 2 * lane;
+  if (c >= W)
+    return;
+  const size_t t0 = static_cast<size_t>(segment) * kStreamRows;
+  const uint32_t seg_rows = static_cast<uint32_t>(min(L - t0, static_cast<size_t>(kStreamRows)));
+  const size_t cols3 = 3 * W;
+
+  PairFir<T, kWin, kTaps, kDirect> fir;
+#pragma unroll
+  for (int ch = 0; ch < 2; ++ch) {
+    float t3[3][kWin];
+    load_window_taps(short_filter, short_len, c + ch, t3);
+#pragma unroll
+    for (int s = 0; s < 3; ++s)
+#pragma unroll
+      for (int i = 0; i < kWin; ++i)
+        fir.stap[3 * ch + s][i] = t3[s][i];
+  }
+  const float *h = filter + (c / group_size) * k;
+#pragma unroll
+  for (int i = 0; i < kTaps; ++i) {
+    const int j = i - (kTaps - k);
+    fir.ftap[i] = j >= 0 ? h[causal ? k - 1 - j : j] : 0.0F;
+  }
+  if constexpr (kDirect) {
+    fir.d[0] = direct[c];
+    fir.d[1] = direct[c + 1];
+  }
+
+  const uint32_t row_bytes = static_cast<uint32_t>(cols3 * sizeof(T));
+  const uint32_t lane_bytes = static_cast<uint32_t>(3 * c * sizeof(T));
+  if (t0 >= static_cast<size_t>(kLead)) {
+    // Interior segment: stream the lead rows through zeroed windows.
+#pragma unroll
+    for (int col = 0; col < 6; ++col)
+#pragma unroll
+      for (int i = 0; i < kWin; ++i)
+        fir.swin[col][i] = 0.0F;
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+      for (int i = 0; i < kTaps; ++i)
+        fir.uwin[ch][i] = 0.0F;
+    const auto lead = buffer_resource(P + (t0 - kLead) * cols3, kLead * row_bytes);
+    PairRow<T> rows[kLead];
+#pragma unroll
+    for (int b = 0; b < kLead; ++b)
+      rows[b].load(lead, lane_bytes, b * row_bytes);
+#pragma unroll
+    for (int b = 0; b < kLead; ++b) {
+      float y[2];
+      fir.step(rows[b], y);
+    }
+  } else {
+    // First segment: the windows start from the caches (zeros without
+    // them); slot i holds row i - kWin (short FIR) or i - kTaps (u).
+#pragma unroll
+    for (int col = 0; col < 6; ++col)
+#pragma unroll
+      for (int i = 0; i < kWin; ++i) {
+        const long hrow = static_cast<long>(short_len - 1) + i - kWin;
+        fir.swin[col][i] = (short_history != nullptr && hrow >= 0)
+                               ? short_history[static_cast<size_t>(hrow) * cols3 + 3 * c + col]
+                               : 0.0F;
+      }
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+      for (int i = 0; i < kTaps; ++i) {
+        const long hrow = static_cast<long>(k - 1) + i - kTaps;
+        fir.uwin[ch][i] = (inner_history != nullptr && hrow >= 0)
+                              ? inner_history[static_cast<size_t>(hrow) * W + c + ch]
+                              : 0.0F;
+      }
+  }
+
+  // Segment rows: loads past the sequence end read 0, stores past it drop.
+  const auto in = buffer_resource(P + t0 * cols3, seg_rows * row_bytes);
+  const PairOut<O> sink(out, t0, seg_rows, W);
+  const uint32_t out_lane = static_cast<uint32_t>(c * 2);
+  const uint32_t out_row = static_cast<uint32_t>(W * 2);
+  PairRow<T> next[kStreamBatch];
+#pragma unroll
+  for (int b = 0; b < kStreamBatch; ++b)
+    next[b].load(in, lane_bytes, b * row_bytes);
+  for (uint32_t base = 0; base < seg_rows; base += kStreamBatch) {
+    PairRow<T> cur[kStreamBatch];
+#pragma unroll
+    for (int b = 0; b < kStreamBatch; ++b)
+      cur[b] = next[b];
+    if (base + kStreamBatch < seg_rows) {
+#pragma unroll
+      for (int b = 0; b < kStreamBatch; ++b)
+        next[b].load(in, lane_bytes, (base + kStreamBatch + b) * row_bytes);
+    }
+#pragma unroll
+    for (int b = 0; b < kStreamBatch; ++b) {
+      float y[2];
+      fir.step(cur[b], y);
+      sink.put(out_lane, (base + b) * out_row, y[0], y[1]);
+    }
   }
 }
 
@@ -584,7 +839,7 @@ __global__ __launch_bounds__(kFirThreads) void hyena_fir_mfma_kernel(
     const long t = t0 + r;
     if (t >= static_cast<long>(L))
       break;
-    put(out, static_cast<size_t>(t) * W + c, x2_s[r * kChannels + lane]);
+    put_nt(out, static_cast<size_t>(t) * W + c, x2_s[r * kChannels + lane]);
   }
 }
 
@@ -688,6 +943,43 @@ Status launch_hcl(const T *projection, const float *short_history, const HyenaWe
   return launch_status("hcl_output_kernel");
 }
 
+template <typename T, typename O, int kWin, int kTaps>
+void launch_fir_stream_taps(const T *projection, const float *short_history,
+                            const HyenaWeights &wt, int short_len, const float *inner_history,
+                            size_t group_size, int k, int causal, const float *direct,
+                            size_t length, size_t width, O out, hipStream_t stream) {
+  const unsigned cblocks = ceil_div(width, kStreamChannels);
+  const unsigned segments = ceil_div(length, kStreamRows);
+  const dim3 grid(cblocks * segments), block(kStreamWaves * 64);
+  if (direct != nullptr)
+    hipLaunchKernelGGL((hyena_fir_stream_kernel<T, O, kWin, kTaps, true>), grid, block, 0, stream,
+                       projection, short_history, wt.short_filter, short_len, inner_history,
+                       wt.inner_filter, group_size, k, causal, direct, length, width, cblocks,
+                       segments, out);
+  else
+    hipLaunchKernelGGL((hyena_fir_stream_kernel<T, O, kWin, kTaps, false>), grid, block, 0,
+                       stream, projection, short_history, wt.short_filter, short_len,
+                       inner_history, wt.inner_filter, group_size, k, causal, direct, length,
+                       width, cblocks, segments, out);
+}
+
+// Exact window widths for the 7B shape (short FIR 3, HCS 7 taps); other
+// lengths run zero-padded windows of 8.
+template <typename T, typename O>
+Status launch_fir_stream(const T *projection, const float *short_history,
+                         const HyenaWeights &wt, int short_len, const float *inner_history,
+                         size_t group_size, int k, int causal, const float *direct,
+                         size_t length, size_t width, O out, hipStream_t stream) {
+  if (short_len == 3 && k == 7)
+    launch_fir_stream_taps<T, O, 3, 7>(projection, short_history, wt, short_len, inner_history,
+                                       group_size, k, causal, direct, length, width, out, stream);
+  else
+    launch_fir_stream_taps<T, O, kMaxShort, 8>(projection, short_history, wt, short_len,
+                                               inner_history, group_size, k, causal, direct,
+                                               length, width, out, stream);
+  return launch_status("hyena_fir_stream_kernel");
+}
+
 template <typename T, typename O, int kMaxTaps>
 Status launch_fir_mfma(const T *projection, const float *short_history,
                        const HyenaWeights &wt, int short_len, const float *inner_history,
@@ -783,7 +1075,11 @@ Status hyena_forward(int kind, const T *projection, size_t length,
     const int causal = kind == kHyenaHcm ? 1 : 0;
     const float *direct = kind == kHyenaHcm ? wt.direct : nullptr;
     const size_t group_size = width / wt.groups;
-    if (width % kChannels == 0 && group_size % 16 == 0) {
+    if (k <= 8 && planar == 0 && width % 2 == 0 && group_size % 2 == 0) {
+      EVO_TRY((launch_fir_stream<T, O>(projection, short_history, wt, short_len, inner_history,
+                                       group_size, k, causal, direct, length, width, out,
+                                       stream)));
+    } else if (width % kChannels == 0 && group_size % 16 == 0) {
       const size_t steps = k <= 8 ? FirMfmaShape<8>::kSteps : FirMfmaShape<128>::kSteps;
       if (workspace == nullptr || workspace_bytes < wt.groups * steps * 2 * 64 * 16)
         return {ErrorCode::kInvalidArgument, "hyena_forward: FIR workspace too small"};
