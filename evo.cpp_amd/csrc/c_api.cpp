@@ -589,11 +589,13 @@ evo_status evo_hip_hyena_forward(evo_hip_hyena_kind kind, evo_hip_dtype dtype,
                                  float *modal_state, void *workspace, size_t workspace_bytes,
                                  void *output, void *stream) {
   return protect([&]() -> evo_status {
-    evo::hip::HyenaWeights w{short_filter, short_len, inner_filter, groups, inner_len,
-                             direct, poles, residues, state_size};
-    const auto s = static_cast<hipStream_t>(stream);
     const bool planar = (static_cast<int>(dtype) & EVO_HIP_PLANAR) != 0;
-    dtype = static_cast<evo_hip_dtype>(static_cast<int>(dtype) & ~EVO_HIP_PLANAR);
+    const bool taps_bf16 = (static_cast<int>(dtype) & EVO_HIP_BF16_TAPS) != 0;
+    evo::hip::HyenaWeights w{short_filter, short_len, inner_filter, groups, inner_len,
+                             direct, poles, residues, state_size, taps_bf16};
+    const auto s = static_cast<hipStream_t>(stream);
+    dtype = static_cast<evo_hip_dtype>(static_cast<int>(dtype) &
+                                       ~(EVO_HIP_PLANAR | EVO_HIP_BF16_TAPS));
     if (dtype == EVO_HIP_F32)
       return publish(evo::hip::hyena_forward<float, float *>(
           kind, static_cast<const float *>(projection), length, width, planar, w, short_history,

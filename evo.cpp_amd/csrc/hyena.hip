@@ -843,6 +843,413 @@ __global__ __launch_bounds__(kFirThreads) void hyena_fir_mfma_kernel(
   }
 }
 
+// ---- Grouped FIR with k <= 128 (HCM) as a row stream on MFMA.
+// A block owns 64 channels (four 16-channel slices, one per wave; each slice
+// lies in one filter group) and a segment of kMsSegment output rows, walked
+// in steps of 32 rows:
+//  1. production (all lanes, two adjacent channels x 4 rows each): short FIR
+//     and gates from the projection rows, u as split BF16 planes into LDS
+//     ([channel][row], so one ds_read_b128 is a B fragment) and x2 into LDS;
+//  2. each wave appends the new 32-row B fragments to a register ring of the
+//     last five steps (the 160-row window that output rows r0..r0+31 read)
+//     and forms Y = T . U on v_mfma_f32_16x16x32_bf16 for both 16-row
+//     halves. The taps are BF16 values (as stored in evo2 artifacts), so the
+//     product is exact in two passes, T U_hi + T U_lo; the Toeplitz A
+//     fragments T_h[q] depend only on the filter group, so each lane builds
+//     its 80 tap values once. Short FIR length 3 (the Evo 2 value);
+//  3. the epilogue y = x2 * (Y + d u) goes through LDS and leaves as whole
+//     rows of 64 channels (non-temporal stores bounded to the segment).
+// A segment after the first starts kMsLead steps (128 rows) early to fill
+// the ring; the first segment fills it from the inner history instead.
+constexpr int kMsStep = 32;
+constexpr int kMsK = 5;             // K steps in the window
+constexpr int kMsChannels = 64;
+constexpr int kMsSegment = 1024;
+constexpr int kMsLead = 4;
+constexpr int kMsUStride = 40;      // BF16 per channel in the u stage (80 B)
+
+template <typename O> struct MsOut;
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+// One 16-byte non-temporal store (global_store_dwordx4 nt).
+__device__ inline void store16_nt(void *dst, const void *lds_src) {
+  __builtin_nontemporal_store(*reinterpret_cast<const u32x4 *>(lds_src),
+                              reinterpret_cast<u32x4 *>(dst));
+}
+// y is staged in LDS as F32 [row][64]; the flush writes whole rows: lane ->
+// row tid / 8, channels (tid % 8) * 8 .. + 7, converting to the output type
+// there; rows at or past `rows` (the segment end) are skipped. `stores` is
+// the number of store instructions a wave issues per flush.
+// (No __builtin_bit_cast of a vector element anywhere in this file: this
+// compiler folds such a cast to element 0.)
+__device__ inline void load8(const float *s, float (&v)[8]) {
+  const f32x4 a = *reinterpret_cast<const f32x4 *>(s);
+  const f32x4 b = *reinterpret_cast<const f32x4 *>(s + 4);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[i] = a[i];
+    v[4 + i] = b[i];
+  }
+}
+__device__ inline void store16_words(void *dst, const uint32_t (&w)[4]) {
+  const u32x4 v = {w[0], w[1], w[2], w[3]};
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(dst));
+}
+template <> struct MsOut<float *> {
+  __device__ static int stores(float *) { return 2; }
+  __device__ static void flush(const float *s, float *out, size_t first, uint32_t rows,
+                               size_t W, size_t c0, uint32_t r0, int tid) {
+    const int row = tid >> 3, part = tid & 7;
+    if (r0 + row >= rows)
+      return;
+    float *dst = out + (first + r0 + row) * W + c0 + part * 8;
+    const float *src = s + row * kMsChannels + part * 8;
+    store16_nt(dst, src);
+    store16_nt(dst + 4, src + 4);
+  }
+};
+template <> struct MsOut<uint16_t *> {
+  __device__ static int stores(uint16_t *) { return 1; }
+  __device__ static void flush(const float *s, uint16_t *out, size_t first, uint32_t rows,
+                               size_t W, size_t c0, uint32_t r0, int tid) {
+    const int row = tid >> 3, part = tid & 7;
+    if (r0 + row >= rows)
+      return;
+    float v[8];
+    load8(s + row * kMsChannels + part * 8, v);
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = pack_bf16(v[2 * i], v[2 * i + 1]);
+    store16_words(out + (first + r0 + row) * W + c0 + part * 8, w);
+  }
+};
+template <> struct MsOut<SplitOut> {
+  __device__ static int stores(const SplitOut &out) { return out.lo != nullptr ? 2 : 1; }
+  __device__ static void flush(const float *s, const SplitOut &out, size_t first,
+                               uint32_t rows, size_t W, size_t c0, uint32_t r0, int tid) {
+    const int row = tid >> 3, part = tid & 7;
+    if (r0 + row >= rows)
+      return;
+    float v[8];
+    load8(s + row * kMsChannels + part * 8, v);
+    uint32_t hi[4], lo[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      hi[i] = pack_bf16(v[2 * i], v[2 * i + 1]);
+      lo[i] = pack_bf16(v[2 * i] - __builtin_bit_cast(float, hi[i] << 16),
+                        v[2 * i + 1] - __builtin_bit_cast(float, hi[i] & 0xffff0000U));
+    }
+    const size_t index = (first + r0 + row) * W + c0 + part * 8;
+    store16_words(out.hi + index, hi);
+    if (out.lo != nullptr)
+      store16_words(out.lo + index, lo);
+  }
+};
+
+template <typename T, typename O>
+__global__ __launch_bounds__(256, 2) void hyena_fir_mfma_stream_kernel(
+    const T *__restrict__ P, const float *__restrict__ short_history,
+    const uint16_t *__restrict__ short_filter, int short_len,
+    const float *__restrict__ inner_history, const float *__restrict__ filter,
+    size_t group_size, int k, int causal, const float *__restrict__ direct,
+    size_t L, size_t W, unsigned channel_blocks, unsigned segments, O out) {
+  constexpr int kWin = 3;          // short FIR length
+  constexpr int kRows = kWin + 3;  // projection rows per production lane
+  // Projection stage of one step: rows R0 - 2 .. R0 + 31 of the block's 64
+  // channels (384 B per row in BF16), copied by DMA kMsStages - 1 steps ahead.
+  constexpr int kStageRows = kMsStep + kWin - 1;
+  constexpr int kRowBytes = kMsChannels * 3 * static_cast<int>(sizeof(T));
+  constexpr int kUnits = kStageRows * kRowBytes / 16;      // 16-byte DMA units
+  constexpr int kUnitsPerRow = kRowBytes / 16;
+  constexpr int kDmaPerStep = (kUnits + 255) / 256;        // per thread
+  constexpr int kDmaMin = kUnits / 256;                    // per wave, at least
+  constexpr int kStages = sizeof(T) == 2 ? 3 : 2;
+  __shared__ __attribute__((aligned(16))) unsigned char p_s[kStages][kStageRows * kRowBytes];
+  __shared__ __attribute__((aligned(16))) uint16_t u_s[2][kMsChannels][kMsUStride];
+  __shared__ __attribute__((aligned(16))) float x2_s[kMsStep][kMsChannels];
+  __shared__ __attribute__((aligned(16))) float y_s[kMsStep][kMsChannels];
+
+  const unsigned total = channel_blocks * segments;
+  const unsigned xcd = blockIdx.x % 8, q8 = total / 8, r8 = total % 8;
+  const unsigned linear = xcd * q8 + min(xcd, r8) + blockIdx.x / 8;
+  const unsigned segment = linear / channel_blocks;
+  const size_t c0 = static_cast<size_t>(linear % channel_blocks) * kMsChannels;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const size_t t0 = static_cast<size_t>(segment) * kMsSegment;
+  const uint32_t seg_rows = static_cast<uint32_t>(min(L - t0, static_cast<size_t>(kMsSegment)));
+  const int lead = t0 == 0 ? 0 : kMsLead;
+  const size_t t_start = t0 - static_cast<size_t>(lead) * kMsStep;  // first produced row
+  const int steps = lead + static_cast<int>((seg_rows + kMsStep - 1) / kMsStep);
+  const size_t cols3 = 3 * W;
+
+  // ---- Production lane: channels cp, cp + 1 and rows 4 * rg .. + 3 of a step.
+  const int pair = tid & 31, rg = tid >> 5;
+  const size_t cp = c0 + 2 * pair;
+  float stap[6][kWin];
+#pragma unroll
+  for (int ch = 0; ch < 2; ++ch) {
+    float t3[3][kWin];
+    load_window_taps(short_filter, short_len, cp + ch, t3);
+#pragma unroll
+    for (int s = 0; s < 3; ++s)
+#pragma unroll
+      for (int i = 0; i < kWin; ++i)
+        stap[3 * ch + s][i] = t3[s][i];
+  }
+  // DMA of step `step` into stage `step % kStages`: rows clamp to [0, L), so
+  // no access leaves the tensor (rows before 0 are replaced from the short
+  // history in production; rows past L only feed outputs that are dropped).
+  // Per-lane unit offsets within a stage (row within the stage, 16-byte
+  // part within the row), fixed for the whole walk.
+  uint32_t unit_row[kDmaPerStep], unit_byte[kDmaPerStep];
+#pragma unroll
+  for (int j = 0; j < kDmaPerStep; ++j) {
+    const int unit = min(j * 256 + tid, kUnits - 1);
+    unit_row[j] = static_cast<uint32_t>(unit / kUnitsPerRow);
+    unit_byte[j] = static_cast<uint32_t>(unit_row[j] * cols3 * sizeof(T) +
+                                         16 * (unit % kUnitsPerRow));
+  }
+  const unsigned char *p_block = reinterpret_cast<const unsigned char *>(P + 3 * c0);
+  auto issue = [&](int step) {
+    const long r_first = static_cast<long>(t_start) + step * kMsStep - (kWin - 1);
+    unsigned char *stage = p_s[step % kStages];
+    const bool inside = r_first >= 0 && r_first + kStageRows <= static_cast<long>(L);
+    const unsigned char *base = p_block + static_cast<size_t>(max(r_first, 0L)) * cols3 * sizeof(T);
+#pragma unroll
+    for (int j = 0; j < kDmaPerStep; ++j) {
+      if (j * 256 + wave * 64 < kUnits && j * 256 + tid < kUnits) {
+        const unsigned char *src;
+        if (inside) {
+          src = base + unit_byte[j];
+        } else {
+          const long row = min(max(r_first + static_cast<long>(unit_row[j]), 0L),
+                               static_cast<long>(L) - 1);
+          src = p_block + static_cast<size_t>(row) * cols3 * sizeof(T) +
+                (unit_byte[j] - unit_row[j] * cols3 * sizeof(T));
+        }
+        dma16(src, stage + 16 * (j * 256 + wave * 64));
+      }
+    }
+  };
+  // Six projection values of row i (0 .. kStageRows-1) of a stage.
+  auto stage_row = [&](int step, int i, PairRow<T> &dst) {
+    const uint32_t *src = reinterpret_cast<const uint32_t *>(
+        p_s[step % kStages] + i * kRowBytes + 2 * pair * 3 * sizeof(T));
+#pragma unroll
+    for (int w = 0; w < PairRow<T>::kWords; ++w)
+      dst.word[w] = src[w];
+  };
+  // Rows before 0 (first segment, first step) come from the short history.
+  auto history_row = [&](long row, PairRow<T> &dst) {
+    const long hrow = static_cast<long>(short_len - 1) + row;
+#pragma unroll
+    for (int i = 0; i < PairRow<T>::kWords; ++i)
+      dst.word[i] = 0;
+    if (short_history != nullptr && hrow >= 0) {
+      float v[6];
+#pragma unroll
+      for (int col = 0; col < 6; ++col)
+        v[col] = short_history[static_cast<size_t>(hrow) * cols3 + 3 * cp + col];
+      if constexpr (sizeof(T) == 2) {
+        // BF16 inputs: the history holds BF16 values.
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+          dst.word[i] = (__builtin_bit_cast(uint32_t, v[2 * i]) >> 16) |
+                        (__builtin_bit_cast(uint32_t, v[2 * i + 1]) & 0xffff0000U);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 6; ++i)
+          dst.word[i] = __builtin_bit_cast(uint32_t, v[i]);
+      }
+    }
+  };
+  for (int step = 0; step < kStages && step < steps; ++step)
+    issue(step);
+
+  // ---- MFMA lane: channel slice `wave`, fragment group g.
+  const int col = lane & 15, g = lane >> 4;
+  const size_t cw = c0 + 16 * wave + col;
+  const float *h = filter + ((c0 + 16 * wave) / group_size) * k;
+  const int stores = MsOut<O>::stores(out);
+  // The taps are BF16 values, so T has no lo plane.
+  u32x4 a[2][kMsK];
+#pragma unroll
+  for (int half = 0; half < 2; ++half)
+#pragma unroll
+    for (int q = 0; q < kMsK; ++q) {
+      uint16_t taps[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int i = 32 * q + 8 * g + e;
+        const int o = i - 16 * half - col - 128 + (k - 1);
+        taps[e] = f32_to_bf16((o >= 0 && o < k) ? h[causal ? k - 1 - o : o] : 0.0F);
+      }
+      a[half][q] = __builtin_bit_cast(u32x4, taps);
+    }
+  float d = direct != nullptr ? direct[cw] : 0.0F;
+  // Keep d in a register: a global load re-issued inside the step loop would
+  // make the wait for it also wait for every DMA in flight.
+  asm volatile("" : "+v"(d));
+  u32x4 ring_hi[kMsK], ring_lo[kMsK];  // BF16 x 8 fragments as raw words
+#pragma unroll
+  for (int q = 0; q < kMsK; ++q) {
+    // Window rows before the first step (only the first segment has them:
+    // u rows -128 .. -1 from the inner history; others start at zero). The
+    // ring shifts once before its first use, so slot q holds rows of step
+    // q - 1 relative to the first window.
+    uint16_t hi[8] = {}, lo[8] = {};
+    if (lead == 0 && inner_history != nullptr && q > 0) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const long row = 32 * q + 8 * g + e - 160;
+        const long hrow = static_cast<long>(k - 1) + row;
+        const float u = hrow >= 0 ? inner_history[static_cast<size_t>(hrow) * W + cw] : 0.0F;
+        hi[e] = f32_to_bf16(u);
+        lo[e] = f32_to_bf16(u - bf16_to_f32(hi[e]));
+      }
+    }
+    ring_hi[q] = __builtin_bit_cast(u32x4, hi);
+    ring_lo[q] = __builtin_bit_cast(u32x4, lo);
+  }
+
+  // Stage 0 complete before the first production (younger: stages 1, 2).
+  if (steps > 2 && kStages == 3)
+    wait_dma<2 * kDmaMin>();
+  else if (steps > 1)
+    wait_dma<kDmaMin>();
+  else
+    wait_dma<0>();
+  __syncthreads();
+
+  for (int step = 0; step < steps; ++step) {
+    // ---- 1. production of rows t_start + 32 step + 4 rg .. + 3 (the stage
+    // of this step is complete: every wave waited for its DMA before the
+    // barrier that ended the previous step, or before the loop).
+    PairRow<T> cur[kRows];
+    const long first_row = static_cast<long>(t_start) + step * kMsStep + 4 * rg - (kWin - 1);
+    if (static_cast<long>(t_start) + step * kMsStep >= kWin - 1) {
+#pragma unroll
+      for (int i = 0; i < kRows; ++i)
+        stage_row(step, 4 * rg + i, cur[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kRows; ++i) {
+        if (first_row + i >= 0)
+          stage_row(step, 4 * rg + i, cur[i]);
+        else
+          history_row(first_row + i, cur[i]);
+      }
+    }
+    uint32_t uh[2][2], ul[2][2];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float fir[6];
+#pragma unroll
+      for (int c6 = 0; c6 < 6; ++c6) {
+        float total = 0.0F;
+#pragma unroll
+        for (int i = 0; i < kWin; ++i)
+          total += cur[j + i].at(c6) * stap[c6][i];
+        fir[c6] = total;
+      }
+#pragma unroll
+      for (int ch = 0; ch < 2; ++ch) {
+        const float u = fir[3 * ch + 1] * fir[3 * ch + 2];
+        const uint32_t hb = f32_to_bf16(u);
+        const uint32_t lb = f32_to_bf16(u - __builtin_bit_cast(float, hb << 16));
+        if ((j & 1) == 0) {
+          uh[ch][j >> 1] = hb;
+          ul[ch][j >> 1] = lb;
+        } else {
+          uh[ch][j >> 1] |= hb << 16;
+          ul[ch][j >> 1] |= lb << 16;
+        }
+      }
+      *reinterpret_cast<float2 *>(&x2_s[4 * rg + j][2 * pair]) = make_float2(fir[0], fir[3]);
+    }
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) {
+      *reinterpret_cast<uint2 *>(&u_s[0][2 * pair + ch][4 * rg]) = make_uint2(uh[ch][0], uh[ch][1]);
+      *reinterpret_cast<uint2 *>(&u_s[1][2 * pair + ch][4 * rg]) = make_uint2(ul[ch][0], ul[ch][1]);
+    }
+    __syncthreads();
+
+    // ---- 2. ring update and products.
+    const int ch = 16 * wave + col;
+#pragma unroll
+    for (int q = 0; q < kMsK - 1; ++q) {
+      ring_hi[q] = ring_hi[q + 1];
+      ring_lo[q] = ring_lo[q + 1];
+    }
+    ring_hi[kMsK - 1] = *reinterpret_cast<const u32x4 *>(&u_s[0][ch][8 * g]);
+    ring_lo[kMsK - 1] = *reinterpret_cast<const u32x4 *>(&u_s[1][ch][8 * g]);
+    const bool emit = step >= lead;
+    if (emit) {
+      // Two independent accumulator chains, interleaved.
+      f32x4 accs[2] = {{0.0F, 0.0F, 0.0F, 0.0F}, {0.0F, 0.0F, 0.0F, 0.0F}};
+#pragma unroll
+      for (int q = 0; q < kMsK; ++q)
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          const bf16x8 t = __builtin_bit_cast(bf16x8, a[half][q]);
+          accs[half] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              t, __builtin_bit_cast(bf16x8, ring_hi[q]), accs[half], 0, 0, 0);
+          accs[half] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              t, __builtin_bit_cast(bf16x8, ring_lo[q]), accs[half], 0, 0, 0);
+        }
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const f32x4 acc = accs[half];
+        const int r = 16 * half + 4 * g;
+        const uint2 uhi = *reinterpret_cast<const uint2 *>(&u_s[0][ch][r]);
+        const uint2 ulo = *reinterpret_cast<const uint2 *>(&u_s[1][ch][r]);
+        const uint32_t hw[4] = {uhi.x << 16, uhi.x & 0xffff0000U, uhi.y << 16, uhi.y & 0xffff0000U};
+        const uint32_t lw[4] = {ulo.x << 16, ulo.x & 0xffff0000U, ulo.y << 16, ulo.y & 0xffff0000U};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float total = acc[e];
+          if (direct != nullptr)
+            total += d * (__builtin_bit_cast(float, hw[e]) + __builtin_bit_cast(float, lw[e]));
+          y_s[r + e][ch] = x2_s[r + e][ch] * total;
+        }
+      }
+    }
+    // The next step's stage must be complete before the barrier. Per wave,
+    // vector-memory operations complete in issue order; younger than the DMA
+    // of step + 1 are the previous step's stores and (three stages) the DMA
+    // of step + 2, so wait until at most those are outstanding (counts per
+    // wave: `stores` per flush, at least kDmaMin per DMA step).
+    if (step + 1 < steps) {
+      const bool stored = step - 1 >= lead;
+      const bool ahead = kStages == 3 && step + 2 < steps;
+      if (!ahead) {
+        if (stored && stores == 2)
+          wait_dma<2>();
+        else if (stored)
+          wait_dma<1>();
+        else
+          wait_dma<0>();
+      } else {
+        if (stored && stores == 2)
+          wait_dma<2 + kDmaMin>();
+        else if (stored)
+          wait_dma<1 + kDmaMin>();
+        else
+          wait_dma<kDmaMin>();
+      }
+    }
+    __syncthreads();
+
+    // ---- 3. whole-row stores of the step's outputs, then the DMA of the
+    // step kStages ahead into the stage this step used.
+    if (emit)
+      MsOut<O>::flush(&y_s[0][0], out, t0, seg_rows, W, c0,
+                      static_cast<uint32_t>((step - lead) * kMsStep), tid);
+    if (step + kStages < steps)
+      issue(step + kStages);
+  }
+}
+
 // Rewrites the inner (u) history with the last k-1 rows of [history ; u].
 // Runs after the main kernel and before the short history moves on.
 template <typename T>
@@ -1079,6 +1486,15 @@ Status hyena_forward(int kind, const T *projection, size_t length,
       EVO_TRY((launch_fir_stream<T, O>(projection, short_history, wt, short_len, inner_history,
                                        group_size, k, causal, direct, length, width, out,
                                        stream)));
+    } else if (wt.taps_bf16 && short_len == 3 && planar == 0 && width % kMsChannels == 0 &&
+               group_size % 16 == 0) {
+      const unsigned cblocks = static_cast<unsigned>(width / kMsChannels);
+      const unsigned segments = ceil_div(length, kMsSegment);
+      hipLaunchKernelGGL((hyena_fir_mfma_stream_kernel<T, O>), dim3(cblocks * segments),
+                         dim3(256), 0, stream, projection, short_history, wt.short_filter,
+                         short_len, inner_history, wt.inner_filter, group_size, k, causal, direct,
+                         length, width, cblocks, segments, out);
+      EVO_TRY(launch_status("hyena_fir_mfma_stream_kernel"));
     } else if (width % kChannels == 0 && group_size % 16 == 0) {
       const size_t steps = k <= 8 ? FirMfmaShape<8>::kSteps : FirMfmaShape<128>::kSteps;
       if (workspace == nullptr || workspace_bytes < wt.groups * steps * 2 * 64 * 16)

@@ -465,6 +465,7 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
       hw.poles = L.poles.as<float>();
       hw.residues = L.residues.as<float>();
       hw.state = c.state;
+      hw.taps_bf16 = true;  // `.filter.h` is BF16 in the artifact
       const int kind = L.type == Mixer::kHcs ? kHyenaHcs
                        : L.type == Mixer::kHcm ? kHyenaHcm : kHyenaHcl;
       if (L.fp8)

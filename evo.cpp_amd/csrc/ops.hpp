@@ -105,6 +105,7 @@ struct HyenaWeights {
   const float *poles;            // F32 [W, S] = exp(log_poles) (HCL)
   const float *residues;         // F32 [W, S] (HCL)
   size_t state;
+  bool taps_bf16;                // every inner tap is a BF16 value (artifact filters)
 };
 size_t hyena_workspace_bytes(int kind, size_t length, size_t width,
                              size_t state);

@@ -52,7 +52,12 @@ typedef enum evo_hip_dtype {
   /* OR-ed into the Hyena operator's dtype: the projection holds stream s
    * (x2, x1, v) of channel c at column s*W + c instead of the reference's
    * 3c + s (the library permutes its projection weights this way). */
-  EVO_HIP_PLANAR = 0x100
+  EVO_HIP_PLANAR = 0x100,
+  /* OR-ed into the Hyena operator's dtype: every inner_filter tap is a BF16
+   * value (evo2 artifacts store `filter.h` as BF16), which lets the HCM
+   * operator form its Toeplitz product in two MFMA passes instead of three
+   * (same result). */
+  EVO_HIP_BF16_TAPS = 0x200
 } evo_hip_dtype;
 typedef enum evo_hip_hyena_kind {
   EVO_HIP_HYENA_HCS = 0,

@@ -292,7 +292,7 @@ def planar(proj):
 
 
 def hyena_gpu(kind, case, dtype=N.DTYPE_F32, rows=None, caches=None, projection=None,
-              planar_layout=False):
+              planar_layout=False, bf16_taps=False):
     proj = case["projection"] if projection is None else projection
     if planar_layout:
         proj = planar(proj)
@@ -315,7 +315,8 @@ def hyena_gpu(kind, case, dtype=N.DTYPE_F32, rows=None, caches=None, projection=
         proj_d = dev(proj)
         out = empty((length, width))
     caches = caches or {}
-    N.call("evo_hip_hyena_forward", kind, dtype | (N.DTYPE_PLANAR if planar_layout else 0),
+    flags = (N.DTYPE_PLANAR if planar_layout else 0) | (N.DTYPE_BF16_TAPS if bf16_taps else 0)
+    N.call("evo_hip_hyena_forward", kind, dtype | flags,
            p(proj_d), length, width,
            p(dev(case["short"])), 3, p(dev(case["inner"]) if "inner" in case else None),
            case.get("groups", 1), case.get("inner_len", 0),
@@ -417,6 +418,41 @@ def test_hyena_continuation_equals_one_pass(kind, inner_len, split, groups, layo
                        planar_layout=layout)
     joined = np.concatenate([first, second])
     assert rel_err(joined, whole) < 1e-5
+
+
+@pytest.mark.parametrize("inner_len", [128, 33, 2])
+@pytest.mark.parametrize("length,width,groups", [(1, 64, 4), (31, 128, 8), (1025, 64, 4),
+                                                 (2100, 128, 8), (3000, 256, 16)])
+@pytest.mark.parametrize("dtype", [N.DTYPE_F32, N.DTYPE_SPLIT, N.DTYPE_BF16_SPLIT])
+def test_hcm_stream_mfma_matches_oracle(inner_len, length, width, groups, dtype):
+    """BF16 taps (the artifact case) run the row-streaming MFMA FIR: segments
+    of 1024 rows with a 128-row lead, 32-row steps, a register ring of the
+    160-row window; lengths cross segment and step boundaries."""
+    case = hyena_case(length + width + inner_len, N.HYENA_HCM, length, width, groups=groups,
+                      inner_len=inner_len)
+    proj = case["projection"]
+    if dtype == N.DTYPE_BF16_SPLIT:
+        proj = bf16_to_f32(bf16_bits(proj))
+    expected = hyena_oracle(N.HYENA_HCM, case, projection=proj)
+    actual = hyena_gpu(N.HYENA_HCM, case, dtype=dtype, projection=proj, bf16_taps=True)
+    assert rel_err(actual, expected) < 2e-5
+
+
+@pytest.mark.parametrize("split", [1, 31, 32, 300, 1024, 1500])
+def test_hcm_stream_continuation(split):
+    """Continuation through the caches with the streaming kernel: the first
+    segment of each call fills its window from the inner and short histories."""
+    width, length = 128, 2100
+    case = hyena_case(split, N.HYENA_HCM, length, width, groups=8, inner_len=128)
+    whole = hyena_gpu(N.HYENA_HCM, case, bf16_taps=True)
+    caches = {"short": zeros((2, 3 * width)), "inner": zeros((127, width)), "modal": None}
+    first = hyena_gpu(N.HYENA_HCM, case, projection=case["projection"][:split], caches=caches,
+                      bf16_taps=True)
+    second = hyena_gpu(N.HYENA_HCM, case, projection=case["projection"][split:],
+                       caches=caches, bf16_taps=True)
+    assert rel_err(np.concatenate([first, second]), whole) < 1e-5
+    reference = hyena_gpu(N.HYENA_HCM, case)  # three-pass MFMA kernel
+    assert rel_err(whole, reference) < 1e-6
 
 
 # ----------------------------------------------------------- attention
