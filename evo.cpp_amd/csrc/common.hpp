@@ -53,6 +53,15 @@ __device__ inline void dma16(const void *global, const void *lds) {
                :: "v"(global), "s"(address) : "memory");
 }
 
+// The same DMA with a wave-uniform base address (SGPR pair) and a 32-bit
+// per-lane byte offset: no per-lane 64-bit address arithmetic.
+__device__ inline void dma16(const void *base, uint32_t offset, const void *lds) {
+  const unsigned address = __builtin_amdgcn_readfirstlane(
+      static_cast<unsigned>(reinterpret_cast<size_t>((const lds_void *)(lds))));
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(offset), "s"(base), "s"(address) : "memory");
+}
+
 template <int kPending>
 __device__ inline void wait_dma() {
   asm volatile("s_waitcnt vmcnt(%0)" :: "n"(kPending) : "memory");

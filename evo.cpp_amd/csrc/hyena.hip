@@ -395,8 +395,12 @@ template <typename T> struct PairRow {
   }
 };
 
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+// {bf16(a), bf16(b)} in one v_cvt_pk_bf16_f32 (round to nearest even).
 __device__ inline uint32_t pack_bf16(float a, float b) {
-  return static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
+  const f32x2 v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
 // Output of a channel pair through segment-bounded buffer resources:
@@ -963,11 +967,13 @@ __global__ __launch_bounds__(256, 2) void hyena_fir_mfma_stream_kernel(
   constexpr int kUnitsPerRow = kRowBytes / 16;
   constexpr int kDmaPerStep = (kUnits + 255) / 256;        // per thread
   constexpr int kDmaMin = kUnits / 256;                    // per wave, at least
-  constexpr int kStages = sizeof(T) == 2 ? 3 : 2;
+  constexpr int kStages = 2;
+  // Software pipeline: in phase s the block flushes step s-1, produces step
+  // s+1 and multiplies step s, so u is double buffered and x2 (overwritten in
+  // place by y) triple buffered.
   __shared__ __attribute__((aligned(16))) unsigned char p_s[kStages][kStageRows * kRowBytes];
-  __shared__ __attribute__((aligned(16))) uint16_t u_s[2][kMsChannels][kMsUStride];
-  __shared__ __attribute__((aligned(16))) float x2_s[kMsStep][kMsChannels];
-  __shared__ __attribute__((aligned(16))) float y_s[kMsStep][kMsChannels];
+  __shared__ __attribute__((aligned(16))) uint16_t u_s[2][2][kMsChannels][kMsUStride];
+  __shared__ __attribute__((aligned(16))) float xy_s[3][kMsStep][kMsChannels];
 
   const unsigned total = channel_blocks * segments;
   const unsigned xcd = blockIdx.x % 8, q8 = total / 8, r8 = total % 8;
@@ -1020,14 +1026,14 @@ __global__ __launch_bounds__(256, 2) void hyena_fir_mfma_stream_kernel(
       if (j * 256 + wave * 64 < kUnits && j * 256 + tid < kUnits) {
         const unsigned char *src;
         if (inside) {
-          src = base + unit_byte[j];
+          dma16(base, unit_byte[j], stage + 16 * (j * 256 + wave * 64));
         } else {
           const long row = min(max(r_first + static_cast<long>(unit_row[j]), 0L),
                                static_cast<long>(L) - 1);
           src = p_block + static_cast<size_t>(row) * cols3 * sizeof(T) +
                 (unit_byte[j] - unit_row[j] * cols3 * sizeof(T));
+          dma16(src, stage + 16 * (j * 256 + wave * 64));
         }
-        dma16(src, stage + 16 * (j * 256 + wave * 64));
       }
     }
   };
@@ -1112,19 +1118,10 @@ __global__ __launch_bounds__(256, 2) void hyena_fir_mfma_stream_kernel(
     ring_lo[q] = __builtin_bit_cast(u32x4, lo);
   }
 
-  // Stage 0 complete before the first production (younger: stages 1, 2).
-  if (steps > 2 && kStages == 3)
-    wait_dma<2 * kDmaMin>();
-  else if (steps > 1)
-    wait_dma<kDmaMin>();
-  else
-    wait_dma<0>();
-  __syncthreads();
-
-  for (int step = 0; step < steps; ++step) {
-    // ---- 1. production of rows t_start + 32 step + 4 rg .. + 3 (the stage
-    // of this step is complete: every wave waited for its DMA before the
-    // barrier that ended the previous step, or before the loop).
+  // ---- Production of step `step`: rows t_start + 32 step + 4 rg .. + 3
+  // from its stage (complete: waited for before the last barrier), u into
+  // u_s[step % 2] and x2 into xy_s[step % 3].
+  auto produce = [&](int step) {
     PairRow<T> cur[kRows];
     const long first_row = static_cast<long>(t_start) + step * kMsStep + 4 * rg - (kWin - 1);
     if (static_cast<long>(t_start) + step * kMsStep >= kWin - 1) {
@@ -1140,7 +1137,9 @@ __global__ __launch_bounds__(256, 2) void hyena_fir_mfma_stream_kernel(
           history_row(first_row + i, cur[i]);
       }
     }
-    uint32_t uh[2][2], ul[2][2];
+    float(*x2)[kMsChannels] = xy_s[step % 3];
+    uint16_t(*uplanes)[kMsChannels][kMsUStride] = u_s[step & 1];
+    float u[2][4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       float fir[6];
@@ -1152,102 +1151,112 @@ __global__ __launch_bounds__(256, 2) void hyena_fir_mfma_stream_kernel(
           total += cur[j + i].at(c6) * stap[c6][i];
         fir[c6] = total;
       }
-#pragma unroll
-      for (int ch = 0; ch < 2; ++ch) {
-        const float u = fir[3 * ch + 1] * fir[3 * ch + 2];
-        const uint32_t hb = f32_to_bf16(u);
-        const uint32_t lb = f32_to_bf16(u - __builtin_bit_cast(float, hb << 16));
-        if ((j & 1) == 0) {
-          uh[ch][j >> 1] = hb;
-          ul[ch][j >> 1] = lb;
-        } else {
-          uh[ch][j >> 1] |= hb << 16;
-          ul[ch][j >> 1] |= lb << 16;
-        }
-      }
-      *reinterpret_cast<float2 *>(&x2_s[4 * rg + j][2 * pair]) = make_float2(fir[0], fir[3]);
+      u[0][j] = fir[1] * fir[2];
+      u[1][j] = fir[4] * fir[5];
+      *reinterpret_cast<float2 *>(&x2[4 * rg + j][2 * pair]) = make_float2(fir[0], fir[3]);
     }
+    // Rows (0, 1) and (2, 3) of a channel pack into one word per plane.
+    uint32_t uh[2][2], ul[2][2];
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+      for (int w = 0; w < 2; ++w) {
+        uh[ch][w] = pack_bf16(u[ch][2 * w], u[ch][2 * w + 1]);
+        ul[ch][w] = pack_bf16(u[ch][2 * w] - __builtin_bit_cast(float, uh[ch][w] << 16),
+                              u[ch][2 * w + 1] - __builtin_bit_cast(float, uh[ch][w] & 0xffff0000U));
+      }
 #pragma unroll
     for (int ch = 0; ch < 2; ++ch) {
-      *reinterpret_cast<uint2 *>(&u_s[0][2 * pair + ch][4 * rg]) = make_uint2(uh[ch][0], uh[ch][1]);
-      *reinterpret_cast<uint2 *>(&u_s[1][2 * pair + ch][4 * rg]) = make_uint2(ul[ch][0], ul[ch][1]);
+      *reinterpret_cast<uint2 *>(&uplanes[0][2 * pair + ch][4 * rg]) =
+          make_uint2(uh[ch][0], uh[ch][1]);
+      *reinterpret_cast<uint2 *>(&uplanes[1][2 * pair + ch][4 * rg]) =
+          make_uint2(ul[ch][0], ul[ch][1]);
     }
-    __syncthreads();
+  };
 
-    // ---- 2. ring update and products.
-    const int ch = 16 * wave + col;
+  // ---- Products of step `step`: ring update from u_s[step % 2]; when the
+  // step emits, Y = T . U and y = x2 * (Y + d u) in place of x2.
+  const int ch = 16 * wave + col;
+  auto multiply = [&](int step) {
+    const uint16_t(*uplanes)[kMsChannels][kMsUStride] = u_s[step & 1];
 #pragma unroll
     for (int q = 0; q < kMsK - 1; ++q) {
       ring_hi[q] = ring_hi[q + 1];
       ring_lo[q] = ring_lo[q + 1];
     }
-    ring_hi[kMsK - 1] = *reinterpret_cast<const u32x4 *>(&u_s[0][ch][8 * g]);
-    ring_lo[kMsK - 1] = *reinterpret_cast<const u32x4 *>(&u_s[1][ch][8 * g]);
-    const bool emit = step >= lead;
-    if (emit) {
-      // Two independent accumulator chains, interleaved.
-      f32x4 accs[2] = {{0.0F, 0.0F, 0.0F, 0.0F}, {0.0F, 0.0F, 0.0F, 0.0F}};
+    ring_hi[kMsK - 1] = *reinterpret_cast<const u32x4 *>(&uplanes[0][ch][8 * g]);
+    ring_lo[kMsK - 1] = *reinterpret_cast<const u32x4 *>(&uplanes[1][ch][8 * g]);
+    if (step < lead)
+      return;
+    // Two independent accumulator chains, interleaved.
+    f32x4 accs[2] = {{0.0F, 0.0F, 0.0F, 0.0F}, {0.0F, 0.0F, 0.0F, 0.0F}};
 #pragma unroll
-      for (int q = 0; q < kMsK; ++q)
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          const bf16x8 t = __builtin_bit_cast(bf16x8, a[half][q]);
-          accs[half] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              t, __builtin_bit_cast(bf16x8, ring_hi[q]), accs[half], 0, 0, 0);
-          accs[half] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              t, __builtin_bit_cast(bf16x8, ring_lo[q]), accs[half], 0, 0, 0);
-        }
+    for (int q = 0; q < kMsK; ++q)
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
-        const f32x4 acc = accs[half];
-        const int r = 16 * half + 4 * g;
-        const uint2 uhi = *reinterpret_cast<const uint2 *>(&u_s[0][ch][r]);
-        const uint2 ulo = *reinterpret_cast<const uint2 *>(&u_s[1][ch][r]);
-        const uint32_t hw[4] = {uhi.x << 16, uhi.x & 0xffff0000U, uhi.y << 16, uhi.y & 0xffff0000U};
-        const uint32_t lw[4] = {ulo.x << 16, ulo.x & 0xffff0000U, ulo.y << 16, ulo.y & 0xffff0000U};
+        const bf16x8 t = __builtin_bit_cast(bf16x8, a[half][q]);
+        accs[half] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            t, __builtin_bit_cast(bf16x8, ring_hi[q]), accs[half], 0, 0, 0);
+        accs[half] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            t, __builtin_bit_cast(bf16x8, ring_lo[q]), accs[half], 0, 0, 0);
+      }
+    float(*xy)[kMsChannels] = xy_s[step % 3];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float total = acc[e];
-          if (direct != nullptr)
-            total += d * (__builtin_bit_cast(float, hw[e]) + __builtin_bit_cast(float, lw[e]));
-          y_s[r + e][ch] = x2_s[r + e][ch] * total;
-        }
+    for (int half = 0; half < 2; ++half) {
+      const f32x4 acc = accs[half];
+      const int r = 16 * half + 4 * g;
+      const uint2 uhi = *reinterpret_cast<const uint2 *>(&uplanes[0][ch][r]);
+      const uint2 ulo = *reinterpret_cast<const uint2 *>(&uplanes[1][ch][r]);
+      const uint32_t hw[4] = {uhi.x << 16, uhi.x & 0xffff0000U, uhi.y << 16, uhi.y & 0xffff0000U};
+      const uint32_t lw[4] = {ulo.x << 16, ulo.x & 0xffff0000U, ulo.y << 16, ulo.y & 0xffff0000U};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float total = acc[e];
+        if (direct != nullptr)
+          total += d * (__builtin_bit_cast(float, hw[e]) + __builtin_bit_cast(float, lw[e]));
+        xy[r + e][ch] *= total;
       }
     }
-    // The next step's stage must be complete before the barrier. Per wave,
-    // vector-memory operations complete in issue order; younger than the DMA
-    // of step + 1 are the previous step's stores and (three stages) the DMA
-    // of step + 2, so wait until at most those are outstanding (counts per
-    // wave: `stores` per flush, at least kDmaMin per DMA step).
-    if (step + 1 < steps) {
-      const bool stored = step - 1 >= lead;
-      const bool ahead = kStages == 3 && step + 2 < steps;
-      if (!ahead) {
-        if (stored && stores == 2)
-          wait_dma<2>();
-        else if (stored)
-          wait_dma<1>();
-        else
-          wait_dma<0>();
-      } else {
-        if (stored && stores == 2)
-          wait_dma<2 + kDmaMin>();
-        else if (stored)
-          wait_dma<1 + kDmaMin>();
-        else
-          wait_dma<kDmaMin>();
-      }
+  };
+  auto flush = [&](int step) {
+    if (step >= lead)
+      MsOut<O>::flush(&xy_s[step % 3][0][0], out, t0, seg_rows, W, c0,
+                      static_cast<uint32_t>((step - lead) * kMsStep), tid);
+  };
+
+  // Prologue: stage 0 (younger: the DMA of stage 1), production of step 0,
+  // then stage 1 complete.
+  if (steps > 1)
+    wait_dma<kDmaMin>();
+  else
+    wait_dma<0>();
+  __syncthreads();
+  produce(0);
+  wait_dma<0>();
+  __syncthreads();
+
+  // Phase s: DMA of step s + 2 into the stage step s used; flush s - 1;
+  // produce s + 1; multiply s. Before the barrier, the DMA of step s + 2 must
+  // be complete (younger: only the flush stores of step s - 1).
+  for (int step = 0; step < steps; ++step) {
+    if (step + 2 < steps)
+      issue(step + 2);
+    if (step >= 1)
+      flush(step - 1);
+    if (step + 1 < steps)
+      produce(step + 1);
+    multiply(step);
+    if (step + 2 < steps) {
+      if (step - 1 >= lead && stores == 2)
+        wait_dma<2>();
+      else if (step - 1 >= lead)
+        wait_dma<1>();
+      else
+        wait_dma<0>();
     }
     __syncthreads();
-
-    // ---- 3. whole-row stores of the step's outputs, then the DMA of the
-    // step kStages ahead into the stage this step used.
-    if (emit)
-      MsOut<O>::flush(&y_s[0][0], out, t0, seg_rows, W, c0,
-                      static_cast<uint32_t>((step - lead) * kMsStep), tid);
-    if (step + kStages < steps)
-      issue(step + kStages);
   }
+  flush(steps - 1);
 }
 
 // Rewrites the inner (u) history with the last k-1 rows of [history ; u].
