@@ -847,6 +847,247 @@ __global__ __launch_bounds__(kFirThreads) void hyena_fir_mfma_kernel(
   }
 }
 
+// ---- HCL on channel pairs (interleaved projection, short FIR of 3): the
+// chunked scan of the modal recurrence with the row stream of the HCS kernel
+// (12/24-byte loads of two channels per lane, packed non-temporal stores).
+// A wave covers 128 channels of one kChunk-row chunk.
+template <typename T>
+struct PairShort {
+  float stap[6][3], swin[6][3];  // slot 2 is the newest row
+  __device__ void taps(const uint16_t *short_filter, size_t c) {
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) {
+      float t3[3][3];
+      load_window_taps(short_filter, 3, c + ch, t3);
+#pragma unroll
+      for (int s = 0; s < 3; ++s)
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+          stap[3 * ch + s][i] = t3[s][i];
+    }
+  }
+  // Window before row t0: rows t0-2, t0-1 from P, or from the short history
+  // (F32 [2][3W]) when they precede row 0.
+  __device__ void prime(const T *P, const float *short_history, size_t t0, size_t W, size_t c) {
+    const size_t cols3 = 3 * W;
+#pragma unroll
+    for (int i = 1; i < 3; ++i) {
+      const long row = static_cast<long>(t0) - 3 + i;
+#pragma unroll
+      for (int col = 0; col < 6; ++col) {
+        float v = 0.0F;
+        if (row >= 0)
+          v = load_act(P, static_cast<size_t>(row) * cols3 + 3 * c + col);
+        else if (short_history != nullptr && row + 2 >= 0)
+          v = short_history[static_cast<size_t>(row + 2) * cols3 + 3 * c + col];
+        swin[col][i] = v;
+      }
+    }
+  }
+  // Shifts in one row; x2 and u of both channels.
+  __device__ void step(const PairRow<T> &row, float (&x2)[2], float (&u)[2]) {
+    float fir[6];
+#pragma unroll
+    for (int col = 0; col < 6; ++col) {
+      swin[col][0] = swin[col][1];
+      swin[col][1] = swin[col][2];
+      swin[col][2] = row.at(col);
+      float total = 0.0F;
+#pragma unroll
+      for (int i = 0; i < 3; ++i)
+        total += swin[col][i] * stap[col][i];
+      fir[col] = total;
+    }
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) {
+      x2[ch] = fir[3 * ch];
+      u[ch] = fir[3 * ch + 1] * fir[3 * ch + 2];
+    }
+  }
+};
+
+constexpr int kHclBatch = 4;
+
+// Phase 1: final local state of every chunk from a zero start.
+template <typename T>
+__global__ __launch_bounds__(256) void hcl_state_pair_kernel(
+    const T *__restrict__ P, const float *__restrict__ short_history,
+    const uint16_t *__restrict__ short_filter, size_t L, size_t W,
+    const float *__restrict__ poles, int S, float *__restrict__ chunk_state) {
+  const size_t c = blockIdx.x * 512ULL + (threadIdx.x >> 6) * 128 + 2 * (threadIdx.x & 63);
+  if (c >= W)
+    return;
+  const size_t g = blockIdx.y;
+  const size_t t0 = g * kChunk;
+  const uint32_t rows = static_cast<uint32_t>(min(L - t0, static_cast<size_t>(kChunk)));
+  PairShort<T> sh;
+  sh.taps(short_filter, c);
+  sh.prime(P, short_history, t0, W, c);
+  float p[2][kMaxState], st[2][kMaxState];
+#pragma unroll
+  for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+    for (int m = 0; m < kMaxState; ++m) {
+      p[ch][m] = m < S ? poles[(c + ch) * S + m] : 0.0F;
+      st[ch][m] = 0.0F;
+    }
+  const uint32_t row_bytes = static_cast<uint32_t>(3 * W * sizeof(T));
+  const auto in = buffer_resource(P + t0 * 3 * W, rows * row_bytes);
+  const uint32_t lane_bytes = static_cast<uint32_t>(3 * c * sizeof(T));
+  PairRow<T> next[kHclBatch];
+#pragma unroll
+  for (int b = 0; b < kHclBatch; ++b)
+    next[b].load(in, lane_bytes, b * row_bytes);
+  for (uint32_t base = 0; base < rows; base += kHclBatch) {
+    PairRow<T> cur[kHclBatch];
+#pragma unroll
+    for (int b = 0; b < kHclBatch; ++b)
+      cur[b] = next[b];
+    if (base + kHclBatch < rows) {
+#pragma unroll
+      for (int b = 0; b < kHclBatch; ++b)
+        next[b].load(in, lane_bytes, (base + kHclBatch + b) * row_bytes);
+    }
+#pragma unroll
+    for (int b = 0; b < kHclBatch; ++b) {
+      if (base + b >= rows)
+        break;
+      float x2[2], u[2];
+      sh.step(cur[b], x2, u);
+#pragma unroll
+      for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+        for (int m = 0; m < kMaxState; ++m)
+          st[ch][m] = p[ch][m] * st[ch][m] + u[ch];
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < kMaxState; ++m)
+    if (m < S)
+      *reinterpret_cast<float2 *>(&chunk_state[(g * S + m) * W + c]) =
+          make_float2(st[0][m], st[1][m]);
+}
+
+// Phase 2: chunk-start states in place (and the final state), four segments
+// of chunks per (state, channel) in one block: each segment folds its chunks,
+// the segments combine through LDS, each segment rescans its chunks.
+__global__ __launch_bounds__(256) void hcl_carry_seg_kernel(
+    float *__restrict__ chunk_state, size_t G, size_t L, size_t W, int S,
+    const float *__restrict__ poles, float *__restrict__ modal_state) {
+  __shared__ float fold[4][64], power_s[4][64];
+  const int lane = threadIdx.x & 63, seg = threadIdx.x >> 6;
+  const size_t c = blockIdx.x * 64ULL + lane;
+  const int m = static_cast<int>(blockIdx.y);
+  const bool valid = c < W;
+  const float p = valid ? poles[c * S + m] : 0.0F;
+  float full = p;  // p^kChunk by repeated squaring (kChunk is a power of two)
+  for (int e = 1; e < kChunk; e <<= 1)
+    full *= full;
+  const size_t per = (G + 3) / 4;
+  const size_t g0 = min(G, seg * per), g1 = min(G, g0 + per);
+  auto chunk_power = [&](size_t g) {
+    const size_t len = min(L - g * kChunk, static_cast<size_t>(kChunk));
+    if (len == static_cast<size_t>(kChunk))
+      return full;
+    float power = 1.0F;
+    for (size_t e = 0; e < len; ++e)
+      power *= p;
+    return power;
+  };
+  // Fold: the segment's state from a zero start and its total power.
+  float state = 0.0F, power = 1.0F;
+  if (valid)
+    for (size_t g = g0; g < g1; ++g) {
+      const float pw = chunk_power(g);
+      state = pw * state + chunk_state[(g * S + m) * W + c];
+      power *= pw;
+    }
+  fold[seg][lane] = state;
+  power_s[seg][lane] = power;
+  __syncthreads();
+  float in = (valid && modal_state != nullptr) ? modal_state[c * S + m] : 0.0F;
+  for (int q = 0; q < seg; ++q)
+    in = power_s[q][lane] * in + fold[q][lane];
+  if (!valid)
+    return;
+  // Rescan: chunk g's start state, written in place of its local state.
+  state = in;
+  for (size_t g = g0; g < g1; ++g) {
+    const float local = chunk_state[(g * S + m) * W + c];
+    chunk_state[(g * S + m) * W + c] = state;
+    state = chunk_power(g) * state + local;
+  }
+  if (seg == 3 && modal_state != nullptr)
+    modal_state[c * S + m] = state;
+}
+
+// Phase 3: rescan every chunk from its true start state and write y.
+template <typename T, typename O>
+__global__ __launch_bounds__(256) void hcl_output_pair_kernel(
+    const T *__restrict__ P, const float *__restrict__ short_history,
+    const uint16_t *__restrict__ short_filter, size_t L, size_t W,
+    const float *__restrict__ poles, const float *__restrict__ residues,
+    const float *__restrict__ direct, int S, const float *__restrict__ chunk_state, O out) {
+  const size_t c = blockIdx.x * 512ULL + (threadIdx.x >> 6) * 128 + 2 * (threadIdx.x & 63);
+  if (c >= W)
+    return;
+  const size_t g = blockIdx.y;
+  const size_t t0 = g * kChunk;
+  const uint32_t rows = static_cast<uint32_t>(min(L - t0, static_cast<size_t>(kChunk)));
+  PairShort<T> sh;
+  sh.taps(short_filter, c);
+  sh.prime(P, short_history, t0, W, c);
+  float p[2][kMaxState], r[2][kMaxState], st[2][kMaxState], d[2];
+#pragma unroll
+  for (int ch = 0; ch < 2; ++ch) {
+#pragma unroll
+    for (int m = 0; m < kMaxState; ++m) {
+      p[ch][m] = m < S ? poles[(c + ch) * S + m] : 0.0F;
+      r[ch][m] = m < S ? residues[(c + ch) * S + m] : 0.0F;
+      st[ch][m] = m < S ? chunk_state[(g * S + m) * W + c + ch] : 0.0F;
+    }
+    d[ch] = direct[c + ch];
+  }
+  const uint32_t row_bytes = static_cast<uint32_t>(3 * W * sizeof(T));
+  const auto in = buffer_resource(P + t0 * 3 * W, rows * row_bytes);
+  const uint32_t lane_bytes = static_cast<uint32_t>(3 * c * sizeof(T));
+  const PairOut<O> sink(out, t0, rows, W);
+  const uint32_t out_lane = static_cast<uint32_t>(c * 2);
+  const uint32_t out_row = static_cast<uint32_t>(W * 2);
+  PairRow<T> next[kHclBatch];
+#pragma unroll
+  for (int b = 0; b < kHclBatch; ++b)
+    next[b].load(in, lane_bytes, b * row_bytes);
+  for (uint32_t base = 0; base < rows; base += kHclBatch) {
+    PairRow<T> cur[kHclBatch];
+#pragma unroll
+    for (int b = 0; b < kHclBatch; ++b)
+      cur[b] = next[b];
+    if (base + kHclBatch < rows) {
+#pragma unroll
+      for (int b = 0; b < kHclBatch; ++b)
+        next[b].load(in, lane_bytes, (base + kHclBatch + b) * row_bytes);
+    }
+#pragma unroll
+    for (int b = 0; b < kHclBatch; ++b) {
+      float x2[2], u[2], y[2];
+      sh.step(cur[b], x2, u);
+#pragma unroll
+      for (int ch = 0; ch < 2; ++ch) {
+        float modal = 0.0F;
+#pragma unroll
+        for (int m = 0; m < kMaxState; ++m) {
+          st[ch][m] = p[ch][m] * st[ch][m] + u[ch];
+          modal += r[ch][m] * st[ch][m];
+        }
+        y[ch] = x2[ch] * (modal + d[ch] * u[ch]);
+      }
+      // Rows past the chunk end are dropped by the store bound.
+      sink.put(out_lane, (base + b) * out_row, y[0], y[1]);
+    }
+  }
+}
+
 // ---- Grouped FIR with k <= 128 (HCM) as a row stream on MFMA.
 // A block owns 64 channels (four 16-channel slices, one per wave; each slice
 // lies in one filter group) and a segment of kMsSegment output rows, walked
@@ -1475,7 +1716,20 @@ Status hyena_forward(int kind, const T *projection, size_t length,
       return {ErrorCode::kInvalidArgument, "hyena_forward: sequence too long for one call"};
     float *chunk_state = static_cast<float *>(workspace);
     const int S = static_cast<int>(wt.state);
-    if (short_len <= 4) {
+    if (short_len == 3 && planar == 0 && width % 2 == 0) {
+      const dim3 grid(ceil_div(width, 512), static_cast<unsigned>(G));
+      hipLaunchKernelGGL(hcl_state_pair_kernel<T>, grid, dim3(256), 0, stream, projection,
+                         short_history, wt.short_filter, length, width, wt.poles, S,
+                         chunk_state);
+      EVO_TRY(launch_status("hcl_state_pair_kernel"));
+      hipLaunchKernelGGL(hcl_carry_seg_kernel, dim3(ceil_div(width, 64), S), dim3(256), 0,
+                         stream, chunk_state, G, length, width, S, wt.poles, modal_state);
+      EVO_TRY(launch_status("hcl_carry_seg_kernel"));
+      hipLaunchKernelGGL((hcl_output_pair_kernel<T, O>), grid, dim3(256), 0, stream,
+                         projection, short_history, wt.short_filter, length, width, wt.poles,
+                         wt.residues, wt.direct, S, chunk_state, out);
+      EVO_TRY(launch_status("hcl_output_pair_kernel"));
+    } else if (short_len <= 4) {
       EVO_TRY((launch_hcl<T, O, 4>(projection, short_history, wt, short_len, length, width,
                                    planar, S, G, chunk_state, modal_state, out, stream)));
     } else {
