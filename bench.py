@@ -129,15 +129,18 @@ def kernel_rooflines(split):
     planes_out = torch.empty(2, length, width, dtype=torch.int16, device="cuda")
     hbm_bytes = length * 3 * width * 2 + length * width * 4
     out["hyena"] = []
-    for kind, name, taps in ((1, "HCM FIR (128 taps)", 128), (0, "HCS FIR (7 taps)", 7),
-                             (2, "HCL (16 modal states)", 0)):
+    for kind, name, taps in ((1, "HCM FIR, 128 taps (hyena_fir_mfma_stream_kernel)", 128),
+                             (0, "HCS FIR, 7 taps (hyena_fir_stream_kernel)", 7),
+                             (2, "HCL, 16 modal states (hcl_state_pair + hcl_carry_seg + "
+                                 "hcl_output_pair)", 0)):
         filt = (torch.randn(groups, max(taps, 1), device="cuda", generator=g)
                 / max(taps, 1) ** 0.5).to(torch.bfloat16).float()
         st = state if kind == 2 else 0
         ws_bytes = native.call("evo_hip_hyena_workspace_bytes", kind, length, width, st)
         ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device="cuda")
         ms = event_time(lambda: native.call(
-            "evo_hip_hyena_forward", kind, native.DTYPE_BF16_SPLIT, proj.data_ptr(), length,
+            "evo_hip_hyena_forward", kind, native.DTYPE_BF16_SPLIT | native.DTYPE_BF16_TAPS,
+            proj.data_ptr(), length,
             width, short.data_ptr(), 3, filt.data_ptr(), groups, taps, direct.data_ptr(),
             poles.data_ptr(), residues.data_ptr(), st, None, None, None, ws.data_ptr(),
             ws_bytes, planes_out.data_ptr(), stream), 10)
