@@ -15,8 +15,8 @@
 // Reference semantics: `src/cpu/model.cpp:510-544` (full softmax; the online
 // form below equals it up to F32 rounding).
 //
-// MFMA kernel (head_dim 32/64/128): one 256-thread block = 4 waves x 32
-// queries of one head. K [64 keys][d] and V^T [d][64 keys] tiles of both
+// MFMA kernel (head_dim 32/64/128): one block = 8 waves x 32 queries of one
+// head (two waves per SIMD share each K/V tile). K [64 keys][d] and V^T [d][64 keys] tiles of both
 // planes are DMA'd (global_load_lds) into XOR-swizzled LDS, double buffered,
 // so the next tile streams in while this one computes. Each wave computes
 // S^T = K Q^T (keys x queries) with v_mfma_f32_32x32x16_bf16, so every lane
@@ -119,6 +119,7 @@ __global__ __launch_bounds__(256) void v_transpose_kernel(
 // ------------------------------------------------------------ MFMA kernel
 constexpr int kQueriesPerWave = 32;
 constexpr int kKeys = 64;
+constexpr int kFlashWaves = 8;  // waves (query groups of 32) sharing a K/V tile
 
 // Swizzle of a row of kUnits 16-byte units: 8 consecutive rows read at one
 // logical unit hit 8 distinct 16-byte bank groups.
@@ -134,11 +135,12 @@ struct FlashShape {
   static constexpr int kVPlane = kD * kKeys;         // BF16 per V^T plane
   static constexpr int kStage = 2 * kKPlane + 2 * kVPlane;
   static constexpr size_t kLdsBytes = 2 * kStage * sizeof(uint16_t);
-  static constexpr int kDmaPerWave = kD / 8;         // 1 KB DMA ops per wave per tile
+  static constexpr int kChunksPerPlane = kD / 8;     // 1 KB chunks per K or V^T plane
+  static constexpr int kDmaPerWave = 4 * kChunksPerPlane / kFlashWaves;
 };
 
 template <int kD, typename O>
-__global__ __launch_bounds__(256) void flash_attention_kernel(
+__global__ __launch_bounds__(kFlashWaves * 64) void flash_attention_kernel(
     const uint16_t *__restrict__ q, size_t q_plane, const uint16_t *__restrict__ k_cache,
     const uint16_t *__restrict__ vt_cache, size_t cache_plane, size_t capacity, size_t rows,
     size_t prefix, size_t heads, O out) {
@@ -153,7 +155,8 @@ __global__ __launch_bounds__(256) void flash_attention_kernel(
   // Block -> (head, query block): heaviest (latest) query blocks first; with
   // heads % 8 == 0 the blocks of a head share an XCD (blocks are dealt to
   // the 8 XCDs round-robin), so its K/V tiles are reused from one L2.
-  const size_t query_blocks = (rows + 4 * kQueriesPerWave - 1) / (4 * kQueriesPerWave);
+  constexpr int kBlockQueries = kFlashWaves * kQueriesPerWave;
+  const size_t query_blocks = (rows + kBlockQueries - 1) / kBlockQueries;
   const size_t b = blockIdx.x;
   size_t head, qb;
   if (heads % 8 == 0) {
@@ -164,7 +167,7 @@ __global__ __launch_bounds__(256) void flash_attention_kernel(
     head = b % heads;
     qb = query_blocks - 1 - b / heads;
   }
-  const size_t block_row = qb * (4 * kQueriesPerWave);
+  const size_t block_row = qb * kBlockQueries;
   const size_t row = block_row + wave * kQueriesPerWave + col;  // this lane's query
   const bool active = row < rows;
   const size_t position = prefix + row;
@@ -187,14 +190,14 @@ __global__ __launch_bounds__(256) void flash_attention_kernel(
     }
   }
 
-  // Per-lane DMA sources of tile 0 (op g of this wave: part g / kDmaPerWave
-  // of {K hi, K lo, V hi, V lo}, 1 KB chunk g % kDmaPerWave of that plane).
+  // Per-lane DMA sources of tile 0 (op g of this wave: part g / kChunksPerPlane
+  // of {K hi, K lo, V hi, V lo}, 1 KB chunk g % kChunksPerPlane of that plane).
   const uint16_t *src[Shape::kDmaPerWave];
   int dst[Shape::kDmaPerWave];
 #pragma unroll
   for (int i = 0; i < Shape::kDmaPerWave; ++i) {
     const int g = wave * Shape::kDmaPerWave + i;
-    const int part = g / Shape::kDmaPerWave, chunk = g % Shape::kDmaPerWave;
+    const int part = g / Shape::kChunksPerPlane, chunk = g % Shape::kChunksPerPlane;
     const int flat = chunk * 64 + lane;  // 16-byte unit within the plane
     if (part < 2) {
       const int key = flat / Shape::kKUnits, unit = swizzle<Shape::kKUnits>(key, flat % Shape::kKUnits);
@@ -214,7 +217,7 @@ __global__ __launch_bounds__(256) void flash_attention_kernel(
 #pragma unroll
     for (int i = 0; i < Shape::kDmaPerWave; ++i) {
       const int g = wave * Shape::kDmaPerWave + i;
-      const bool is_k = g / Shape::kDmaPerWave < 2;
+      const bool is_k = g / Shape::kChunksPerPlane < 2;
       dma16(src[i] + (is_k ? k0 * width : k0), stage + dst[i]);
     }
   };
@@ -227,7 +230,7 @@ __global__ __launch_bounds__(256) void flash_attention_kernel(
       o_acc[t][e] = 0.0F;
   float running_max = -INFINITY, partial_sum = 0.0F;
 
-  const size_t last_row = min(rows, block_row + 4 * kQueriesPerWave) - 1;
+  const size_t last_row = min(rows, block_row + kBlockQueries) - 1;
   const size_t tiles = (prefix + last_row + 1 + kKeys - 1) / kKeys;
   const size_t wave_first = prefix + block_row + wave * kQueriesPerWave;  // lowest position
   issue(0);
@@ -422,8 +425,9 @@ Status launch_flash(const uint16_t *q, size_t q_plane, const uint16_t *k_cache,
                                          hipFuncAttributeMaxDynamicSharedMemorySize,
                                          static_cast<int>(lds)),
                      "flash_attention_kernel LDS opt-in"));
-  const size_t blocks = ceil_div(rows, 4 * kQueriesPerWave) * heads;
-  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), lds, stream, q,
+  const size_t blocks = ceil_div(rows, kFlashWaves * kQueriesPerWave) * heads;
+  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(kFlashWaves * 64), lds,
+                     stream, q,
                      q_plane, k_cache, v_cache, cache_plane, capacity, rows, prefix, heads, out);
   return launch_status("flash_attention_kernel");
 }
