@@ -103,6 +103,68 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(
   }
 }
 
+// Register-resident variant for width % 4 == 0 and width <= 1024 * kVec: the
+// row is read once (kVec 16-byte vectors per thread stay in registers), the
+// same per-thread and shuffle reduction order as rms_norm_kernel, and
+// non-temporal stores (the outputs feed the next kernel from HBM anyway).
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2v __attribute__((ext_vector_type(2)));
+
+template <int kVec>
+__global__ __launch_bounds__(256) void rms_norm_reg_kernel(
+    const float *__restrict__ x, size_t width, const float *__restrict__ scale,
+    float eps, float *__restrict__ out, uint16_t *__restrict__ out_hi,
+    uint16_t *__restrict__ out_lo, uint8_t *__restrict__ codes, float code_scale) {
+  __shared__ float partial[4];
+  const size_t row = blockIdx.x;
+  const float *src = x + row * width;
+  float4 v[kVec];
+  float sum = 0.0F;
+#pragma unroll
+  for (int j = 0; j < kVec; ++j) {
+    const size_t c = threadIdx.x * 4 + j * 1024;
+    v[j] = c < width ? *reinterpret_cast<const float4 *>(src + c) : make_float4(0, 0, 0, 0);
+    sum += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
+  }
+  sum = wave_sum(sum);
+  if ((threadIdx.x & 63) == 0)
+    partial[threadIdx.x >> 6] = sum;
+  __syncthreads();
+  const float total = partial[0] + partial[1] + partial[2] + partial[3];
+  const float denominator = sqrtf(total / static_cast<float>(width)) + eps;
+#pragma unroll
+  for (int j = 0; j < kVec; ++j) {
+    const size_t c = threadIdx.x * 4 + j * 1024;
+    if (c >= width)
+      break;
+    const float4 g = *reinterpret_cast<const float4 *>(scale + c);
+    const float y[4] = {v[j].x / denominator * g.x, v[j].y / denominator * g.y,
+                        v[j].z / denominator * g.z, v[j].w / denominator * g.w};
+    const size_t index = row * width + c;
+    if (out != nullptr) {
+      const f32x4v o = {y[0], y[1], y[2], y[3]};
+      __builtin_nontemporal_store(o, reinterpret_cast<f32x4v *>(out + index));
+    }
+    uint16_t hi[4], lo[4];
+    uint8_t code[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      hi[e] = f32_to_bf16(y[e]);
+      lo[e] = f32_to_bf16(y[e] - bf16_to_f32(hi[e]));
+      code[e] = encode_e4m3(bf16_to_f32(hi[e]) * code_scale);
+    }
+    if (out_hi != nullptr)
+      __builtin_nontemporal_store(__builtin_bit_cast(u32x2v, hi),
+                                  reinterpret_cast<u32x2v *>(out_hi + index));
+    if (out_lo != nullptr)
+      __builtin_nontemporal_store(__builtin_bit_cast(u32x2v, lo),
+                                  reinterpret_cast<u32x2v *>(out_lo + index));
+    if (codes != nullptr)
+      __builtin_nontemporal_store(__builtin_bit_cast(uint32_t, code),
+                                  reinterpret_cast<uint32_t *>(codes + index));
+  }
+}
+
 // history[h, c] <- row h of the last H rows of [history ; x]. Each thread owns
 // one channel and walks h upwards, so an old row is read before it is
 // overwritten (it only moves to a lower index).
@@ -143,8 +205,19 @@ Status rms_norm(const float *x, size_t rows, size_t width, const float *scale,
       width == 0 || rows > (1U << 31) ||
       (codes != nullptr && !(code_scale > 0.0F && __builtin_isfinite(code_scale))))
     return {ErrorCode::kInvalidArgument, "rms_norm: invalid arguments"};
-  hipLaunchKernelGGL(rms_norm_kernel, dim3(static_cast<unsigned>(rows)), dim3(256),
-                     0, stream, x, width, scale, eps, out, out_hi, out_lo, codes, code_scale);
+  const dim3 grid(static_cast<unsigned>(rows)), block(256);
+  if (width % 4 == 0 && width <= 2048)
+    hipLaunchKernelGGL(rms_norm_reg_kernel<2>, grid, block, 0, stream, x, width, scale, eps,
+                       out, out_hi, out_lo, codes, code_scale);
+  else if (width % 4 == 0 && width <= 4096)
+    hipLaunchKernelGGL(rms_norm_reg_kernel<4>, grid, block, 0, stream, x, width, scale, eps,
+                       out, out_hi, out_lo, codes, code_scale);
+  else if (width % 4 == 0 && width <= 8192)
+    hipLaunchKernelGGL(rms_norm_reg_kernel<8>, grid, block, 0, stream, x, width, scale, eps,
+                       out, out_hi, out_lo, codes, code_scale);
+  else
+    hipLaunchKernelGGL(rms_norm_kernel, grid, block, 0, stream, x, width, scale, eps, out,
+                       out_hi, out_lo, codes, code_scale);
   return launch_status("rms_norm_kernel");
 }
 
