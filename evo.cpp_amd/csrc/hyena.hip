@@ -1113,6 +1113,14 @@ constexpr int kMsSegment = 1024;
 constexpr int kMsLead = 4;
 constexpr int kMsUStride = 40;      // BF16 per channel in the u stage (80 B)
 
+// Column of row `row` (0..31) of channel c in the u stage: 8-row units
+// XOR-swizzled by (c >> 3) & 3, so the production writes of 16 lanes (16
+// even channels, one unit) and the fragment reads of 8 lanes (8 consecutive
+// channels) hit distinct banks; 8-row units stay 16-byte aligned.
+__device__ inline int ms_ucol(int c, int row) {
+  return (((row >> 3) ^ ((c >> 3) & 3)) << 3) + (row & 7);
+}
+
 template <typename O> struct MsOut;
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 // One 16-byte non-temporal store (global_store_dwordx4 nt).
@@ -1408,9 +1416,9 @@ __global__ __launch_bounds__(256, 2) void hyena_fir_mfma_stream_kernel(
       }
 #pragma unroll
     for (int ch = 0; ch < 2; ++ch) {
-      *reinterpret_cast<uint2 *>(&uplanes[0][2 * pair + ch][4 * rg]) =
+      *reinterpret_cast<uint2 *>(&uplanes[0][2 * pair + ch][ms_ucol(2 * pair + ch, 4 * rg)]) =
           make_uint2(uh[ch][0], uh[ch][1]);
-      *reinterpret_cast<uint2 *>(&uplanes[1][2 * pair + ch][4 * rg]) =
+      *reinterpret_cast<uint2 *>(&uplanes[1][2 * pair + ch][ms_ucol(2 * pair + ch, 4 * rg)]) =
           make_uint2(ul[ch][0], ul[ch][1]);
     }
   };
@@ -1425,8 +1433,8 @@ __global__ __launch_bounds__(256, 2) void hyena_fir_mfma_stream_kernel(
       ring_hi[q] = ring_hi[q + 1];
       ring_lo[q] = ring_lo[q + 1];
     }
-    ring_hi[kMsK - 1] = *reinterpret_cast<const u32x4 *>(&uplanes[0][ch][8 * g]);
-    ring_lo[kMsK - 1] = *reinterpret_cast<const u32x4 *>(&uplanes[1][ch][8 * g]);
+    ring_hi[kMsK - 1] = *reinterpret_cast<const u32x4 *>(&uplanes[0][ch][ms_ucol(ch, 8 * g)]);
+    ring_lo[kMsK - 1] = *reinterpret_cast<const u32x4 *>(&uplanes[1][ch][ms_ucol(ch, 8 * g)]);
     if (step < lead)
       return;
     // Two independent accumulator chains, interleaved.
@@ -1446,8 +1454,8 @@ __global__ __launch_bounds__(256, 2) void hyena_fir_mfma_stream_kernel(
     for (int half = 0; half < 2; ++half) {
       const f32x4 acc = accs[half];
       const int r = 16 * half + 4 * g;
-      const uint2 uhi = *reinterpret_cast<const uint2 *>(&uplanes[0][ch][r]);
-      const uint2 ulo = *reinterpret_cast<const uint2 *>(&uplanes[1][ch][r]);
+      const uint2 uhi = *reinterpret_cast<const uint2 *>(&uplanes[0][ch][ms_ucol(ch, r)]);
+      const uint2 ulo = *reinterpret_cast<const uint2 *>(&uplanes[1][ch][ms_ucol(ch, r)]);
       const uint32_t hw[4] = {uhi.x << 16, uhi.x & 0xffff0000U, uhi.y << 16, uhi.y & 0xffff0000U};
       const uint32_t lw[4] = {ulo.x << 16, ulo.x & 0xffff0000U, ulo.y << 16, ulo.y & 0xffff0000U};
 #pragma unroll
