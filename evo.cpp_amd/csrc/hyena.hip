@@ -25,7 +25,7 @@ namespace evo::hip {
 namespace {
 
 constexpr int kChannels = 64;    // channels per block (one wave)
-constexpr int kChunk = 64;       // HCL rows per chunk
+constexpr int kChunk = 128;      // HCL rows per chunk
 constexpr int kMaxState = 16;
 constexpr int kMaxShort = 8;
 
@@ -908,13 +908,26 @@ struct PairShort {
 
 constexpr int kHclBatch = 4;
 
+// Lanes l and l ^ 1 share a channel pair: both run the short FIR, lane
+// half h = l & 1 keeps modal states 8h .. 8h+7 of both channels, and the two
+// partial modal sums meet through one DPP swap. Half the state registers per
+// lane (two waves more per SIMD) for a duplicated short FIR.
+constexpr int kHclHalf = kMaxState / 2;
+
+__device__ inline float swap_pair(float v) {
+  // quad_perm [1, 0, 3, 2]: each lane reads its neighbour's value.
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+      0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+}
+
 // Phase 1: final local state of every chunk from a zero start.
 template <typename T>
 __global__ __launch_bounds__(256) void hcl_state_pair_kernel(
     const T *__restrict__ P, const float *__restrict__ short_history,
     const uint16_t *__restrict__ short_filter, size_t L, size_t W,
     const float *__restrict__ poles, int S, float *__restrict__ chunk_state) {
-  const size_t c = blockIdx.x * 512ULL + (threadIdx.x >> 6) * 128 + 2 * (threadIdx.x & 63);
+  const int lane = threadIdx.x & 63, half = lane & 1;
+  const size_t c = blockIdx.x * 256ULL + (threadIdx.x >> 6) * 64 + 2 * (lane >> 1);
   if (c >= W)
     return;
   const size_t g = blockIdx.y;
@@ -923,13 +936,14 @@ __global__ __launch_bounds__(256) void hcl_state_pair_kernel(
   PairShort<T> sh;
   sh.taps(short_filter, c);
   sh.prime(P, short_history, t0, W, c);
-  float p[2][kMaxState], st[2][kMaxState];
+  float p[2][kHclHalf], st[2][kHclHalf];
 #pragma unroll
   for (int ch = 0; ch < 2; ++ch)
 #pragma unroll
-    for (int m = 0; m < kMaxState; ++m) {
-      p[ch][m] = m < S ? poles[(c + ch) * S + m] : 0.0F;
-      st[ch][m] = 0.0F;
+    for (int i = 0; i < kHclHalf; ++i) {
+      const int m = kHclHalf * half + i;
+      p[ch][i] = m < S ? poles[(c + ch) * S + m] : 0.0F;
+      st[ch][i] = 0.0F;
     }
   const uint32_t row_bytes = static_cast<uint32_t>(3 * W * sizeof(T));
   const auto in = buffer_resource(P + t0 * 3 * W, rows * row_bytes);
@@ -957,15 +971,17 @@ __global__ __launch_bounds__(256) void hcl_state_pair_kernel(
 #pragma unroll
       for (int ch = 0; ch < 2; ++ch)
 #pragma unroll
-        for (int m = 0; m < kMaxState; ++m)
-          st[ch][m] = p[ch][m] * st[ch][m] + u[ch];
+        for (int i = 0; i < kHclHalf; ++i)
+          st[ch][i] = p[ch][i] * st[ch][i] + u[ch];
     }
   }
 #pragma unroll
-  for (int m = 0; m < kMaxState; ++m)
+  for (int i = 0; i < kHclHalf; ++i) {
+    const int m = kHclHalf * half + i;
     if (m < S)
       *reinterpret_cast<float2 *>(&chunk_state[(g * S + m) * W + c]) =
-          make_float2(st[0][m], st[1][m]);
+          make_float2(st[0][i], st[1][i]);
+  }
 }
 
 // Phase 2: chunk-start states in place (and the final state), four segments
@@ -1021,14 +1037,61 @@ __global__ __launch_bounds__(256) void hcl_carry_seg_kernel(
     modal_state[c * S + m] = state;
 }
 
-// Phase 3: rescan every chunk from its true start state and write y.
+// Phase 3: rescan every chunk from its true start state and write y. Both
+// lanes of a pair hold y of both channels; the even lane stores the hi
+// plane (or the BF16 / F32 values of channel c), the odd lane the lo plane
+// (or channel c + 1 of an F32 output).
+template <typename O> struct HalfOut;
+template <> struct HalfOut<float *> {
+  __amdgpu_buffer_rsrc_t out;
+  __device__ HalfOut(float *o, size_t first, size_t rows, size_t W) {
+    out = buffer_resource(o + first * W, static_cast<uint32_t>(rows * W * 4));
+  }
+  __device__ void put(int half, uint32_t lane, uint32_t row, float a, float b) const {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, half ? b : a), out,
+                                          static_cast<int>(2 * lane + 4 * half),
+                                          static_cast<int>(2 * row), kStreamStore);
+  }
+};
+template <> struct HalfOut<uint16_t *> {
+  __amdgpu_buffer_rsrc_t out;
+  __device__ HalfOut(uint16_t *o, size_t first, size_t rows, size_t W) {
+    out = buffer_resource(o + first * W, static_cast<uint32_t>(rows * W * 2));
+  }
+  __device__ void put(int half, uint32_t lane, uint32_t row, float a, float b) const {
+    if (half == 0)
+      __builtin_amdgcn_raw_buffer_store_b32(pack_bf16(a, b), out, static_cast<int>(lane),
+                                            static_cast<int>(row), kStreamStore);
+  }
+};
+template <> struct HalfOut<SplitOut> {
+  __amdgpu_buffer_rsrc_t plane;
+  __device__ HalfOut(const SplitOut &o, size_t first, size_t rows, size_t W) {
+    // The odd lane's resource is the lo plane, or empty (stores dropped).
+    const int half = threadIdx.x & 1;
+    const uint16_t *base = half == 0 ? o.hi : o.lo;
+    plane = buffer_resource(base != nullptr ? base + first * W : o.hi,
+                            base != nullptr ? static_cast<uint32_t>(rows * W * 2) : 0);
+  }
+  __device__ void put(int half, uint32_t lane, uint32_t row, float a, float b) const {
+    const uint32_t h = pack_bf16(a, b);
+    const uint32_t word =
+        half == 0 ? h
+                  : pack_bf16(a - __builtin_bit_cast(float, h << 16),
+                              b - __builtin_bit_cast(float, h & 0xffff0000U));
+    __builtin_amdgcn_raw_buffer_store_b32(word, plane, static_cast<int>(lane),
+                                          static_cast<int>(row), kStreamStore);
+  }
+};
+
 template <typename T, typename O>
 __global__ __launch_bounds__(256) void hcl_output_pair_kernel(
     const T *__restrict__ P, const float *__restrict__ short_history,
     const uint16_t *__restrict__ short_filter, size_t L, size_t W,
     const float *__restrict__ poles, const float *__restrict__ residues,
     const float *__restrict__ direct, int S, const float *__restrict__ chunk_state, O out) {
-  const size_t c = blockIdx.x * 512ULL + (threadIdx.x >> 6) * 128 + 2 * (threadIdx.x & 63);
+  const int lane = threadIdx.x & 63, half = lane & 1;
+  const size_t c = blockIdx.x * 256ULL + (threadIdx.x >> 6) * 64 + 2 * (lane >> 1);
   if (c >= W)
     return;
   const size_t g = blockIdx.y;
@@ -1037,21 +1100,22 @@ __global__ __launch_bounds__(256) void hcl_output_pair_kernel(
   PairShort<T> sh;
   sh.taps(short_filter, c);
   sh.prime(P, short_history, t0, W, c);
-  float p[2][kMaxState], r[2][kMaxState], st[2][kMaxState], d[2];
+  float p[2][kHclHalf], r[2][kHclHalf], st[2][kHclHalf], d[2];
 #pragma unroll
   for (int ch = 0; ch < 2; ++ch) {
 #pragma unroll
-    for (int m = 0; m < kMaxState; ++m) {
-      p[ch][m] = m < S ? poles[(c + ch) * S + m] : 0.0F;
-      r[ch][m] = m < S ? residues[(c + ch) * S + m] : 0.0F;
-      st[ch][m] = m < S ? chunk_state[(g * S + m) * W + c + ch] : 0.0F;
+    for (int i = 0; i < kHclHalf; ++i) {
+      const int m = kHclHalf * half + i;
+      p[ch][i] = m < S ? poles[(c + ch) * S + m] : 0.0F;
+      r[ch][i] = m < S ? residues[(c + ch) * S + m] : 0.0F;
+      st[ch][i] = m < S ? chunk_state[(g * S + m) * W + c + ch] : 0.0F;
     }
     d[ch] = direct[c + ch];
   }
   const uint32_t row_bytes = static_cast<uint32_t>(3 * W * sizeof(T));
   const auto in = buffer_resource(P + t0 * 3 * W, rows * row_bytes);
   const uint32_t lane_bytes = static_cast<uint32_t>(3 * c * sizeof(T));
-  const PairOut<O> sink(out, t0, rows, W);
+  const HalfOut<O> sink(out, t0, rows, W);
   const uint32_t out_lane = static_cast<uint32_t>(c * 2);
   const uint32_t out_row = static_cast<uint32_t>(W * 2);
   PairRow<T> next[kHclBatch];
@@ -1076,14 +1140,17 @@ __global__ __launch_bounds__(256) void hcl_output_pair_kernel(
       for (int ch = 0; ch < 2; ++ch) {
         float modal = 0.0F;
 #pragma unroll
-        for (int m = 0; m < kMaxState; ++m) {
-          st[ch][m] = p[ch][m] * st[ch][m] + u[ch];
-          modal += r[ch][m] * st[ch][m];
+        for (int i = 0; i < kHclHalf; ++i) {
+          st[ch][i] = p[ch][i] * st[ch][i] + u[ch];
+          modal += r[ch][i] * st[ch][i];
         }
-        y[ch] = x2[ch] * (modal + d[ch] * u[ch]);
+        // States 0..7 first, then 8..15, in both lanes of the pair.
+        const float other = swap_pair(modal);
+        const float total = half == 0 ? modal + other : other + modal;
+        y[ch] = x2[ch] * (total + d[ch] * u[ch]);
       }
       // Rows past the chunk end are dropped by the store bound.
-      sink.put(out_lane, (base + b) * out_row, y[0], y[1]);
+      sink.put(half, out_lane, (base + b) * out_row, y[0], y[1]);
     }
   }
 }
@@ -1725,7 +1792,7 @@ Status hyena_forward(int kind, const T *projection, size_t length,
     float *chunk_state = static_cast<float *>(workspace);
     const int S = static_cast<int>(wt.state);
     if (short_len == 3 && planar == 0 && width % 2 == 0) {
-      const dim3 grid(ceil_div(width, 512), static_cast<unsigned>(G));
+      const dim3 grid(ceil_div(width, 256), static_cast<unsigned>(G));
       hipLaunchKernelGGL(hcl_state_pair_kernel<T>, grid, dim3(256), 0, stream, projection,
                          short_history, wt.short_filter, length, width, wt.poles, S,
                          chunk_state);
