@@ -14,8 +14,8 @@
 // ~2^-17) for twice the MFMA work; without lo (profile hip-bf16) one pass.
 //
 // Tiling for CDNA4: block tile 256 x 256, K step 32. The main kernel runs
-// 512 threads = 8 waves as 2 (M) x 4 (N), each owning 128 x 64 = 4 x 2 MFMA
-// 32x32x16 tiles (128 F32 accumulators per lane), two waves per SIMD so one
+// 512 threads = 8 waves as 2 (M) x 4 (N), each owning 128 x 64 = 8 x 4 MFMA
+// 16x16x32 tiles (128 F32 accumulators per lane), two waves per SIMD so one
 // wave's MFMAs cover the other's LDS reads and barrier waits. Operands reach
 // LDS by DMA (global_load_lds_dwordx4) into XOR-swizzled, unpadded rows,
 // triple-buffered. The fallback kernel (K % 32 != 0) runs 4 waves of
@@ -45,53 +45,6 @@ struct Epilogue {
 __device__ inline float gelu_erf(const float x) {
   return 0.5F * x * (1.0F + erff(x * 0.7071067811865475244F));
 }
-
-// Epilogue of one 32x32 accumulator tile: element e sits at row
-// row0 + (e/4)*8 + e%4 (row0 already includes the lane-half offset) and
-// column col of the output.
-__device__ __forceinline__ void store_tile(const f32x16 &tile, int row0, int col, int M,
-                                           int N, int ldc, const Epilogue &epi, float *C) {
-  if (col >= N)
-    return;
-  const float bias = (epi.mode == kGemmBias || epi.mode == kGemmBiasResidual)
-                         ? bf16_to_f32(epi.bias[col]) : 0.0F;
-#pragma unroll
-  for (int e = 0; e < 16; ++e) {
-    const int row = row0 + (e >> 2) * 8 + (e & 3);
-    if (row < M) {
-      const size_t index = static_cast<size_t>(row) * ldc + col;
-      float value = tile[e];
-      if (epi.mode == kGemmBias || epi.mode == kGemmBiasResidual)
-        value = value + bias;
-      if (epi.mode == kGemmResidual || epi.mode == kGemmBiasResidual)
-        value = value + epi.residual[index];
-      C[index] = value;
-    }
-  }
-}
-
-// Gated epilogue: `first` holds l1 outputs and `second` the matching l2
-// outputs of the same 32 gated columns; writes act(first) * second as planes.
-__device__ __forceinline__ void store_gated(const f32x16 &first, const f32x16 &second,
-                                            int row0, int col, int M, int ldc,
-                                            const Epilogue &epi, uint16_t *c_hi,
-                                            uint16_t *c_lo) {
-  if (col >= epi.gated_width)
-    return;
-#pragma unroll
-  for (int e = 0; e < 16; ++e) {
-    const int row = row0 + (e >> 2) * 8 + (e & 3);
-    if (row < M) {
-      const float value = (epi.gelu ? gelu_erf(first[e]) : first[e]) * second[e];
-      const size_t index = static_cast<size_t>(row) * ldc + col;
-      const uint16_t hi = f32_to_bf16(value);
-      c_hi[index] = hi;
-      if (c_lo != nullptr)
-        c_lo[index] = f32_to_bf16(value - bf16_to_f32(hi));
-    }
-  }
-}
-
 
 template <bool kSplit>
 __global__ __launch_bounds__(kThreads) void gemm_staged_kernel(
@@ -308,19 +261,21 @@ __global__ __launch_bounds__(512) void gemm_kernel(
     }
   };
 
-  f32x16 acc[4][2];
+  f32x4 acc[8][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int e = 0; e < 16; ++e)
+      for (int e = 0; e < 4; ++e)
         acc[i][j][e] = 0.0F;
 
   const int steps = K / kBK;
   issue(0);
   if (steps > 1)
     issue(1);
+  const int seg = lane >> 4;
+  const int r16 = lane & 15;
   for (int s = 0; s < steps; ++s) {
     // Wait for this wave's DMA of step s (the step s+1 batch may stay in
     // flight), then for every wave's.
@@ -339,71 +294,104 @@ __global__ __launch_bounds__(512) void gemm_kernel(
     const uint16_t *sa_hi = stage;
     const uint16_t *sa_lo = stage + kPlane;
     const uint16_t *sw = stage + (kPlanes - 1) * kPlane;
-    // Fragments of both 16-wide K halves; the reads of half 1 are issued
-    // before the MFMAs of half 0 so their latency hides behind them.
-    bf16x8 b[2][2], ah[2][4], al[2][4];
-    auto read = [&](int ks) {
-      const int seg = 2 * ks + (lane >> 5);
+    // One 16x16x32 fragment covers the whole K step: lane l reads row l%16
+    // of its tile, 16-byte unit l/16. B and the A tiles 0-3 are read first;
+    // the reads of tiles 4-7 interleave with the MFMAs of tiles 0-3 (one
+    // LDS read, then four MFMAs).
+    bf16x8 b[4], ah[8], al[8];
+    auto read_a = [&](int i0) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
-        b[ks][j] = *reinterpret_cast<const bf16x8 *>(
-            sw + swizzled_unit(wave_n * 64 + j * 32 + (lane & 31), seg) * 8);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        ah[ks][i] = *reinterpret_cast<const bf16x8 *>(
-            sa_hi + swizzled_unit(wave_m * 128 + i * 32 + (lane & 31), seg) * 8);
-      if (kSplit) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          al[ks][i] = *reinterpret_cast<const bf16x8 *>(
-              sa_lo + swizzled_unit(wave_m * 128 + i * 32 + (lane & 31), seg) * 8);
+      for (int i = i0; i < i0 + 4; ++i) {
+        ah[i] = *reinterpret_cast<const bf16x8 *>(
+            sa_hi + swizzled_unit(wave_m * 128 + i * 16 + r16, seg) * 8);
+        if (kSplit)
+          al[i] = *reinterpret_cast<const bf16x8 *>(
+              sa_lo + swizzled_unit(wave_m * 128 + i * 16 + r16, seg) * 8);
       }
     };
-    auto multiply = [&](int ks) {
+    auto multiply = [&](int i0) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = i0; i < i0 + 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[ks][i], b[ks][j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], b[j], acc[i][j], 0, 0, 0);
       if (kSplit) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = i0; i < i0 + 4; ++i)
 #pragma unroll
-          for (int j = 0; j < 2; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[ks][i], b[ks][j], acc[i][j], 0, 0, 0);
+          for (int j = 0; j < 4; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], b[j], acc[i][j], 0, 0, 0);
       }
     };
-    read(0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      b[j] = *reinterpret_cast<const bf16x8 *>(
+          sw + swizzled_unit(wave_n * 64 + j * 16 + r16, seg) * 8);
+    read_a(0);
     __builtin_amdgcn_sched_barrier(0);
-    // The K-half-1 reads are interleaved with the K-half-0 MFMAs (one LDS
-    // read, then two MFMAs) instead of being issued as one burst.
-    read(1);
+    read_a(4);
     multiply(0);
 #pragma unroll
-    for (int q = 0; q < 10; ++q) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+    for (int q = 0; q < (kSplit ? 8 : 4); ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
-    multiply(1);
+    multiply(4);
   }
 
+  // Accumulator e of tile (i, j): row i*16 + 4*(lane/16) + e, column
+  // j*16 + lane%16 of the wave's 128 x 64 sub-tile. Gated mode: columns
+  // [64q, 64q+32) hold l1 rows and [64q+32, 64q+64) the matching l2 rows,
+  // so tiles j and j+2 pair up in-lane.
   const int wave_col = block_n + wave_n * 64;
-  const int wave_row = block_m + wave_m * 128 + (lane >> 5) * 4;
-  if (epi.mode == kGemmGated) {
+  const int wave_row = block_m + wave_m * 128 + (lane >> 4) * 4;
+  const bool bias_mode = epi.mode == kGemmBias || epi.mode == kGemmBiasResidual;
+  const bool res_mode = epi.mode == kGemmResidual || epi.mode == kGemmBiasResidual;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 8; ++i) {
+    if (epi.mode == kGemmGated) {
 #pragma unroll
-      for (int pair = 0; pair < 1; ++pair)
-        store_gated(acc[i][2 * pair], acc[i][2 * pair + 1], wave_row + i * 32,
-                    wave_col / 2 + pair * 32 + (lane & 31), M, ldc, epi, c_hi, c_lo);
-  } else {
+      for (int j = 0; j < 2; ++j) {
+        const int col = wave_col / 2 + j * 16 + r16;
+        if (col >= epi.gated_width)
+          continue;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+        for (int e = 0; e < 4; ++e) {
+          const int row = wave_row + i * 16 + e;
+          if (row < M) {
+            const float first = acc[i][j][e];
+            const float value = (epi.gelu ? gelu_erf(first) : first) * acc[i][j + 2][e];
+            const size_t index = static_cast<size_t>(row) * ldc + col;
+            const uint16_t hi = f32_to_bf16(value);
+            c_hi[index] = hi;
+            if (c_lo != nullptr)
+              c_lo[index] = f32_to_bf16(value - bf16_to_f32(hi));
+          }
+        }
+      }
+    } else {
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
-        store_tile(acc[i][j], wave_row + i * 32, wave_col + j * 32 + (lane & 31), M, N, ldc,
-                   epi, C);
+      for (int j = 0; j < 4; ++j) {
+        const int col = wave_col + j * 16 + r16;
+        if (col >= N)
+          continue;
+        const float bias = bias_mode ? bf16_to_f32(epi.bias[col]) : 0.0F;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int row = wave_row + i * 16 + e;
+          if (row < M) {
+            const size_t index = static_cast<size_t>(row) * ldc + col;
+            float value = acc[i][j][e];
+            if (bias_mode)
+              value = value + bias;
+            if (res_mode)
+              value = value + epi.residual[index];
+            C[index] = value;
+          }
+        }
+      }
+    }
   }
 }
 
