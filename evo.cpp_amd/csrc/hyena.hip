@@ -1197,8 +1197,9 @@ __device__ inline void store16_nt(void *dst, const void *lds_src) {
 }
 // y is staged in LDS as F32 [row][64]; the flush writes whole rows: lane ->
 // row tid / 8, channels (tid % 8) * 8 .. + 7, converting to the output type
-// there; rows at or past `rows` (the segment end) are skipped. `stores` is
-// the number of store instructions a wave issues per flush.
+// there. `index` is the lane's first output element; the caller skips rows
+// at or past the segment end. `stores` is the number of store instructions a
+// wave issues per flush.
 // (No __builtin_bit_cast of a vector element anywhere in this file: this
 // compiler folds such a cast to element 0.)
 __device__ inline void load8(const float *s, float (&v)[8]) {
@@ -1216,42 +1217,28 @@ __device__ inline void store16_words(void *dst, const uint32_t (&w)[4]) {
 }
 template <> struct MsOut<float *> {
   __device__ static int stores(float *) { return 2; }
-  __device__ static void flush(const float *s, float *out, size_t first, uint32_t rows,
-                               size_t W, size_t c0, uint32_t r0, int tid) {
-    const int row = tid >> 3, part = tid & 7;
-    if (r0 + row >= rows)
-      return;
-    float *dst = out + (first + r0 + row) * W + c0 + part * 8;
-    const float *src = s + row * kMsChannels + part * 8;
-    store16_nt(dst, src);
-    store16_nt(dst + 4, src + 4);
+  __device__ static void flush(const float *src, float *out, size_t index) {
+    store16_nt(out + index, src);
+    store16_nt(out + index + 4, src + 4);
   }
 };
 template <> struct MsOut<uint16_t *> {
   __device__ static int stores(uint16_t *) { return 1; }
-  __device__ static void flush(const float *s, uint16_t *out, size_t first, uint32_t rows,
-                               size_t W, size_t c0, uint32_t r0, int tid) {
-    const int row = tid >> 3, part = tid & 7;
-    if (r0 + row >= rows)
-      return;
+  __device__ static void flush(const float *src, uint16_t *out, size_t index) {
     float v[8];
-    load8(s + row * kMsChannels + part * 8, v);
+    load8(src, v);
     uint32_t w[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       w[i] = pack_bf16(v[2 * i], v[2 * i + 1]);
-    store16_words(out + (first + r0 + row) * W + c0 + part * 8, w);
+    store16_words(out + index, w);
   }
 };
 template <> struct MsOut<SplitOut> {
   __device__ static int stores(const SplitOut &out) { return out.lo != nullptr ? 2 : 1; }
-  __device__ static void flush(const float *s, const SplitOut &out, size_t first,
-                               uint32_t rows, size_t W, size_t c0, uint32_t r0, int tid) {
-    const int row = tid >> 3, part = tid & 7;
-    if (r0 + row >= rows)
-      return;
+  __device__ static void flush(const float *src, const SplitOut &out, size_t index) {
     float v[8];
-    load8(s + row * kMsChannels + part * 8, v);
+    load8(src, v);
     uint32_t hi[4], lo[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -1259,7 +1246,6 @@ template <> struct MsOut<SplitOut> {
       lo[i] = pack_bf16(v[2 * i] - __builtin_bit_cast(float, hi[i] << 16),
                         v[2 * i + 1] - __builtin_bit_cast(float, hi[i] & 0xffff0000U));
     }
-    const size_t index = (first + r0 + row) * W + c0 + part * 8;
     store16_words(out.hi + index, hi);
     if (out.lo != nullptr)
       store16_words(out.lo + index, lo);
@@ -1296,7 +1282,8 @@ __global__ __launch_bounds__(256, 2) void hyena_fir_mfma_stream_kernel(
   const unsigned linear = xcd * q8 + min(xcd, r8) + blockIdx.x / 8;
   const unsigned segment = linear / channel_blocks;
   const size_t c0 = static_cast<size_t>(linear % channel_blocks) * kMsChannels;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const size_t t0 = static_cast<size_t>(segment) * kMsSegment;
   const uint32_t seg_rows = static_cast<uint32_t>(min(L - t0, static_cast<size_t>(kMsSegment)));
   const int lead = t0 == 0 ? 0 : kMsLead;
@@ -1408,7 +1395,7 @@ __global__ __launch_bounds__(256, 2) void hyena_fir_mfma_stream_kernel(
       }
       a[half][q] = __builtin_bit_cast(u32x4, taps);
     }
-  float d = direct != nullptr ? direct[cw] : 0.0F;
+  float d = direct[cw];
   // Keep d in a register: a global load re-issued inside the step loop would
   // make the wait for it also wait for every DMA in flight.
   asm volatile("" : "+v"(d));
@@ -1416,9 +1403,10 @@ __global__ __launch_bounds__(256, 2) void hyena_fir_mfma_stream_kernel(
 #pragma unroll
   for (int q = 0; q < kMsK; ++q) {
     // Window rows before the first step (only the first segment has them:
-    // u rows -128 .. -1 from the inner history; others start at zero). The
-    // ring shifts once before its first use, so slot q holds rows of step
-    // q - 1 relative to the first window.
+    // u rows -128 .. -1 from the inner history; others start at zero). At
+    // step 0 window slot q is register q + 1 (slot 4, register 0, receives
+    // step 0), so register q holds rows of step q - 1 relative to the first
+    // window.
     uint16_t hi[8] = {}, lo[8] = {};
     if (lead == 0 && inner_history != nullptr && q > 0) {
 #pragma unroll
@@ -1437,7 +1425,11 @@ __global__ __launch_bounds__(256, 2) void hyena_fir_mfma_stream_kernel(
   // ---- Production of step `step`: rows t_start + 32 step + 4 rg .. + 3
   // from its stage (complete: waited for before the last barrier), u into
   // u_s[step % 2] and x2 into xy_s[step % 3].
-  auto produce = [&](int step) {
+  constexpr int kUPlane = kMsChannels * kMsUStride;  // BF16 per u plane
+  const int x2_lane = 4 * rg * kMsChannels + 2 * pair;
+  const int u_prod[2] = {2 * pair * kMsUStride + ms_ucol(2 * pair, 4 * rg),
+                         (2 * pair + 1) * kMsUStride + ms_ucol(2 * pair + 1, 4 * rg)};
+  auto produce = [&](int step) __attribute__((always_inline)) {
     PairRow<T> cur[kRows];
     const long first_row = static_cast<long>(t_start) + step * kMsStep + 4 * rg - (kWin - 1);
     if (static_cast<long>(t_start) + step * kMsStep >= kWin - 1) {
@@ -1453,8 +1445,8 @@ __global__ __launch_bounds__(256, 2) void hyena_fir_mfma_stream_kernel(
           history_row(first_row + i, cur[i]);
       }
     }
-    float(*x2)[kMsChannels] = xy_s[step % 3];
-    uint16_t(*uplanes)[kMsChannels][kMsUStride] = u_s[step & 1];
+    float *x2 = &xy_s[step % 3][0][0] + x2_lane;
+    uint16_t *uplanes = &u_s[step & 1][0][0][0];
     float u[2][4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -1469,7 +1461,7 @@ __global__ __launch_bounds__(256, 2) void hyena_fir_mfma_stream_kernel(
       }
       u[0][j] = fir[1] * fir[2];
       u[1][j] = fir[4] * fir[5];
-      *reinterpret_cast<float2 *>(&x2[4 * rg + j][2 * pair]) = make_float2(fir[0], fir[3]);
+      *reinterpret_cast<float2 *>(x2 + j * kMsChannels) = make_float2(fir[0], fir[3]);
     }
     // Rows (0, 1) and (2, 3) of a channel pack into one word per plane.
     uint32_t uh[2][2], ul[2][2];
@@ -1483,9 +1475,8 @@ __global__ __launch_bounds__(256, 2) void hyena_fir_mfma_stream_kernel(
       }
 #pragma unroll
     for (int ch = 0; ch < 2; ++ch) {
-      *reinterpret_cast<uint2 *>(&uplanes[0][2 * pair + ch][ms_ucol(2 * pair + ch, 4 * rg)]) =
-          make_uint2(uh[ch][0], uh[ch][1]);
-      *reinterpret_cast<uint2 *>(&uplanes[1][2 * pair + ch][ms_ucol(2 * pair + ch, 4 * rg)]) =
+      *reinterpret_cast<uint2 *>(uplanes + u_prod[ch]) = make_uint2(uh[ch][0], uh[ch][1]);
+      *reinterpret_cast<uint2 *>(uplanes + kUPlane + u_prod[ch]) =
           make_uint2(ul[ch][0], ul[ch][1]);
     }
   };
@@ -1493,15 +1484,22 @@ __global__ __launch_bounds__(256, 2) void hyena_fir_mfma_stream_kernel(
   // ---- Products of step `step`: ring update from u_s[step % 2]; when the
   // step emits, Y = T . U and y = x2 * (Y + d u) in place of x2.
   const int ch = 16 * wave + col;
-  auto multiply = [&](int step) {
-    const uint16_t(*uplanes)[kMsChannels][kMsUStride] = u_s[step & 1];
-#pragma unroll
-    for (int q = 0; q < kMsK - 1; ++q) {
-      ring_hi[q] = ring_hi[q + 1];
-      ring_lo[q] = ring_lo[q + 1];
-    }
-    ring_hi[kMsK - 1] = *reinterpret_cast<const u32x4 *>(&uplanes[0][ch][ms_ucol(ch, 8 * g)]);
-    ring_lo[kMsK - 1] = *reinterpret_cast<const u32x4 *>(&uplanes[1][ch][ms_ucol(ch, 8 * g)]);
+  // Per-lane LDS offsets, fixed for the walk: the ring fragment (rows 8g ..
+  // 8g+7 of channel ch), the epilogue's u rows 16 half + 4g .. + 3, and y.
+  const int u_ring = ch * kMsUStride + ms_ucol(ch, 8 * g);
+  const int u_epi[2] = {ch * kMsUStride + ms_ucol(ch, 4 * g),
+                        ch * kMsUStride + ms_ucol(ch, 16 + 4 * g)};
+  const int y_lane = 4 * g * kMsChannels + ch;
+  // The ring is rotated, not shifted: at step s the window slot q (0 oldest
+  // .. kMsK-1 newest) is register (q + s + 1) % kMsK, and the new fragment
+  // replaces the oldest. `rot` = (s + 1) % kMsK is a compile-time constant of
+  // the unrolled step loop.
+  auto multiply = [&](auto rot, int step) __attribute__((always_inline)) {
+    constexpr int kRot = decltype(rot)::value;
+    const uint16_t *uplanes = &u_s[step & 1][0][0][0];
+    ring_hi[(kMsK - 1 + kRot) % kMsK] = *reinterpret_cast<const u32x4 *>(uplanes + u_ring);
+    ring_lo[(kMsK - 1 + kRot) % kMsK] =
+        *reinterpret_cast<const u32x4 *>(uplanes + kUPlane + u_ring);
     if (step < lead)
       return;
     // Two independent accumulator chains, interleaved.
@@ -1512,32 +1510,38 @@ __global__ __launch_bounds__(256, 2) void hyena_fir_mfma_stream_kernel(
       for (int half = 0; half < 2; ++half) {
         const bf16x8 t = __builtin_bit_cast(bf16x8, a[half][q]);
         accs[half] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            t, __builtin_bit_cast(bf16x8, ring_hi[q]), accs[half], 0, 0, 0);
+            t, __builtin_bit_cast(bf16x8, ring_hi[(q + kRot) % kMsK]), accs[half], 0, 0, 0);
         accs[half] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            t, __builtin_bit_cast(bf16x8, ring_lo[q]), accs[half], 0, 0, 0);
+            t, __builtin_bit_cast(bf16x8, ring_lo[(q + kRot) % kMsK]), accs[half], 0, 0, 0);
       }
-    float(*xy)[kMsChannels] = xy_s[step % 3];
+    float *xy = &xy_s[step % 3][0][0] + y_lane;
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
       const f32x4 acc = accs[half];
-      const int r = 16 * half + 4 * g;
-      const uint2 uhi = *reinterpret_cast<const uint2 *>(&uplanes[0][ch][ms_ucol(ch, r)]);
-      const uint2 ulo = *reinterpret_cast<const uint2 *>(&uplanes[1][ch][ms_ucol(ch, r)]);
+      const uint2 uhi = *reinterpret_cast<const uint2 *>(uplanes + u_epi[half]);
+      const uint2 ulo = *reinterpret_cast<const uint2 *>(uplanes + kUPlane + u_epi[half]);
       const uint32_t hw[4] = {uhi.x << 16, uhi.x & 0xffff0000U, uhi.y << 16, uhi.y & 0xffff0000U};
       const uint32_t lw[4] = {ulo.x << 16, ulo.x & 0xffff0000U, ulo.y << 16, ulo.y & 0xffff0000U};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        float total = acc[e];
-        if (direct != nullptr)
-          total += d * (__builtin_bit_cast(float, hw[e]) + __builtin_bit_cast(float, lw[e]));
-        xy[r + e][ch] *= total;
+        const float total =
+            acc[e] + d * (__builtin_bit_cast(float, hw[e]) + __builtin_bit_cast(float, lw[e]));
+        xy[(16 * half + e) * kMsChannels] *= total;
       }
     }
   };
-  auto flush = [&](int step) {
-    if (step >= lead)
-      MsOut<O>::flush(&xy_s[step % 3][0][0], out, t0, seg_rows, W, c0,
-                      static_cast<uint32_t>((step - lead) * kMsStep), tid);
+  // Flush lane: row tid / 8 of the step, channels (tid % 8) * 8 .. + 7; its
+  // output index advances by one step of rows per flushed step.
+  const int frow = tid >> 3, fpart = tid & 7;
+  size_t flush_index = (t0 + frow) * W + c0 + fpart * 8;
+  uint32_t flush_r0 = 0;
+  auto flush = [&](int step) __attribute__((always_inline)) {
+    if (step >= lead) {
+      if (flush_r0 + frow < seg_rows)
+        MsOut<O>::flush(&xy_s[step % 3][frow][fpart * 8], out, flush_index);
+      flush_index += static_cast<size_t>(kMsStep) * W;
+      flush_r0 += kMsStep;
+    }
   };
 
   // Prologue: stage 0 (younger: the DMA of stage 1), production of step 0,
@@ -1554,14 +1558,14 @@ __global__ __launch_bounds__(256, 2) void hyena_fir_mfma_stream_kernel(
   // Phase s: DMA of step s + 2 into the stage step s used; flush s - 1;
   // produce s + 1; multiply s. Before the barrier, the DMA of step s + 2 must
   // be complete (younger: only the flush stores of step s - 1).
-  for (int step = 0; step < steps; ++step) {
+  auto phase = [&](auto rot, int step) __attribute__((always_inline)) {
     if (step + 2 < steps)
       issue(step + 2);
     if (step >= 1)
       flush(step - 1);
     if (step + 1 < steps)
       produce(step + 1);
-    multiply(step);
+    multiply(rot, step);
     if (step + 2 < steps) {
       if (step - 1 >= lead && stores == 2)
         wait_dma<2>();
@@ -1571,6 +1575,18 @@ __global__ __launch_bounds__(256, 2) void hyena_fir_mfma_stream_kernel(
         wait_dma<0>();
     }
     __syncthreads();
+  };
+  // Unrolled by the ring length so that the rotation is static.
+  for (int step = 0; step < steps; step += kMsK) {
+    phase(std::integral_constant<int, 1>{}, step);
+    if (step + 1 < steps)
+      phase(std::integral_constant<int, 2>{}, step + 1);
+    if (step + 2 < steps)
+      phase(std::integral_constant<int, 3>{}, step + 2);
+    if (step + 3 < steps)
+      phase(std::integral_constant<int, 4>{}, step + 3);
+    if (step + 4 < steps)
+      phase(std::integral_constant<int, 0>{}, step + 4);
   }
   flush(steps - 1);
 }
@@ -1825,7 +1841,7 @@ Status hyena_forward(int kind, const T *projection, size_t length,
                                        group_size, k, causal, direct, length, width, out,
                                        stream)));
     } else if (wt.taps_bf16 && short_len == 3 && planar == 0 && width % kMsChannels == 0 &&
-               group_size % 16 == 0) {
+               group_size % 16 == 0 && direct != nullptr) {
       const unsigned cblocks = static_cast<unsigned>(width / kMsChannels);
       const unsigned segments = ceil_div(length, kMsSegment);
       hipLaunchKernelGGL((hyena_fir_mfma_stream_kernel<T, O>), dim3(cblocks * segments),
