@@ -851,74 +851,87 @@ __global__ __launch_bounds__(kFirThreads) void hyena_fir_mfma_kernel(
 // chunked scan of the modal recurrence with the row stream of the HCS kernel
 // (12/24-byte loads of two channels per lane, packed non-temporal stores).
 // A wave covers 128 channels of one kChunk-row chunk.
+__device__ inline float swap_pair(float v) {
+  // quad_perm [1, 0, 3, 2]: each lane reads its neighbour's value.
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+      0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+}
+
 template <typename T>
 struct PairShort {
-  float stap[6][3], swin[6][3];  // slot 2 is the newest row
+  // Lane half h computes the short FIR of its own channel c + h only; the
+  // pair exchanges what the other lane needs through DPP swaps.
+  float stap[3][3], swin[3][3];  // slot 2 is the newest row
+  uint32_t sel[3];                // BF16 rows: byte selectors of the own columns
+  int half;
   __device__ void taps(const uint16_t *short_filter, size_t c) {
-#pragma unroll
-    for (int ch = 0; ch < 2; ++ch) {
-      float t3[3][3];
-      load_window_taps(short_filter, 3, c + ch, t3);
-#pragma unroll
-      for (int s = 0; s < 3; ++s)
-#pragma unroll
-        for (int i = 0; i < 3; ++i)
-          stap[3 * ch + s][i] = t3[s][i];
-    }
+    half = threadIdx.x & 1;
+    load_window_taps(short_filter, 3, c + half, stap);
+    // The pair's row words are [c col0 | c col1], [c col2 | c+1 col0],
+    // [c+1 col1 | c+1 col2]; v_perm moves the own column's two bytes into
+    // the high half (low half zero), which is its F32 value.
+    sel[0] = half ? 0x07060c0cU : 0x01000c0cU;  // perm(w1, w0)
+    sel[1] = half ? 0x05040c0cU : 0x03020c0cU;  // perm(w2, w0)
+    sel[2] = half ? 0x07060c0cU : 0x01000c0cU;  // perm(w2, w1)
   }
   // Window before row t0: rows t0-2, t0-1 from P, or from the short history
   // (F32 [2][3W]) when they precede row 0.
   __device__ void prime(const T *P, const float *short_history, size_t t0, size_t W, size_t c) {
     const size_t cols3 = 3 * W;
+    const size_t own = 3 * (c + half);
 #pragma unroll
     for (int i = 1; i < 3; ++i) {
       const long row = static_cast<long>(t0) - 3 + i;
 #pragma unroll
-      for (int col = 0; col < 6; ++col) {
+      for (int col = 0; col < 3; ++col) {
         float v = 0.0F;
         if (row >= 0)
-          v = load_act(P, static_cast<size_t>(row) * cols3 + 3 * c + col);
+          v = load_act(P, static_cast<size_t>(row) * cols3 + own + col);
         else if (short_history != nullptr && row + 2 >= 0)
-          v = short_history[static_cast<size_t>(row + 2) * cols3 + 3 * c + col];
+          v = short_history[static_cast<size_t>(row + 2) * cols3 + own + col];
         swin[col][i] = v;
       }
     }
   }
-  // Shifts in one row; x2 and u of both channels.
-  __device__ void step(const PairRow<T> &row, float (&x2)[2], float (&u)[2]) {
-    float fir[6];
+  // Shifts in one row; x2 and u of the own channel, u of the other.
+  __device__ void step(const PairRow<T> &row, float &x2, float &u_own, float &u_other) {
+    float v[3];
+    if constexpr (sizeof(T) == 2) {
+      v[0] = __builtin_bit_cast(float, __builtin_amdgcn_perm(row.word[1], row.word[0], sel[0]));
+      v[1] = __builtin_bit_cast(float, __builtin_amdgcn_perm(row.word[2], row.word[0], sel[1]));
+      v[2] = __builtin_bit_cast(float, __builtin_amdgcn_perm(row.word[2], row.word[1], sel[2]));
+    } else {
 #pragma unroll
-    for (int col = 0; col < 6; ++col) {
+      for (int col = 0; col < 3; ++col)
+        v[col] = __builtin_bit_cast(float, half ? row.word[3 + col] : row.word[col]);
+    }
+    float fir[3];
+#pragma unroll
+    for (int col = 0; col < 3; ++col) {
       swin[col][0] = swin[col][1];
       swin[col][1] = swin[col][2];
-      swin[col][2] = row.at(col);
+      swin[col][2] = v[col];
       float total = 0.0F;
 #pragma unroll
       for (int i = 0; i < 3; ++i)
         total += swin[col][i] * stap[col][i];
       fir[col] = total;
     }
-#pragma unroll
-    for (int ch = 0; ch < 2; ++ch) {
-      x2[ch] = fir[3 * ch];
-      u[ch] = fir[3 * ch + 1] * fir[3 * ch + 2];
-    }
+    x2 = fir[0];
+    u_own = fir[1] * fir[2];
+    u_other = swap_pair(u_own);
   }
 };
 
 constexpr int kHclBatch = 4;
 
-// Lanes l and l ^ 1 share a channel pair: both run the short FIR, lane
-// half h = l & 1 keeps modal states 8h .. 8h+7 of both channels, and the two
-// partial modal sums meet through one DPP swap. Half the state registers per
-// lane (two waves more per SIMD) for a duplicated short FIR.
+// Lanes l and l ^ 1 share a channel pair: lane half h = l & 1 runs the short
+// FIR of channel c + h ("own"; the partner's is "other") and keeps modal
+// states 8h .. 8h+7 of both channels. Per row the pair swaps u, the partial
+// modal sums of the partner's channel and y (DPP), so each lane computes y
+// of its own channel only. Arrays indexed [0] own, [1] other.
 constexpr int kHclHalf = kMaxState / 2;
 
-__device__ inline float swap_pair(float v) {
-  // quad_perm [1, 0, 3, 2]: each lane reads its neighbour's value.
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-      0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
-}
 
 // Phase 1: final local state of every chunk from a zero start.
 template <typename T>
@@ -942,7 +955,7 @@ __global__ __launch_bounds__(256) void hcl_state_pair_kernel(
 #pragma unroll
     for (int i = 0; i < kHclHalf; ++i) {
       const int m = kHclHalf * half + i;
-      p[ch][i] = m < S ? poles[(c + ch) * S + m] : 0.0F;
+      p[ch][i] = m < S ? poles[(c + (ch ^ half)) * S + m] : 0.0F;
       st[ch][i] = 0.0F;
     }
   const uint32_t row_bytes = static_cast<uint32_t>(3 * W * sizeof(T));
@@ -966,8 +979,8 @@ __global__ __launch_bounds__(256) void hcl_state_pair_kernel(
     for (int b = 0; b < kHclBatch; ++b) {
       if (base + b >= rows)
         break;
-      float x2[2], u[2];
-      sh.step(cur[b], x2, u);
+      float x2, u[2];
+      sh.step(cur[b], x2, u[0], u[1]);
 #pragma unroll
       for (int ch = 0; ch < 2; ++ch)
 #pragma unroll
@@ -980,7 +993,7 @@ __global__ __launch_bounds__(256) void hcl_state_pair_kernel(
     const int m = kHclHalf * half + i;
     if (m < S)
       *reinterpret_cast<float2 *>(&chunk_state[(g * S + m) * W + c]) =
-          make_float2(st[0][i], st[1][i]);
+          half == 0 ? make_float2(st[0][i], st[1][i]) : make_float2(st[1][i], st[0][i]);
   }
 }
 
@@ -1103,14 +1116,15 @@ __global__ __launch_bounds__(256) void hcl_output_pair_kernel(
   float p[2][kHclHalf], r[2][kHclHalf], st[2][kHclHalf], d[2];
 #pragma unroll
   for (int ch = 0; ch < 2; ++ch) {
+    const size_t cc = c + (ch ^ half);
 #pragma unroll
     for (int i = 0; i < kHclHalf; ++i) {
       const int m = kHclHalf * half + i;
-      p[ch][i] = m < S ? poles[(c + ch) * S + m] : 0.0F;
-      r[ch][i] = m < S ? residues[(c + ch) * S + m] : 0.0F;
-      st[ch][i] = m < S ? chunk_state[(g * S + m) * W + c + ch] : 0.0F;
+      p[ch][i] = m < S ? poles[cc * S + m] : 0.0F;
+      r[ch][i] = m < S ? residues[cc * S + m] : 0.0F;
+      st[ch][i] = m < S ? chunk_state[(g * S + m) * W + cc] : 0.0F;
     }
-    d[ch] = direct[c + ch];
+    d[ch] = direct[cc];
   }
   const uint32_t row_bytes = static_cast<uint32_t>(3 * W * sizeof(T));
   const auto in = buffer_resource(P + t0 * 3 * W, rows * row_bytes);
@@ -1134,23 +1148,26 @@ __global__ __launch_bounds__(256) void hcl_output_pair_kernel(
     }
 #pragma unroll
     for (int b = 0; b < kHclBatch; ++b) {
-      float x2[2], u[2], y[2];
-      sh.step(cur[b], x2, u);
+      float x2, u[2], modal[2];
+      sh.step(cur[b], x2, u[0], u[1]);
 #pragma unroll
       for (int ch = 0; ch < 2; ++ch) {
-        float modal = 0.0F;
+        modal[ch] = 0.0F;
 #pragma unroll
         for (int i = 0; i < kHclHalf; ++i) {
           st[ch][i] = p[ch][i] * st[ch][i] + u[ch];
-          modal += r[ch][i] * st[ch][i];
+          modal[ch] += r[ch][i] * st[ch][i];
         }
-        // States 0..7 first, then 8..15, in both lanes of the pair.
-        const float other = swap_pair(modal);
-        const float total = half == 0 ? modal + other : other + modal;
-        y[ch] = x2[ch] * (total + d[ch] * u[ch]);
       }
+      // The partner's partial sum of the own channel; states 0..7 first,
+      // then 8..15.
+      const float partner = swap_pair(modal[1]);
+      const float total = half == 0 ? modal[0] + partner : partner + modal[0];
+      const float y = x2 * (total + d[0] * u[0]);
+      const float y_other = swap_pair(y);
       // Rows past the chunk end are dropped by the store bound.
-      sink.put(half, out_lane, (base + b) * out_row, y[0], y[1]);
+      sink.put(half, out_lane, (base + b) * out_row, half == 0 ? y : y_other,
+               half == 0 ? y_other : y);
     }
   }
 }
