@@ -683,6 +683,22 @@ evo_status evo_hip_linear(const uint16_t *x_hi, const uint16_t *x_lo, const uint
   });
 }
 
+evo_status evo_hip_linear_split(const uint16_t *x_hi, const uint16_t *x_lo, const uint16_t *w,
+                                const uint16_t *bias, const float *residual, size_t m,
+                                size_t n, size_t k, float *out, float *workspace,
+                                size_t workspace_bytes, void *stream) {
+  return protect([&]() -> evo_status {
+    const evo::hip::GemmEpilogue mode =
+        bias != nullptr ? (residual != nullptr ? evo::hip::kGemmBiasResidual : evo::hip::kGemmBias)
+                        : (residual != nullptr ? evo::hip::kGemmResidual : evo::hip::kGemmStore);
+    return publish(evo::hip::gemm_bf16w(evo::hip::Activation{x_hi, x_lo, k}, w,
+                                        evo::hip::GemmOutput{out, nullptr, nullptr, n}, m, n,
+                                        k, mode, bias, residual, false, 0,
+                                        static_cast<hipStream_t>(stream), workspace,
+                                        workspace_bytes));
+  });
+}
+
 evo_status evo_hip_pack_mlp(const uint16_t *l1, const uint16_t *l2, size_t inner,
                             size_t width, uint16_t *w12, void *stream) {
   return protect([&]() -> evo_status {

@@ -216,12 +216,22 @@ __device__ inline int swizzled_unit(int row, int seg) {
   return row * 4 + (seg ^ ((row >> 2) & 3));
 }
 
+// Split K: block row blockIdx.y multiplies K range [y K, (y + 1) K) (K is
+// the per-split length, ldw the weight row stride) into C + y c_split.
 template <bool kSplit>
 __global__ __launch_bounds__(512) void gemm_kernel(
     const uint16_t *__restrict__ a_hi, const uint16_t *__restrict__ a_lo, int lda,
-    const uint16_t *__restrict__ W, int M, int N, int K, float *__restrict__ C,
-    uint16_t *__restrict__ c_hi, uint16_t *__restrict__ c_lo, int ldc,
+    const uint16_t *__restrict__ W, int ldw, int M, int N, int K, float *__restrict__ C,
+    size_t c_split, uint16_t *__restrict__ c_hi, uint16_t *__restrict__ c_lo, int ldc,
     const Epilogue epi) {
+  {
+    const size_t k_first = static_cast<size_t>(blockIdx.y) * K;
+    a_hi += k_first;
+    if (kSplit)
+      a_lo += k_first;
+    W += k_first;
+    C += blockIdx.y * c_split;
+  }
   constexpr int kPlanes = kSplit ? 3 : 2;  // A hi, (A lo), W
   constexpr int kStage = kPlanes * kPlane;
   __shared__ __attribute__((aligned(16))) uint16_t lds[kStages * kStage];
@@ -246,7 +256,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(
     const int ar = min(block_m + r, M - 1), wr = min(block_n + r, N - 1);
     src_a_hi[i] = a_hi + static_cast<size_t>(ar) * lda + seg * 8;
     src_a_lo[i] = kSplit ? a_lo + static_cast<size_t>(ar) * lda + seg * 8 : nullptr;
-    src_w[i] = W + static_cast<size_t>(wr) * K + seg * 8;
+    src_w[i] = W + static_cast<size_t>(wr) * ldw + seg * 8;
   }
   auto issue = [&](int step) {
     uint16_t *stage = lds + (step % kStages) * kStage;
@@ -531,6 +541,37 @@ __global__ void split_kernel(const float *__restrict__ x, size_t n,
   }
 }
 
+// Sum of the split-K partials in split order, then the epilogue:
+// C[m, n] = sum_s part[s][m, n] (+ bias[n]) (+ residual[m, n]). Four columns
+// per thread (N % 4 == 0).
+__global__ void split_k_reduce_kernel(const float *__restrict__ part, int splits, int M, int N,
+                                      float *__restrict__ C, int ldc, const Epilogue epi) {
+  const size_t quads = static_cast<size_t>(M) * (N / 4);
+  const size_t plane = static_cast<size_t>(M) * N;
+  for (size_t q = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; q < quads;
+       q += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    const size_t m = q / (N / 4);
+    const int n = static_cast<int>(q % (N / 4)) * 4;
+    f32x4 acc = *reinterpret_cast<const f32x4 *>(part + m * N + n);
+    for (int sp = 1; sp < splits; ++sp) {
+      const f32x4 v = *reinterpret_cast<const f32x4 *>(part + sp * plane + m * N + n);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        acc[e] = acc[e] + v[e];
+    }
+    const size_t index = m * ldc + n;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float value = acc[e];
+      if (epi.mode == kGemmBias || epi.mode == kGemmBiasResidual)
+        value = value + bf16_to_f32(epi.bias[n + e]);
+      if (epi.mode == kGemmResidual || epi.mode == kGemmBiasResidual)
+        value = value + epi.residual[index + e];
+      C[index + e] = value;
+    }
+  }
+}
+
 }  // namespace
 
 Status split_planes(const float *x, size_t n, uint16_t *hi, uint16_t *lo,
@@ -545,7 +586,8 @@ Status split_planes(const float *x, size_t n, uint16_t *hi, uint16_t *lo,
 Status gemm_bf16w(const Activation &a, const uint16_t *W, const GemmOutput &out,
                   size_t M, size_t N, size_t K, GemmEpilogue mode,
                   const uint16_t *bias, const float *residual, bool gelu,
-                  size_t gated_width, hipStream_t stream) {
+                  size_t gated_width, hipStream_t stream, float *split_workspace,
+                  size_t split_workspace_bytes) {
   const bool split = a.lo != nullptr;
   if (a.hi == nullptr || W == nullptr || M == 0 || N == 0 || K == 0 || K % 8 != 0 ||
       a.ld < K || a.ld % 8 != 0 || M > (1U << 30) || N > (1U << 30) || K > (1U << 30))
@@ -582,12 +624,41 @@ Status gemm_bf16w(const Activation &a, const uint16_t *W, const GemmOutput &out,
     return launch_status("gemv_kernel");
   }
   if (K % kBK == 0) {
+    // Few tiles (short prompts against W-wide outputs): split K so that about
+    // one tile per CU runs, partials in the workspace, then one reduction.
+    int splits = 1;
+    if (mode != kGemmGated && split_workspace != nullptr && N % 4 == 0 && tiles < 128) {
+      for (int s = 2; s <= 16 && tiles * s <= 256; s *= 2)
+        if (K % (static_cast<size_t>(s) * kBK) == 0 && K / s >= 8 * kBK &&
+            static_cast<size_t>(s) * M * N * sizeof(float) <= split_workspace_bytes)
+          splits = s;
+    }
+    if (splits > 1) {
+      const Epilogue store{kGemmStore, nullptr, nullptr, 0, 0};
+      const dim3 split_grid(static_cast<unsigned>(tiles), static_cast<unsigned>(splits));
+      const int ks = k / splits;
+      const size_t plane = M * N;
+      if (split)
+        hipLaunchKernelGGL(gemm_kernel<true>, split_grid, dim3(512), 0, stream, a.hi, a.lo,
+                           lda, W, k, m, n, ks, split_workspace, plane, nullptr, nullptr, n,
+                           store);
+      else
+        hipLaunchKernelGGL(gemm_kernel<false>, split_grid, dim3(512), 0, stream, a.hi, a.lo,
+                           lda, W, k, m, n, ks, split_workspace, plane, nullptr, nullptr, n,
+                           store);
+      EVO_TRY(launch_status("gemm_kernel (split K)"));
+      const size_t quads = plane / 4;
+      const unsigned blocks = static_cast<unsigned>(std::min<size_t>((quads + 255) / 256, 8192));
+      hipLaunchKernelGGL(split_k_reduce_kernel, dim3(blocks), dim3(256), 0, stream,
+                         split_workspace, splits, m, n, out.f32, ldc, epi);
+      return launch_status("split_k_reduce_kernel");
+    }
     if (split)
       hipLaunchKernelGGL(gemm_kernel<true>, grid, dim3(512), 0, stream, a.hi, a.lo, lda,
-                         W, m, n, k, out.f32, out.hi, out.lo, ldc, epi);
+                         W, k, m, n, k, out.f32, size_t{0}, out.hi, out.lo, ldc, epi);
     else
       hipLaunchKernelGGL(gemm_kernel<false>, grid, dim3(512), 0, stream, a.hi, a.lo, lda,
-                         W, m, n, k, out.f32, out.hi, out.lo, ldc, epi);
+                         W, k, m, n, k, out.f32, size_t{0}, out.hi, out.lo, ldc, epi);
     return launch_status("gemm_kernel");
   }
   if (split)

@@ -13,6 +13,9 @@ namespace {
 
 constexpr size_t kArenaRows = 8192;  // activation rows per prefill chunk
 constexpr float kFp8InputAmax = 8.0F;  // activation amax of load-time FP8 conversion
+// Split-K partials of short-prompt GEMMs (splits x rows x N F32; the split
+// count is capped so that it fits).
+constexpr size_t kSplitWorkspaceBytes = size_t{64} << 20;
 
 Status hip_check(hipError_t error, const std::string &what) {
   if (error == hipSuccess)
@@ -359,9 +362,12 @@ Status Context::initialize(std::shared_ptr<const Model> model, size_t capacity,
   EVO_TRY(hip_check(hipMemsetAsync(flag_.as<void>(), 0, sizeof(int), stream_), "flag reset"));
   EVO_TRY(hip_check(hipHostMalloc(reinterpret_cast<void **>(&host_flag_), sizeof(int),
                                   hipHostMallocDefault), "pinned flag"));
+  // Shared by the Hyena operators (chunk states, Toeplitz tables) and the
+  // split-K partials of short-prompt GEMMs, which run after them.
   workspace_bytes_ = std::max({hyena_workspace_bytes(kHyenaHcl, R, w, c.state),
                                hyena_workspace_bytes(kHyenaHcs, R, w, c.state),
-                               hyena_workspace_bytes(kHyenaHcm, R, w, c.state)});
+                               hyena_workspace_bytes(kHyenaHcm, R, w, c.state),
+                               kSplitWorkspaceBytes});
   EVO_TRY(workspace_.allocate(std::max<size_t>(workspace_bytes_, 256), "hyena workspace"));
   EVO_TRY(hip_check(hipHostMalloc(reinterpret_cast<void **>(&host_logits_),
                                   R * std::max(c.vocab, w) * 4, hipHostMallocDefault),
@@ -487,7 +493,7 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
     EVO_TRY(gemm_bf16w(mixed, L.out_weight.as<uint16_t>(),
                        GemmOutput{residual, nullptr, nullptr, w}, rows, w, w,
                        kGemmBiasResidual, L.out_bias.as<uint16_t>(), hidden, false, 0,
-                       stream_));
+                       stream_, workspace_.as<float>(), workspace_.bytes()));
     EVO_TRY(rms_norm(residual, rows, w, L.post_norm.as<float>(), c.eps, nullptr, normed_hi,
                      split ? normed_lo : nullptr, stream_));
     // gated = act(l1 x) * (l2 x), act = erf-GELU in block 0 only (`:650-667`)
@@ -497,7 +503,8 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
                        c.inner, stream_));
     // hidden = gated . l3^T + residual
     EVO_TRY(gemm_bf16w(gated, L.mlp_out.as<uint16_t>(), GemmOutput{hidden, nullptr, nullptr, w},
-                       rows, w, c.inner, kGemmResidual, nullptr, residual, false, 0, stream_));
+                       rows, w, c.inner, kGemmResidual, nullptr, residual, false, 0, stream_,
+                       workspace_.as<float>(), workspace_.bytes()));
     if (capture != nullptr && capture_layer == i)
       EVO_TRY(hip_check(hipMemcpyAsync(capture, hidden, rows * w * 4,
                                        hipMemcpyDeviceToHost, stream_),
@@ -534,7 +541,8 @@ Status Context::enqueue(const uint32_t *device_tokens, size_t rows, bool initial
                      c.eps, nullptr, hi, lo, stream_));
     EVO_TRY(gemm_bf16w(Activation{hi, lo, c.width}, model_->embedding.as<uint16_t>(),
                        GemmOutput{device_logits, nullptr, nullptr, c.vocab}, rows, c.vocab,
-                       c.width, kGemmStore, nullptr, nullptr, false, 0, stream_));
+                       c.width, kGemmStore, nullptr, nullptr, false, 0, stream_,
+                       workspace_.as<float>(), workspace_.bytes()));
   }
   position_ = initial ? rows : position_ + rows;
   return Status::Ok();

@@ -44,10 +44,13 @@ struct GemmOutput {
   size_t ld;
 };
 // C = A . W^T with W BF16 [N,K]; see gemm.hip.
+// With a split workspace (F32), launches with few output tiles (non-gated
+// modes) split K across blocks and sum the partials in split order.
 Status gemm_bf16w(const Activation &a, const uint16_t *W, const GemmOutput &out,
                   size_t M, size_t N, size_t K, GemmEpilogue mode,
                   const uint16_t *bias, const float *residual, bool gelu,
-                  size_t gated_width, hipStream_t stream);
+                  size_t gated_width, hipStream_t stream, float *split_workspace = nullptr,
+                  size_t split_workspace_bytes = 0);
 // hi[i] = bf16(x[i]), lo[i] = bf16(x[i] - hi[i]) (lo may be null).
 Status split_planes(const float *x, size_t n, uint16_t *hi, uint16_t *lo,
                     hipStream_t stream);

@@ -36,6 +36,8 @@ _OPS = {
     "evo_hip_split_f32": (c_int, [c_void, c_size, c_void, c_void, c_void]),
     "evo_hip_linear": (c_int, [c_void, c_void, c_void, c_void, c_void, c_size, c_size,
                                c_size, c_void, c_void]),
+    "evo_hip_linear_split": (c_int, [c_void, c_void, c_void, c_void, c_void, c_size, c_size,
+                                     c_size, c_void, c_void, c_size, c_void]),
     "evo_hip_pack_mlp": (c_int, [c_void, c_void, c_size, c_size, c_void, c_void]),
     "evo_hip_gated_mlp": (c_int, [c_void, c_void, c_void, c_void, c_size, c_size, c_size,
                                   c_int, c_void, c_void, c_void, c_void]),

@@ -163,6 +163,37 @@ def test_linear_split_matches_oracle(m, n, k, bias, residual):
     assert rel_err(host(out), expected) < 2e-5
 
 
+@pytest.mark.parametrize("m,n,k", [(256, 512, 1920), (300, 1000, 2048), (5, 64, 512),
+                                   (1024, 4096, 11264)])
+@pytest.mark.parametrize("bias,residual", [(False, False), (True, True), (False, True)])
+def test_linear_split_k_matches_oracle(m, n, k, bias, residual):
+    """Few-tile launches split K over blocks (2-16 splits on these shapes) and
+    sum the partials in split order before the epilogue: the result is the
+    unsplit product up to the F32 summation order, and matches the oracle."""
+    r = rng(m + n + k + 7)
+    x = r.standard_normal((m, k)).astype(np.float32)
+    w = bf16_bits(r.standard_normal((n, k)).astype(np.float32) / np.sqrt(k))
+    b = bf16_bits(r.standard_normal(n).astype(np.float32) * 0.1) if bias else None
+    res = r.standard_normal((m, n)).astype(np.float32) if residual else None
+    hi, lo = split_gpu(x)
+    args = (p(hi), p(lo), p(dev(w)), p(dev(b) if bias else None),
+            p(dev(res) if residual else None), m, n, k)
+    unsplit, parted = empty((m, n)), empty((m, n))
+    N.call("evo_hip_linear", *args, p(unsplit), stream())
+    workspace = empty((16 * m * n,))
+    N.call("evo_hip_linear_split", *args, p(parted), p(workspace), 16 * m * n * 4, stream())
+    assert rel_err(host(parted), host(unsplit)) < 1e-5  # ~sqrt(K) F32 ulps
+    if m * n * k <= 1 << 31:
+        expected = O.linear_bf16w(x, w, b)
+        if residual:
+            expected = expected + res
+        assert rel_err(host(parted), expected) < 2e-5
+    # A workspace too small for any split runs the unsplit kernel.
+    tiny = empty((m * n,))
+    N.call("evo_hip_linear_split", *args, p(parted), p(tiny), m * n * 4, stream())
+    assert np.array_equal(host(parted), host(unsplit))
+
+
 def split_gpu(x):
     hi, lo = empty(x.shape, np.uint16), empty(x.shape, np.uint16)
     N.call("evo_hip_split_f32", p(dev(x)), x.size, p(hi), p(lo), stream())
