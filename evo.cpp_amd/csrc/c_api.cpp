@@ -132,17 +132,21 @@ evo_status run_prefill(evo_context *context, const evo_batch *batch,
   const size_t chunk = context->hip->activation_capacity();
   const bool capture = capture_layer != std::numeric_limits<size_t>::max();
   const size_t columns = capture ? config.width : config.vocab;
-  std::vector<float> output(std::min(chunk, tokens.size()) * columns);
+  // Logits are handed to the callback straight from the context's pinned
+  // staging buffer; captured hidden states go through a host vector.
+  std::vector<float> captured(capture ? std::min(chunk, tokens.size()) * columns : 0);
   size_t offset = 0;
   while (offset < tokens.size()) {
     const size_t rows = std::min(chunk, tokens.size() - offset);
-    const auto status = context->hip->forward(
-        tokens.data() + offset, rows, offset == 0, capture ? nullptr : output.data(),
-        capture ? capture_layer : std::numeric_limits<size_t>::max(),
-        capture ? output.data() : nullptr);
+    const float *values = captured.data();
+    const auto status =
+        capture ? context->hip->forward(tokens.data() + offset, rows, offset == 0, nullptr,
+                                        capture_layer, captured.data())
+                : context->hip->forward_view(tokens.data() + offset, rows, offset == 0,
+                                             &values);
     if (!status.ok())
       return publish(status);
-    const evo_status callback = sink(output.data(), rows, columns, offset);
+    const evo_status callback = sink(values, rows, columns, offset);
     if (callback != EVO_STATUS_OK)
       return publish(valid_status(callback) ? callback : EVO_STATUS_INTERNAL,
                      "callback: consumer aborted HIP prefill");

@@ -576,8 +576,19 @@ Status Context::forward(const uint32_t *tokens, size_t rows, bool initial,
     EVO_TRY(hip_check(hipMemcpyAsync(host_logits_, logits_.as<void>(), rows * c.vocab * 4,
                                      hipMemcpyDeviceToHost, stream_), "logits download"));
   EVO_TRY(finish());
-  if (logits != nullptr)
+  if (logits != nullptr && logits != host_logits_)
     std::memcpy(logits, host_logits_, rows * c.vocab * 4);
+  return Status::Ok();
+}
+
+Status Context::forward_view(const uint32_t *tokens, size_t rows, bool initial,
+                             const float **logits) {
+  if (logits == nullptr)
+    return {ErrorCode::kInvalidArgument, "invalid_argument: forward arguments are invalid"};
+  // host_logits_ as the destination: the copy onto itself is skipped.
+  EVO_TRY(forward(tokens, rows, initial, host_logits_, std::numeric_limits<size_t>::max(),
+                  nullptr));
+  *logits = host_logits_;
   return Status::Ok();
 }
 

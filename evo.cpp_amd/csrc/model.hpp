@@ -115,6 +115,10 @@ public:
   // state after block capture_layer) receive the outputs.
   Status forward(const uint32_t *tokens, size_t rows, bool initial,
                  float *logits, size_t capture_layer, float *capture);
+  // forward() with logits left in the context's pinned staging buffer:
+  // *logits points at [rows, vocab] F32 there until the next call.
+  Status forward_view(const uint32_t *tokens, size_t rows, bool initial,
+                      const float **logits);
   // Whole-sequence prefill with tokens and logits ([count, vocab] F32) in
   // device memory: chunks are enqueued back to back on the context stream,
   // one synchronisation at the end, no host transfer of activations.
