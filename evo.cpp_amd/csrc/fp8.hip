@@ -22,6 +22,8 @@
 //    inside a chunk is not reproduced, so results differ from exact mode by
 //    a few E8M13 ulps.
 // All modes finish with bf16(acc * output_scale).
+#include <type_traits>
+
 #include "common.hpp"
 #include "ops.hpp"
 
@@ -319,7 +321,7 @@ __device__ inline void decode16(const uint4 codes, float (&out)[16]) {
   }
 }
 
-template <int kChunk, typename Out>
+template <int kChunk, int kM, typename Out>
 __global__ __launch_bounds__(256) void fp8_gemv_kernel(
     const uint8_t *__restrict__ a, const uint8_t *__restrict__ w, Out *__restrict__ out,
     int M, int N, int K, float output_scale) {
@@ -330,28 +332,32 @@ __global__ __launch_bounds__(256) void fp8_gemv_kernel(
   const int chunks = K / kChunk;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int row0 = blockIdx.x * kGemv8Rows + wave * kRowsPerWave;
-  for (int k = lane * 16; k < K; k += 1024) {
-    float av[kGemv8MaxM][16];
-#pragma unroll
-    for (int m = 0; m < kGemv8MaxM; ++m) {
-      if (m >= M)
-        break;
-      decode16(*reinterpret_cast<const uint4 *>(a + static_cast<size_t>(m) * K + k), av[m]);
-    }
-    uint4 codes[kRowsPerWave];
+  // The codes of the next 1024-K sweep load before this sweep is multiplied.
+  auto load_codes = [&](int k, uint4 (&codes)[kRowsPerWave]) {
 #pragma unroll
     for (int r = 0; r < kRowsPerWave; ++r)
       codes[r] = row0 + r < N ? *reinterpret_cast<const uint4 *>(
                                     w + static_cast<size_t>(row0 + r) * K + k)
                               : make_uint4(0, 0, 0, 0);
+  };
+  int k = lane * 16;
+  uint4 codes[kRowsPerWave];
+  if (k < K)
+    load_codes(k, codes);
+  for (; k < K; k += 1024) {
+    uint4 next[kRowsPerWave];
+    if (k + 1024 < K)
+      load_codes(k + 1024, next);
+    float av[kM][16];
+#pragma unroll
+    for (int m = 0; m < kM; ++m)
+      decode16(*reinterpret_cast<const uint4 *>(a + static_cast<size_t>(m) * K + k), av[m]);
 #pragma unroll
     for (int r = 0; r < kRowsPerWave; ++r) {
       float wv[16];
       decode16(codes[r], wv);
 #pragma unroll
-      for (int m = 0; m < kGemv8MaxM; ++m) {
-        if (m >= M)
-          break;
+      for (int m = 0; m < kM; ++m) {
         float sum = 0.0F;
 #pragma unroll
         for (int e = 0; e < 16; ++e)
@@ -363,6 +369,9 @@ __global__ __launch_bounds__(256) void fp8_gemv_kernel(
           chunk_s[((wave * kRowsPerWave + r) * M + m) * chunks + k / kChunk] = sum;
       }
     }
+#pragma unroll
+    for (int r = 0; r < kRowsPerWave; ++r)
+      codes[r] = next[r];
   }
   __syncthreads();
   if (tid >= kGemv8Rows * kGemv8MaxM)
@@ -429,8 +438,14 @@ Status fp8_linear_impl(const uint8_t *in_codes, const uint8_t *w_codes, Out *out
     const dim3 grid(static_cast<unsigned>(ceil_div(N, kGemv8Rows)));
     const int chunk = mode == kFp8MfmaK32 ? 32 : 128;
     const size_t lds = kGemv8Rows * M * (K / chunk) * sizeof(float);
-    const auto kernel = mode == kFp8MfmaK32 ? fp8_gemv_kernel<32, Out>
-                                            : fp8_gemv_kernel<128, Out>;
+    auto pick = [&](auto rows_c) {
+      constexpr int kM = decltype(rows_c)::value;
+      return mode == kFp8MfmaK32 ? fp8_gemv_kernel<32, kM, Out> : fp8_gemv_kernel<128, kM, Out>;
+    };
+    const auto kernel = M == 1   ? pick(std::integral_constant<int, 1>{})
+                        : M == 2 ? pick(std::integral_constant<int, 2>{})
+                        : M == 3 ? pick(std::integral_constant<int, 3>{})
+                                 : pick(std::integral_constant<int, 4>{});
     if (lds > 64 * 1024)
       EVO_TRY(hip_status(hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
                                              hipFuncAttributeMaxDynamicSharedMemorySize,

@@ -22,6 +22,8 @@
 // 128 x 128 with register-staged, padded LDS rows.
 // Tiles are renumbered so that each of the 8 XCDs (own L2) receives a
 // contiguous band of the tile grid, walked in groups of 8 tile-rows.
+#include <type_traits>
+
 #include "common.hpp"
 #include "ops.hpp"
 
@@ -417,7 +419,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(
 constexpr int kGemvRows = 8;
 constexpr int kGemvMaxM = 4;
 
-template <bool kSplit>
+template <bool kSplit, int kM>
 __global__ __launch_bounds__(256) void gemv_kernel(
     const uint16_t *__restrict__ a_hi, const uint16_t *__restrict__ a_lo, int lda,
     const uint16_t *__restrict__ W, int M, int N, int K, float *__restrict__ C,
@@ -437,18 +439,32 @@ __global__ __launch_bounds__(256) void gemv_kernel(
       rows[r] = unit * kGemvRows + r;
     }
   }
-  float acc[kGemvRows][kGemvMaxM];
+  float acc[kGemvRows][kM];
 #pragma unroll
   for (int r = 0; r < kGemvRows; ++r)
 #pragma unroll
-    for (int m = 0; m < kGemvMaxM; ++m)
+    for (int m = 0; m < kM; ++m)
       acc[r][m] = 0.0F;
-  for (int k = wave * 512 + lane * 8; k < K; k += 2048) {
-    float x[kGemvMaxM][8];
+  // The weights of the wave's next K chunk are loaded before the current
+  // chunk is multiplied, so two chunks (16 KB per wave) are in flight.
+  auto load_w = [&](int k, uint4 (&wv)[kGemvRows]) {
 #pragma unroll
-    for (int m = 0; m < kGemvMaxM; ++m) {
-      if (m >= M)
-        break;
+    for (int r = 0; r < kGemvRows; ++r)
+      wv[r] = rows[r] < N ? *reinterpret_cast<const uint4 *>(
+                                W + static_cast<size_t>(rows[r]) * K + k)
+                          : make_uint4(0, 0, 0, 0);
+  };
+  int k = wave * 512 + lane * 8;
+  uint4 wv[kGemvRows];
+  if (k < K)
+    load_w(k, wv);
+  for (; k < K; k += 2048) {
+    uint4 wn[kGemvRows];
+    if (k + 2048 < K)
+      load_w(k + 2048, wn);
+    float x[kM][8];
+#pragma unroll
+    for (int m = 0; m < kM; ++m) {
       const uint4 h = *reinterpret_cast<const uint4 *>(a_hi + static_cast<size_t>(m) * lda + k);
       const uint16_t *hs = reinterpret_cast<const uint16_t *>(&h);
       uint4 l = make_uint4(0, 0, 0, 0);
@@ -459,29 +475,23 @@ __global__ __launch_bounds__(256) void gemv_kernel(
       for (int e = 0; e < 8; ++e)
         x[m][e] = bf16_to_f32(hs[e]) + (kSplit ? bf16_to_f32(ls[e]) : 0.0F);
     }
-    uint4 wv[kGemvRows];
-#pragma unroll
-    for (int r = 0; r < kGemvRows; ++r)
-      wv[r] = rows[r] < N ? *reinterpret_cast<const uint4 *>(
-                                W + static_cast<size_t>(rows[r]) * K + k)
-                          : make_uint4(0, 0, 0, 0);
 #pragma unroll
     for (int r = 0; r < kGemvRows; ++r) {
       const uint16_t *ws = reinterpret_cast<const uint16_t *>(&wv[r]);
 #pragma unroll
-      for (int m = 0; m < kGemvMaxM; ++m) {
-        if (m >= M)
-          break;
+      for (int m = 0; m < kM; ++m)
 #pragma unroll
         for (int e = 0; e < 8; ++e)
           acc[r][m] = fmaf(x[m][e], bf16_to_f32(ws[e]), acc[r][m]);
-      }
     }
+#pragma unroll
+    for (int r = 0; r < kGemvRows; ++r)
+      wv[r] = wn[r];
   }
 #pragma unroll
   for (int r = 0; r < kGemvRows; ++r)
 #pragma unroll
-    for (int m = 0; m < kGemvMaxM; ++m) {
+    for (int m = 0; m < kM; ++m) {
       float v = acc[r][m];
 #pragma unroll
       for (int offset = 32; offset > 0; offset >>= 1)
@@ -490,11 +500,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(
         partial[wave][r][m] = v;
     }
   __syncthreads();
-  if (wave != 0 || lane >= kGemvMaxM)
+  if (wave != 0 || lane >= kM)
     return;
   const int m = lane;
-  if (m >= M)
-    return;
   float total[kGemvRows];
 #pragma unroll
   for (int r = 0; r < kGemvRows; ++r)
@@ -615,12 +623,21 @@ Status gemm_bf16w(const Activation &a, const uint16_t *W, const GemmOutput &out,
   const int lda = static_cast<int>(a.ld), ldc = static_cast<int>(out.ld);
   if (M <= static_cast<size_t>(kGemvMaxM)) {
     const dim3 gemv_grid(static_cast<unsigned>(ceil_div(N, kGemvRows)));
-    if (split)
-      hipLaunchKernelGGL(gemv_kernel<true>, gemv_grid, dim3(256), 0, stream, a.hi, a.lo, lda,
-                         W, m, n, k, out.f32, out.hi, out.lo, ldc, epi);
-    else
-      hipLaunchKernelGGL(gemv_kernel<false>, gemv_grid, dim3(256), 0, stream, a.hi, a.lo,
-                         lda, W, m, n, k, out.f32, out.hi, out.lo, ldc, epi);
+    auto launch = [&](auto rows_c) {
+      constexpr int kM = decltype(rows_c)::value;
+      if (split)
+        hipLaunchKernelGGL((gemv_kernel<true, kM>), gemv_grid, dim3(256), 0, stream, a.hi,
+                           a.lo, lda, W, m, n, k, out.f32, out.hi, out.lo, ldc, epi);
+      else
+        hipLaunchKernelGGL((gemv_kernel<false, kM>), gemv_grid, dim3(256), 0, stream, a.hi,
+                           a.lo, lda, W, m, n, k, out.f32, out.hi, out.lo, ldc, epi);
+    };
+    switch (M) {
+      case 1: launch(std::integral_constant<int, 1>{}); break;
+      case 2: launch(std::integral_constant<int, 2>{}); break;
+      case 3: launch(std::integral_constant<int, 3>{}); break;
+      default: launch(std::integral_constant<int, 4>{}); break;
+    }
     return launch_status("gemv_kernel");
   }
   if (K % kBK == 0) {

@@ -126,7 +126,7 @@ class Model:
     def close(self) -> None:
         if self.handle:
             self.library.lib.evo_model_free(self.handle)
-            self.handle = ctypes.c_void_p()
+            self.handle = None
 
     __del__ = close
 
@@ -155,7 +155,7 @@ class Context:
     def close(self) -> None:
         if self.handle:
             self.model.library.lib.evo_context_free(self.handle)
-            self.handle = ctypes.c_void_p()
+            self.handle = None
 
     __del__ = close
 
