@@ -1,5 +1,5 @@
 // SPDX-License-Identifier: Apache-2.0
-// Attention block of StripedHyena2 on gfx950 (prefill).
+// Attention block of StripedHyena2 on gfx950 (prefill; single-query decode).
 //
 // qkv_rope: splits the Wqkv projection (head-major `column_split` layout
 // [h][q,k,v][d], or component-major [q,k,v][h][d]), applies GPT-NeoX
@@ -432,6 +432,146 @@ Status launch_flash(const uint16_t *q, size_t q_plane, const uint16_t *k_cache,
   return launch_status("flash_attention_kernel");
 }
 
+
+// ---- Single-query (decode) attention, split over the keys: one block per
+// (head, chunk of 256 keys). Each lane scores one key (F32 dot of q with
+// the key's hi + lo planes), the block takes its max and exponentials, and
+// 256 threads form the chunk's P V with thread t on dimension t / 2 and
+// keys of half t % 2 (reading the transposed value cache row of that
+// dimension; its 16-key permutation swaps position bits 2 and 3, so column c
+// holds key vt_column(c)). The chunk leaves (max, sum, o[d]); a second
+// kernel per head rescales the chunks to the common max and sums them in
+// chunk order. Full-softmax semantics as `src/cpu/model.cpp:510-544`.
+constexpr int kDecodeKeys = 256;
+
+template <int kD>
+__global__ __launch_bounds__(256) void decode_attention_kernel(
+    const uint16_t *__restrict__ q, size_t q_plane, const uint16_t *__restrict__ k_cache,
+    const uint16_t *__restrict__ v_cache, size_t cache_plane, size_t capacity,
+    size_t keys, size_t heads, float *__restrict__ part) {
+  __shared__ float q_s[kD];
+  __shared__ float p_s[kDecodeKeys];
+  __shared__ float red_s[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const size_t chunk = blockIdx.x, h = blockIdx.y;
+  const size_t width = heads * kD;
+  if (tid < kD)
+    q_s[tid] = get_split(q, q + q_plane, h * kD + tid);
+  __syncthreads();
+  const size_t key = chunk * kDecodeKeys + tid;
+  float score = -INFINITY;
+  if (key < keys) {
+    const uint16_t *k_hi = k_cache + key * width + h * kD;
+    const uint16_t *k_lo = k_hi + cache_plane;
+    float dot = 0.0F;
+#pragma unroll
+    for (int d0 = 0; d0 < kD; d0 += 8) {
+      const uint4 hv = *reinterpret_cast<const uint4 *>(k_hi + d0);
+      const uint4 lv = *reinterpret_cast<const uint4 *>(k_lo + d0);
+      const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w}, lw[4] = {lv.x, lv.y, lv.z, lv.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float k0 = __builtin_bit_cast(float, hw[i] << 16) +
+                         __builtin_bit_cast(float, lw[i] << 16);
+        const float k1 = __builtin_bit_cast(float, hw[i] & 0xffff0000U) +
+                         __builtin_bit_cast(float, lw[i] & 0xffff0000U);
+        dot = fmaf(q_s[d0 + 2 * i], k0, dot);
+        dot = fmaf(q_s[d0 + 2 * i + 1], k1, dot);
+      }
+    }
+    score = dot * (1.0F / sqrtf(static_cast<float>(kD)));
+  }
+  float m = score;
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1)
+    m = fmaxf(m, __shfl_xor(m, offset, 64));
+  if (lane == 0)
+    red_s[wave] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(red_s[0], red_s[1]), fmaxf(red_s[2], red_s[3]));
+  const float p = key < keys ? expf(score - m) : 0.0F;
+  p_s[tid] = p;
+  float l = p;
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1)
+    l += __shfl_xor(l, offset, 64);
+  __syncthreads();  // p_s complete; red_s reads done
+  if (lane == 0)
+    red_s[wave] = l;
+  // P V: thread t -> dimension t / 2 (t < 2 kD), keys of half t % 2.
+  float o = 0.0F;
+  const int d = tid >> 1, part_half = tid & 1;
+  if (d < kD) {
+    const size_t row = h * kD + d;
+    const size_t col0 = chunk * kDecodeKeys + part_half * (kDecodeKeys / 2);
+    const uint16_t *v_hi = v_cache + row * capacity + col0;
+    const uint16_t *v_lo = v_hi + cache_plane;
+    // Whole 16-column blocks: the permutation moves a key up to 8 columns
+    // past its position inside its block (key 84 of 85 sits in column 88).
+    const size_t end = min(static_cast<size_t>(kDecodeKeys / 2),
+                           keys > col0 ? (keys - col0 + 15) / 16 * 16 : size_t{0});
+    for (size_t c0 = 0; c0 < end; c0 += 8) {
+      const uint4 hv = *reinterpret_cast<const uint4 *>(v_hi + c0);
+      const uint4 lv = *reinterpret_cast<const uint4 *>(v_lo + c0);
+      const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w}, lw[4] = {lv.x, lv.y, lv.z, lv.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const size_t c = part_half * (kDecodeKeys / 2) + c0 + 2 * i;
+        const float v0 = __builtin_bit_cast(float, hw[i] << 16) +
+                         __builtin_bit_cast(float, lw[i] << 16);
+        const float v1 = __builtin_bit_cast(float, hw[i] & 0xffff0000U) +
+                         __builtin_bit_cast(float, lw[i] & 0xffff0000U);
+        // Zero weights are skipped: columns of keys past the end may hold
+        // unwritten cache.
+        const float p0 = p_s[vt_column(c)], p1 = p_s[vt_column(c + 1)];
+        if (p0 != 0.0F)
+          o = fmaf(p0, v0, o);
+        if (p1 != 0.0F)
+          o = fmaf(p1, v1, o);
+      }
+    }
+  }
+  o += __shfl_xor(o, 1, 64);
+  __syncthreads();
+  float *dst = part + (h * gridDim.x + chunk) * (kD + 2);
+  if (d < kD && part_half == 0)
+    dst[2 + d] = o;
+  if (tid == 0) {
+    dst[0] = m;
+    dst[1] = red_s[0] + red_s[1] + red_s[2] + red_s[3];
+  }
+}
+
+template <int kD, typename O>
+__global__ void decode_combine_kernel(const float *__restrict__ part, int chunks, O out) {
+  const size_t h = blockIdx.x;
+  const int d = threadIdx.x;
+  const float *base = part + h * chunks * (kD + 2);
+  float m = -INFINITY;
+  for (int c = 0; c < chunks; ++c)
+    m = fmaxf(m, base[c * (kD + 2)]);
+  float l = 0.0F, o = 0.0F;
+  for (int c = 0; c < chunks; ++c) {
+    const float scale = expf(base[c * (kD + 2)] - m);
+    l = fmaf(base[c * (kD + 2) + 1], scale, l);
+    o = fmaf(base[c * (kD + 2) + 2 + d], scale, o);
+  }
+  put(out, h * kD + d, o / l);
+}
+
+template <int kD, typename O>
+Status launch_decode(const uint16_t *q, size_t q_plane, const uint16_t *k_cache,
+                     const uint16_t *v_cache, size_t cache_plane, size_t capacity, size_t keys,
+                     size_t heads, float *workspace, O out, hipStream_t stream) {
+  const unsigned chunks = static_cast<unsigned>(ceil_div(keys, kDecodeKeys));
+  hipLaunchKernelGGL(decode_attention_kernel<kD>, dim3(chunks, heads), dim3(256), 0, stream, q,
+                     q_plane, k_cache, v_cache, cache_plane, capacity, keys, heads, workspace);
+  EVO_TRY(launch_status("decode_attention_kernel"));
+  hipLaunchKernelGGL((decode_combine_kernel<kD, O>), dim3(heads), dim3(kD), 0, stream,
+                     workspace, static_cast<int>(chunks), out);
+  return launch_status("decode_combine_kernel");
+}
+
 template <typename O>
 Status launch_attention(const uint16_t *q, size_t q_plane, const uint16_t *k_cache,
                         const uint16_t *v_cache, size_t cache_plane, size_t capacity,
@@ -486,12 +626,34 @@ Status causal_attention(const uint16_t *q, size_t q_plane, const uint16_t *k_cac
                         const uint16_t *v_cache, size_t cache_plane, size_t capacity,
                         size_t rows, size_t prefix, size_t heads, size_t head_dim,
                         float *out_f32, uint16_t *out_hi, uint16_t *out_lo,
-                        hipStream_t stream) {
+                        hipStream_t stream, float *workspace, size_t workspace_bytes) {
   if (q == nullptr || k_cache == nullptr || v_cache == nullptr ||
       (out_f32 == nullptr && out_hi == nullptr) || rows == 0 || heads == 0 ||
       heads > 65535 || q_plane < rows * heads * head_dim || capacity % kKeys != 0 ||
       prefix + rows > capacity || cache_plane < capacity * heads * head_dim)
     return {ErrorCode::kInvalidArgument, "causal_attention: invalid arguments"};
+  // One query with a workspace for the chunk partials: split over the keys.
+  const size_t keys = prefix + 1;
+  if (rows == 1 && workspace != nullptr &&
+      (head_dim == 32 || head_dim == 64 || head_dim == 128) &&
+      heads * ceil_div(keys, kDecodeKeys) * (head_dim + 2) * sizeof(float) <= workspace_bytes) {
+    auto run = [&](auto out) -> Status {
+      switch (head_dim) {
+      case 32:
+        return launch_decode<32>(q, q_plane, k_cache, v_cache, cache_plane, capacity, keys,
+                                 heads, workspace, out, stream);
+      case 64:
+        return launch_decode<64>(q, q_plane, k_cache, v_cache, cache_plane, capacity, keys,
+                                 heads, workspace, out, stream);
+      default:
+        return launch_decode<128>(q, q_plane, k_cache, v_cache, cache_plane, capacity, keys,
+                                  heads, workspace, out, stream);
+      }
+    };
+    if (out_f32 != nullptr)
+      return run(out_f32);
+    return run(SplitOut{out_hi, out_lo});
+  }
   if (out_f32 != nullptr)
     return launch_attention(q, q_plane, k_cache, v_cache, cache_plane, capacity, rows, prefix,
                             heads, head_dim, out_f32, stream);

@@ -775,6 +775,16 @@ evo_status evo_hip_attention(const float *projected, size_t rows, size_t width, 
                              size_t prefix, uint16_t *query, uint16_t *key_cache,
                              uint16_t *value_cache, size_t capacity, float *out,
                              void *stream) {
+  return evo_hip_attention_ws(projected, rows, width, heads, column_split, inv_freq, rope_scale,
+                              prefix, query, key_cache, value_cache, capacity, out, nullptr, 0,
+                              stream);
+}
+
+evo_status evo_hip_attention_ws(const float *projected, size_t rows, size_t width, size_t heads,
+                                int column_split, const float *inv_freq, float rope_scale,
+                                size_t prefix, uint16_t *query, uint16_t *key_cache,
+                                uint16_t *value_cache, size_t capacity, float *out,
+                                float *workspace, size_t workspace_bytes, void *stream) {
   return protect([&]() -> evo_status {
     const auto s = static_cast<hipStream_t>(stream);
     if (prefix + rows > capacity || capacity % 64 != 0)
@@ -789,7 +799,7 @@ evo_status evo_hip_attention(const float *projected, size_t rows, size_t width, 
     return publish(evo::hip::causal_attention(query, rows * width, key_cache, value_cache,
                                               capacity * width, capacity, rows, prefix, heads,
                                               heads == 0 ? 0 : width / heads, out, nullptr,
-                                              nullptr, s));
+                                              nullptr, s, workspace, workspace_bytes));
   });
 }
 

@@ -459,7 +459,7 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
                                k.values.as<uint16_t>(), cache_plane, cache_capacity_, rows,
                                position_,
                                c.heads, c.head_dim(), nullptr, mixed_out.hi, mixed_out.lo,
-                               stream_));
+                               stream_, workspace_.as<float>(), workspace_.bytes()));
     } else {
       HyenaWeights hw{};
       hw.short_filter = L.short_filter.as<uint16_t>();

@@ -141,6 +141,7 @@ Status causal_attention(const uint16_t *q, size_t q_plane, const uint16_t *k_cac
                         const uint16_t *v_cache, size_t cache_plane, size_t capacity,
                         size_t rows, size_t prefix, size_t heads, size_t head_dim,
                         float *out_f32, uint16_t *out_hi, uint16_t *out_lo,
-                        hipStream_t stream);
+                        hipStream_t stream, float *workspace = nullptr,
+                        size_t workspace_bytes = 0);
 
 }  // namespace evo::hip

@@ -48,6 +48,9 @@ _OPS = {
     "evo_hip_context_prefill_resident": (c_int, [c_void, c_void, c_size, c_void]),
     "evo_hip_attention": (c_int, [c_void, c_size, c_size, c_size, c_int, c_void, c_float,
                                   c_size, c_void, c_void, c_void, c_size, c_void, c_void]),
+    "evo_hip_attention_ws": (c_int, [c_void, c_size, c_size, c_size, c_int, c_void, c_float,
+                                     c_size, c_void, c_void, c_void, c_size, c_void, c_void,
+                                     c_size, c_void]),
 }
 
 

@@ -190,6 +190,19 @@ EVO_API evo_status evo_hip_attention(const float *projected, size_t rows,
                                      uint16_t *value_cache, size_t capacity,
                                      float *out, void *stream);
 
+/* evo_hip_attention with an F32 device workspace: a single query (rows == 1,
+ * head_dim 32/64/128) is then split over its keys in chunks of 256 (per
+ * chunk and head: max, sum and head_dim partial outputs in the workspace),
+ * the decode step's path. The same reference interface. */
+EVO_API evo_status evo_hip_attention_ws(const float *projected, size_t rows,
+                                        size_t width, size_t heads,
+                                        int column_split, const float *inv_freq,
+                                        float rope_scale, size_t prefix,
+                                        uint16_t *query, uint16_t *key_cache,
+                                        uint16_t *value_cache, size_t capacity,
+                                        float *out, float *workspace,
+                                        size_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -527,6 +527,46 @@ def test_attention_matches_oracle(oracle, rows, heads, head_dim, prefix):
     assert np.abs(stored - v_rows).max() <= 2.0 ** -16 * np.abs(v_rows).max()
 
 
+@pytest.mark.parametrize("heads,head_dim,prefix", [(2, 128, 0), (2, 128, 255), (2, 128, 256),
+                                                  (2, 128, 1000), (4, 64, 3000), (3, 32, 77),
+                                                  (2, 32, 84), (2, 128, 1003), (1, 64, 92)])
+def test_single_query_attention_split_over_keys(oracle, heads, head_dim, prefix):
+    """One query (the decode step) with a workspace: keys split in chunks of
+    256 and the chunk partials combined; against the oracle and the same
+    call without a workspace (MFMA flash kernel)."""
+    r = rng(prefix + heads + head_dim)
+    width = heads * head_dim
+    total = prefix + 1
+    proj = r.standard_normal((total, 3 * width)).astype(np.float32)
+    inv_freq = (1.0 / 10000 ** (np.arange(0, head_dim, 2) / head_dim)).astype(np.float32)
+    qkv = proj.reshape(total, heads, 3, head_dim)
+    q = np.ascontiguousarray(qkv[:, :, 0]).reshape(total * heads * head_dim)
+    k = np.ascontiguousarray(qkv[:, :, 1]).reshape(total * heads * head_dim)
+    v = np.ascontiguousarray(qkv[:, :, 2]).reshape(total * heads * head_dim)
+    O.check(oracle.oracle_apply_rope(O.ptr(q), O.ptr(k), total, heads, head_dim,
+                                     O.ptr(inv_freq), 0, 8.0))
+    expected = np.zeros_like(q)
+    O.check(oracle.oracle_causal_attention(O.ptr(q), O.ptr(k), O.ptr(v), total, heads,
+                                           head_dim, O.ptr(expected)))
+    expected = expected.reshape(total, width)[prefix:]
+    capacity = (total + 63) // 64 * 64
+    results = []
+    for workspace_floats in (heads * ((total + 255) // 256) * (head_dim + 2), 0):
+        kc, vc = zeros((2, capacity, width), np.uint16), zeros((2, width, capacity), np.uint16)
+        query, out = empty((2, total, width), np.uint16), empty((total, width))
+        if prefix:
+            N.call("evo_hip_attention", p(dev(proj[:prefix])), prefix, width, heads, 1,
+                   p(dev(inv_freq)), 8.0, 0, p(query), p(kc), p(vc), capacity, p(out),
+                   stream())
+        workspace = empty((max(workspace_floats, 1),))
+        N.call("evo_hip_attention_ws", p(dev(proj[prefix:])), 1, width, heads, 1,
+               p(dev(inv_freq)), 8.0, prefix, p(query), p(kc), p(vc), capacity, p(out),
+               p(workspace), workspace_floats * 4, stream())
+        results.append(host(out)[:1].copy())
+    assert rel_err(results[0], expected) < 1e-5
+    assert rel_err(results[0], results[1]) < 1e-5
+
+
 def test_attention_rejects_unaligned_capacity():
     width, heads = 64, 2
     proj = zeros((4, 3 * width))
