@@ -1688,6 +1688,104 @@ __global__ void short_history_kernel(const T *__restrict__ P, size_t L,
   }
 }
 
+
+// ---- One-row continuation (the decode step) of the whole operator in one
+// launch. A block of 256 threads owns 64 channels; thread (g, lane) of
+// channel lane reads history rows g, g + 4, ... (each row once) into
+// registers, adds its share of the inner FIR (HCS / HCM), and after a
+// barrier writes them one row down (the new u goes to the last row); the
+// four partial sums meet in LDS and group 0 finishes the channel: short FIR
+// and gates from the short history and the projection row, the modal
+// recurrence instead for HCL (state updated in place), the outer gate, and
+// the projection row appended to the short history. Sums as in
+// hyena_fir_kernel except that the history part is added per row group
+// (groups 0..3 in order).
+constexpr int kDecodeRowsPerThread = 32;  // ceil(127 / 4)
+
+template <typename T, typename O>
+__global__ __launch_bounds__(256) void hyena_decode_kernel(
+    int kind, const T *__restrict__ P, float *__restrict__ short_history,
+    const uint16_t *__restrict__ short_filter, int short_len, float *__restrict__ inner_history,
+    const float *__restrict__ filter, size_t groups, int k, int causal,
+    const float *__restrict__ direct, const float *__restrict__ poles,
+    const float *__restrict__ residues, float *__restrict__ modal_state, int S, size_t W,
+    O out) {
+  __shared__ float partial_s[4][64];
+  __shared__ float u_s[64];
+  const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
+  const size_t c = blockIdx.x * 64ULL + lane;
+  const bool valid = c < W;
+  const size_t cols3 = 3 * W;
+  float x2 = 0.0F, u = 0.0F;
+  if (g == 0 && valid) {
+    float taps[3][kMaxShort];
+    load_short_taps(short_filter, short_len, c, taps);
+    gates(P, short_history, taps, short_len, cols3, 0, 0, c, &x2, &u);
+    u_s[lane] = u;
+  }
+  const bool fir = kind != kHyenaHcl;
+  const int hist = k - 1;
+  float part = 0.0F;
+  float v[kDecodeRowsPerThread];
+  if (fir && valid && inner_history != nullptr) {
+    const float *h = filter + (c / (W / groups)) * k;
+#pragma unroll
+    for (int i = 0; i < kDecodeRowsPerThread; ++i) {
+      const int old = g + 4 * i;
+      v[i] = old < hist ? inner_history[old * W + c] : 0.0F;
+    }
+#pragma unroll
+    for (int i = 0; i < kDecodeRowsPerThread; ++i) {
+      const int old = g + 4 * i;
+      if (old < hist)
+        part += v[i] * h[causal ? k - 1 - old : old];
+    }
+  }
+  partial_s[g][lane] = part;
+  __syncthreads();  // every history row read; u of the block's channels ready
+  if (fir && valid && inner_history != nullptr) {
+#pragma unroll
+    for (int i = 0; i < kDecodeRowsPerThread; ++i) {
+      const int old = g + 4 * i;
+      if (old >= 1 && old < hist)
+        inner_history[(old - 1) * W + c] = v[i];
+    }
+    if (g == 0 && hist > 0)
+      inner_history[(hist - 1) * W + c] = u_s[lane];
+  }
+  if (g != 0 || !valid)
+    return;
+  if (short_history != nullptr && short_len > 1) {
+    const int rows = short_len - 1;
+#pragma unroll
+    for (int s = 0; s < 3; ++s) {
+      const size_t col = 3 * c + s;
+      for (int h = 0; h + 1 < rows; ++h)
+        short_history[h * cols3 + col] = short_history[(h + 1) * cols3 + col];
+      short_history[(rows - 1) * cols3 + col] = load_act(P, col);
+    }
+  }
+  float total;
+  if (!fir) {
+    float modal = 0.0F;
+    for (int m = 0; m < S; ++m) {
+      float st = modal_state != nullptr ? modal_state[c * S + m] : 0.0F;
+      st = poles[c * S + m] * st + u;
+      if (modal_state != nullptr)
+        modal_state[c * S + m] = st;
+      modal += residues[c * S + m] * st;
+    }
+    total = modal + direct[c] * u;
+  } else {
+    const float *h = filter + (c / (W / groups)) * k;
+    total = ((partial_s[0][lane] + partial_s[1][lane]) + partial_s[2][lane]) + partial_s[3][lane];
+    total += u * h[causal ? 0 : hist];
+    if (direct != nullptr)
+      total += direct[c] * u;
+  }
+  put(out, c, x2 * total);
+}
+
 size_t hcl_chunks(size_t length) { return (length + kChunk - 1) / kChunk; }
 
 template <typename T, typename O, int kWin>
@@ -1812,6 +1910,23 @@ Status hyena_forward(int kind, const T *projection, size_t length,
   const int short_len = static_cast<int>(wt.short_len);
   const size_t planar = planar_projection ? width : 0;
   const dim3 channel_blocks(ceil_div(width, kChannels));
+  // One row (decode): the whole operator and both history updates in one
+  // launch.
+  if (length == 1 && planar == 0 &&
+      ((kind == kHyenaHcl && wt.poles != nullptr && wt.residues != nullptr &&
+        wt.direct != nullptr && wt.state >= 1 && wt.state <= kMaxState) ||
+       ((kind == kHyenaHcs || kind == kHyenaHcm) && wt.inner_filter != nullptr &&
+        wt.groups != 0 && width % wt.groups == 0 && wt.inner_len >= 1 &&
+        wt.inner_len <= 128 && (kind == kHyenaHcs || wt.direct != nullptr)))) {
+    const bool hcm = kind == kHyenaHcm;
+    hipLaunchKernelGGL((hyena_decode_kernel<T, O>), dim3(ceil_div(width, 64)), dim3(256), 0,
+                       stream, kind, projection, short_history, wt.short_filter, short_len,
+                       inner_history, wt.inner_filter, wt.groups,
+                       static_cast<int>(wt.inner_len), hcm ? 1 : 0,
+                       kind == kHyenaHcs ? nullptr : wt.direct, wt.poles, wt.residues,
+                       modal_state, static_cast<int>(wt.state), width, out);
+    return launch_status("hyena_decode_kernel");
+  }
   if (kind == kHyenaHcl) {
     if (wt.poles == nullptr || wt.residues == nullptr || wt.direct == nullptr ||
         wt.state == 0 || wt.state > kMaxState)
