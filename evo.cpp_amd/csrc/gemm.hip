@@ -644,7 +644,9 @@ Status gemm_bf16w(const Activation &a, const uint16_t *W, const GemmOutput &out,
     // Few tiles (short prompts against W-wide outputs): split K so that about
     // one tile per CU runs, partials in the workspace, then one reduction.
     int splits = 1;
-    if (mode != kGemmGated && split_workspace != nullptr && N % 4 == 0 && tiles < 128) {
+    // (The reduction reads the partials as 16-byte vectors.)
+    if (mode != kGemmGated && split_workspace != nullptr &&
+        reinterpret_cast<uintptr_t>(split_workspace) % 16 == 0 && N % 4 == 0 && tiles < 128) {
       for (int s = 2; s <= 16 && tiles * s <= 256; s *= 2)
         if (K % (static_cast<size_t>(s) * kBK) == 0 && K / s >= 8 * kBK &&
             static_cast<size_t>(s) * M * N * sizeof(float) <= split_workspace_bytes)

@@ -131,10 +131,11 @@ EVO_API evo_status evo_hip_linear(const uint16_t *x_hi, const uint16_t *x_lo,
                                   const float *residual, size_t m, size_t n,
                                   size_t k, float *out, void *stream);
 
-/* evo_hip_linear with an F32 device workspace: launches with few output
- * tiles split K across blocks (partials in the workspace, summed in split
- * order before the epilogue), the path the model takes for short prompts.
- * The same reference interface as evo_hip_linear. */
+/* evo_hip_linear with an F32 device workspace (16-byte aligned; otherwise
+ * it is not used): launches with few output tiles split K across blocks
+ * (partials in the workspace, summed in split order before the epilogue),
+ * the path the model takes for short prompts. The same reference interface
+ * as evo_hip_linear. */
 EVO_API evo_status evo_hip_linear_split(const uint16_t *x_hi, const uint16_t *x_lo,
                                         const uint16_t *w, const uint16_t *bias,
                                         const float *residual, size_t m, size_t n,
