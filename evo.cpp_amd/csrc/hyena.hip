@@ -223,7 +223,7 @@ __global__ void hcl_carry_kernel(float *__restrict__ chunk_state, size_t G,
     for (int q = 0; q < kAhead; ++q) {
       const size_t g = g0 + q;
       if (g >= G)
-        break;
+        continue;
       chunk_state[(g * S + m) * W + c] = state;
       const size_t len = min(L - g * kChunk, static_cast<size_t>(kChunk));
       float power = full;
@@ -1269,8 +1269,10 @@ template <> struct MsOut<SplitOut> {
   }
 };
 
+// Two blocks per CU for BF16 projections (71 KB of LDS); F32 projection
+// rows double the DMA stage (97 KB), so one block per CU.
 template <typename T, typename O>
-__global__ __launch_bounds__(256, 2) void hyena_fir_mfma_stream_kernel(
+__global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void hyena_fir_mfma_stream_kernel(
     const T *__restrict__ P, const float *__restrict__ short_history,
     const uint16_t *__restrict__ short_filter, int short_len,
     const float *__restrict__ inner_history, const float *__restrict__ filter,
