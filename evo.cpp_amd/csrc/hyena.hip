@@ -923,7 +923,7 @@ struct PairShort {
   }
 };
 
-constexpr int kHclBatch = 4;
+constexpr int kHclBatch = 4;  // even: the output pass stores rows in pairs
 
 // Lanes l and l ^ 1 share a channel pair: lane half h = l & 1 runs the short
 // FIR of channel c + h ("own"; the partner's is "other") and keeps modal
@@ -1051,9 +1051,10 @@ __global__ __launch_bounds__(256) void hcl_carry_seg_kernel(
 }
 
 // Phase 3: rescan every chunk from its true start state and write y. Both
-// lanes of a pair hold y of both channels; the even lane stores the hi
-// plane (or the BF16 / F32 values of channel c), the odd lane the lo plane
-// (or channel c + 1 of an F32 output).
+// lanes of a pair hold y of both channels. Rows leave in pairs: for BF16 and
+// split outputs the even lane writes the first row's word (both channels;
+// hi and lo planes through two uniform resources), the odd lane the second
+// row's; for F32 each lane writes its own channel of both rows.
 template <typename O> struct HalfOut;
 template <> struct HalfOut<float *> {
   __amdgpu_buffer_rsrc_t out;
@@ -1065,35 +1066,46 @@ template <> struct HalfOut<float *> {
                                           static_cast<int>(2 * lane + 4 * half),
                                           static_cast<int>(2 * row), kStreamStore);
   }
+  __device__ void put_rows(int half, uint32_t lane, uint32_t row, uint32_t row_bytes, float a0,
+                           float b0, float a1, float b1) const {
+    put(half, lane, row, a0, b0);
+    put(half, lane, row + row_bytes, a1, b1);
+  }
 };
 template <> struct HalfOut<uint16_t *> {
   __amdgpu_buffer_rsrc_t out;
   __device__ HalfOut(uint16_t *o, size_t first, size_t rows, size_t W) {
     out = buffer_resource(o + first * W, static_cast<uint32_t>(rows * W * 2));
   }
-  __device__ void put(int half, uint32_t lane, uint32_t row, float a, float b) const {
-    if (half == 0)
-      __builtin_amdgcn_raw_buffer_store_b32(pack_bf16(a, b), out, static_cast<int>(lane),
-                                            static_cast<int>(row), kStreamStore);
+  __device__ void put_rows(int half, uint32_t lane, uint32_t row, uint32_t row_bytes, float a0,
+                           float b0, float a1, float b1) const {
+    // Even lane row `row`, odd lane the next one.
+    const uint32_t word = half == 0 ? pack_bf16(a0, b0) : pack_bf16(a1, b1);
+    __builtin_amdgcn_raw_buffer_store_b32(word, out,
+                                          static_cast<int>(lane + row + half * row_bytes), 0,
+                                          kStreamStore);
   }
 };
 template <> struct HalfOut<SplitOut> {
-  __amdgpu_buffer_rsrc_t plane;
+  // Both resources are uniform; a missing lo plane gets an empty one (its
+  // stores are dropped).
+  __amdgpu_buffer_rsrc_t hi, lo;
   __device__ HalfOut(const SplitOut &o, size_t first, size_t rows, size_t W) {
-    // The odd lane's resource is the lo plane, or empty (stores dropped).
-    const int half = threadIdx.x & 1;
-    const uint16_t *base = half == 0 ? o.hi : o.lo;
-    plane = buffer_resource(base != nullptr ? base + first * W : o.hi,
-                            base != nullptr ? static_cast<uint32_t>(rows * W * 2) : 0);
+    const uint32_t bytes = static_cast<uint32_t>(rows * W * 2);
+    hi = buffer_resource(o.hi + first * W, bytes);
+    lo = buffer_resource(o.lo != nullptr ? o.lo + first * W : o.hi, o.lo != nullptr ? bytes : 0);
   }
-  __device__ void put(int half, uint32_t lane, uint32_t row, float a, float b) const {
+  // Two rows of the pair's channels (a: channel c, b: channel c + 1): the even
+  // lane writes row `row`, the odd lane the next one, each both planes.
+  __device__ void put_rows(int half, uint32_t lane, uint32_t row, uint32_t row_bytes, float a0,
+                           float b0, float a1, float b1) const {
+    const float a = half == 0 ? a0 : a1, b = half == 0 ? b0 : b1;
     const uint32_t h = pack_bf16(a, b);
-    const uint32_t word =
-        half == 0 ? h
-                  : pack_bf16(a - __builtin_bit_cast(float, h << 16),
-                              b - __builtin_bit_cast(float, h & 0xffff0000U));
-    __builtin_amdgcn_raw_buffer_store_b32(word, plane, static_cast<int>(lane),
-                                          static_cast<int>(row), kStreamStore);
+    const uint32_t l = pack_bf16(a - __builtin_bit_cast(float, h << 16),
+                                 b - __builtin_bit_cast(float, h & 0xffff0000U));
+    const int offset = static_cast<int>(lane + row + half * row_bytes);
+    __builtin_amdgcn_raw_buffer_store_b32(h, hi, offset, 0, kStreamStore);
+    __builtin_amdgcn_raw_buffer_store_b32(l, lo, offset, 0, kStreamStore);
   }
 };
 
@@ -1146,6 +1158,7 @@ __global__ __launch_bounds__(256) void hcl_output_pair_kernel(
       for (int b = 0; b < kHclBatch; ++b)
         next[b].load(in, lane_bytes, (base + kHclBatch + b) * row_bytes);
     }
+    float ya[2], yb[2];  // channels c and c + 1 of the batch's last two rows
 #pragma unroll
     for (int b = 0; b < kHclBatch; ++b) {
       float x2, u[2], modal[2];
@@ -1165,9 +1178,12 @@ __global__ __launch_bounds__(256) void hcl_output_pair_kernel(
       const float total = half == 0 ? modal[0] + partner : partner + modal[0];
       const float y = x2 * (total + d[0] * u[0]);
       const float y_other = swap_pair(y);
+      ya[b & 1] = half == 0 ? y : y_other;
+      yb[b & 1] = half == 0 ? y_other : y;
       // Rows past the chunk end are dropped by the store bound.
-      sink.put(half, out_lane, (base + b) * out_row, half == 0 ? y : y_other,
-               half == 0 ? y_other : y);
+      if (b & 1)
+        sink.put_rows(half, out_lane, (base + b - 1) * out_row, out_row, ya[0], yb[0], ya[1],
+                      yb[1]);
     }
   }
 }
