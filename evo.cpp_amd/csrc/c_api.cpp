@@ -324,8 +324,11 @@ evo_status evo_context_create(const evo_model *model, const evo_context_params *
       return publish(EVO_STATUS_INVALID_ARGUMENT,
                      "invalid_argument: evo_context_params is too small");
     const evo_context_params options = params == nullptr ? evo_context_default_params() : *params;
-    const uint32_t known = EVO_CONTEXT_FLAG_HIP_BF16 | EVO_CONTEXT_FLAG_HIP_FP8_EXACT;
-    if (options.context_size == 0 || (options.flags & ~known) != 0)
+    const uint32_t known = EVO_CONTEXT_FLAG_HIP_BF16 | EVO_CONTEXT_FLAG_HIP_FP8_EXACT |
+                           EVO_CONTEXT_FLAG_HIP_FP8_K32;
+    const uint32_t fp8_modes = EVO_CONTEXT_FLAG_HIP_FP8_EXACT | EVO_CONTEXT_FLAG_HIP_FP8_K32;
+    if (options.context_size == 0 || (options.flags & ~known) != 0 ||
+        (options.flags & fp8_modes) == fp8_modes)
       return publish(EVO_STATUS_INVALID_ARGUMENT,
                      "invalid_argument: invalid context parameters");
     const auto &config = model->state->weights->config();
@@ -336,6 +339,8 @@ evo_status evo_context_create(const evo_model *model, const evo_context_params *
     hip_options.split_activations = (options.flags & EVO_CONTEXT_FLAG_HIP_BF16) == 0;
     hip_options.fp8_mode = (options.flags & EVO_CONTEXT_FLAG_HIP_FP8_EXACT) != 0
                                ? evo::hip::kFp8Exact
+                           : (options.flags & EVO_CONTEXT_FLAG_HIP_FP8_K32) != 0
+                               ? evo::hip::kFp8MfmaK32
                                : evo::hip::kFp8MfmaK128;
     auto handle = std::make_unique<evo_context>();
     handle->state = model->state;

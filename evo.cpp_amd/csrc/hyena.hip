@@ -383,8 +383,8 @@ template <typename T> struct PairRow {
   __device__ void load(__amdgpu_buffer_rsrc_t resource, uint32_t lane, uint32_t row) {
 #pragma unroll
     for (int i = 0; i < kWords; ++i)
-      word[i] = __builtin_amdgcn_raw_buffer_load_b32(resource, static_cast<int>(lane + 4 * i),
-                                                     static_cast<int>(row), 0);
+      word[i] = __builtin_amdgcn_raw_buffer_load_b32(resource,
+                                                     static_cast<int>(lane + row + 4 * i), 0, 0);
   }
   __device__ float at(int i) const {
     if constexpr (sizeof(T) == 2)
@@ -413,12 +413,12 @@ template <> struct PairOut<float *> {
     out = buffer_resource(o + first * W, static_cast<uint32_t>(rows * W * 4));
   }
   __device__ void put(uint32_t lane, uint32_t row, float a, float b) const {
+    // The row offset goes into voffset: soffset is not part of the buffer
+    // range check, so only voffset bounds the rows past the segment end.
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, a), out,
-                                          static_cast<int>(2 * lane), static_cast<int>(2 * row),
-                                          kStreamStore);
+                                          static_cast<int>(2 * (lane + row)), 0, kStreamStore);
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, b), out,
-                                          static_cast<int>(2 * lane + 4), static_cast<int>(2 * row),
-                                          kStreamStore);
+                                          static_cast<int>(2 * (lane + row) + 4), 0, kStreamStore);
   }
 };
 template <> struct PairOut<uint16_t *> {
@@ -427,8 +427,8 @@ template <> struct PairOut<uint16_t *> {
     out = buffer_resource(o + first * W, static_cast<uint32_t>(rows * W * 2));
   }
   __device__ void put(uint32_t lane, uint32_t row, float a, float b) const {
-    __builtin_amdgcn_raw_buffer_store_b32(pack_bf16(a, b), out, static_cast<int>(lane),
-                                          static_cast<int>(row), kStreamStore);
+    __builtin_amdgcn_raw_buffer_store_b32(pack_bf16(a, b), out, static_cast<int>(lane + row), 0,
+                                          kStreamStore);
   }
 };
 template <> struct PairOut<SplitOut> {
@@ -441,13 +441,12 @@ template <> struct PairOut<SplitOut> {
   }
   __device__ void put(uint32_t lane, uint32_t row, float a, float b) const {
     const uint32_t h = pack_bf16(a, b);
-    __builtin_amdgcn_raw_buffer_store_b32(h, hi, static_cast<int>(lane), static_cast<int>(row),
-                                          kStreamStore);
+    __builtin_amdgcn_raw_buffer_store_b32(h, hi, static_cast<int>(lane + row), 0, kStreamStore);
     // With no lo plane the resource has zero size and the store is dropped.
     __builtin_amdgcn_raw_buffer_store_b32(
         pack_bf16(a - __builtin_bit_cast(float, h << 16),
                   b - __builtin_bit_cast(float, h & 0xffff0000U)),
-        lo, static_cast<int>(lane), static_cast<int>(row), kStreamStore);
+        lo, static_cast<int>(lane + row), 0, kStreamStore);
   }
 };
 
@@ -1063,8 +1062,8 @@ template <> struct HalfOut<float *> {
   }
   __device__ void put(int half, uint32_t lane, uint32_t row, float a, float b) const {
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, half ? b : a), out,
-                                          static_cast<int>(2 * lane + 4 * half),
-                                          static_cast<int>(2 * row), kStreamStore);
+                                          static_cast<int>(2 * (lane + row) + 4 * half), 0,
+                                          kStreamStore);
   }
   __device__ void put_rows(int half, uint32_t lane, uint32_t row, uint32_t row_bytes, float a0,
                            float b0, float a1, float b1) const {

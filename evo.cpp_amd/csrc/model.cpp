@@ -345,6 +345,8 @@ Status Context::initialize(std::shared_ptr<const Model> model, size_t capacity,
   profile_ = options.split_activations ? "hip-f32" : "hip-bf16";
   if (options.fp8_mode == kFp8Exact)
     profile_ += "+fp8-exact";
+  else if (options.fp8_mode == kFp8MfmaK32)
+    profile_ += "+fp8-k32";
   EVO_TRY(hip_check(hipSetDevice(model_->device()), "select device"));
   EVO_TRY(hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "create stream"));
   const size_t R = arena_rows_, w = c.width;

@@ -91,6 +91,8 @@ class EvoLibrary:
                                             LOGITS_CALLBACK, ctypes.c_void_p]
         lib.evo_context_decode.argtypes = [ctypes.c_void_p, ctypes.c_uint32,
                                            LOGITS_CALLBACK, ctypes.c_void_p]
+        lib.evo_context_embed.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                          LOGITS_CALLBACK, ctypes.c_void_p]
         lib.evo_batch_create.argtypes = [ctypes.c_size_t,
                                          ctypes.POINTER(ctypes.c_void_p)]
         lib.evo_batch_free.argtypes = [ctypes.c_void_p]
@@ -193,6 +195,29 @@ class Context:
             lib.evo_batch_free(batch)
         if not chunks:
             return np.zeros((0, self.model.vocab), dtype=np.float32)
+        return np.concatenate(chunks, axis=0)
+
+    def embed(self, sequence: bytes, layer: int) -> np.ndarray:
+        """Prefill one sequence and return block `layer`'s output hidden
+        states [len, width] F32 (evo_context_embed; the context must be
+        fresh)."""
+        lib = self.model.library.lib
+        chunks: List[np.ndarray] = []
+
+        def callback(values, rows, columns, _offset, _user):
+            chunks.append(np.ctypeslib.as_array(values, shape=(rows, columns)).copy())
+            return 0
+
+        c_callback = LOGITS_CALLBACK(callback)
+        batch = ctypes.c_void_p()
+        self.model.library.check(lib.evo_batch_create(1, ctypes.byref(batch)))
+        try:
+            self.model.library.check(
+                lib.evo_batch_add_sequence(batch, sequence, len(sequence)))
+            self.model.library.check(
+                lib.evo_context_embed(self.handle, batch, layer, c_callback, None))
+        finally:
+            lib.evo_batch_free(batch)
         return np.concatenate(chunks, axis=0)
 
     def decode(self, token: int) -> np.ndarray:

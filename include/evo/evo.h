@@ -81,7 +81,10 @@ enum {
   /* Software-FP8 projections run through the bit-exact integer QGMMA
    * emulation ("+fp8-exact") instead of the default E4M3 MFMA path, which
    * promotes each 128-K chunk into an E8M13-truncated accumulator. */
-  EVO_CONTEXT_FLAG_HIP_FP8_EXACT = 1u << 9u
+  EVO_CONTEXT_FLAG_HIP_FP8_EXACT = 1u << 9u,
+  /* E4M3 MFMA path promoting every 32-K chunk (the reference's QGMMA group
+   * size) instead of every 128 K ("+fp8-k32"); exclusive with FP8_EXACT. */
+  EVO_CONTEXT_FLAG_HIP_FP8_K32 = 1u << 10u
 };
 
 typedef struct evo_model evo_model;

@@ -27,6 +27,7 @@
 #endif
 #ifdef _OPENMP
 #include <omp.h>
+#include <deque>
 #endif
 
 namespace {
@@ -146,6 +147,76 @@ float dot_bf16(const float *const input, const uint16_t *const weight,
   for (std::size_t index = 0; index < size; ++index)
     result += input[index] * bf16_bits_to_float(weight[index]);
   return result;
+}
+
+// Dots of a tile of rows x targets, each bit-identical to dot_bf16 of that
+// pair: the AVX2 path runs 4 rows x 2 targets as eight independent chains of
+// the same FMA sequence (one chain per output, so FMA latency is hidden
+// without changing any output's order of operations).
+#if defined(__x86_64__)
+__attribute__((target("avx2,fma"))) void
+dot_block_4x2_avx2(const float *const *input, const uint16_t *const *weight,
+                   const std::size_t size, float result[4][2]) {
+  __m256 total[4][2];
+  for (int r = 0; r < 4; ++r)
+    for (int t = 0; t < 2; ++t)
+      total[r][t] = _mm256_setzero_ps();
+  std::size_t index = 0;
+  for (; index + 8 <= size; index += 8) {
+    __m256 w[2];
+    for (int t = 0; t < 2; ++t) {
+      const auto packed =
+          _mm_loadu_si128(reinterpret_cast<const __m128i *>(weight[t] + index));
+      w[t] = _mm256_castsi256_ps(_mm256_slli_epi32(_mm256_cvtepu16_epi32(packed), 16));
+    }
+    for (int r = 0; r < 4; ++r) {
+      const __m256 x = _mm256_loadu_ps(input[r] + index);
+      for (int t = 0; t < 2; ++t)
+        total[r][t] = _mm256_fmadd_ps(x, w[t], total[r][t]);
+    }
+  }
+  for (int r = 0; r < 4; ++r)
+    for (int t = 0; t < 2; ++t) {
+      alignas(32) float lanes[8];
+      _mm256_store_ps(lanes, total[r][t]);
+      float value = lanes[0] + lanes[1] + lanes[2] + lanes[3] + lanes[4] +
+                    lanes[5] + lanes[6] + lanes[7];
+      for (std::size_t k = index; k < size; ++k)
+        value += input[r][k] * bf16_bits_to_float(weight[t][k]);
+      result[r][t] = value;
+    }
+}
+#endif
+
+// out[row * ldo + target] = dot_bf16(x + row * in, w + target * in, in) for
+// rows [r0, r1) and targets [c0, c1).
+void dot_tile_bf16(const float *x, const uint16_t *w, size_t in, size_t r0,
+                   size_t r1, size_t c0, size_t c1, float *out, size_t ldo) {
+  size_t row = r0;
+#if defined(__x86_64__)
+  static const bool avx2 = cpu_has_avx2_fma();
+  if (avx2) {
+    for (; row + 4 <= r1; row += 4) {
+      size_t target = c0;
+      for (; target + 2 <= c1; target += 2) {
+        const float *inputs[4] = {x + row * in, x + (row + 1) * in,
+                                  x + (row + 2) * in, x + (row + 3) * in};
+        const uint16_t *weights[2] = {w + target * in, w + (target + 1) * in};
+        float result[4][2];
+        dot_block_4x2_avx2(inputs, weights, in, result);
+        for (int r = 0; r < 4; ++r)
+          for (int t = 0; t < 2; ++t)
+            out[(row + r) * ldo + target + t] = result[r][t];
+      }
+      for (; target < c1; ++target)
+        for (size_t r = row; r < row + 4; ++r)
+          out[r * ldo + target] = dot_bf16(x + r * in, w + target * in, in);
+    }
+  }
+#endif
+  for (; row < r1; ++row)
+    for (size_t target = c0; target < c1; ++target)
+      out[row * ldo + target] = dot_bf16(x + row * in, w + target * in, in);
 }
 
 float gelu_erf(const float value) {
@@ -325,6 +396,9 @@ struct Model {
   void *map{nullptr};
   size_t map_size{0};
   std::map<std::string, Tensor> tensors;
+  // Tensors made after load (load-time FP8 conversion) and their bytes.
+  std::deque<Tensor> converted;
+  std::deque<std::vector<uint8_t>> converted_bytes;
   std::map<std::string, std::string> metadata;
   size_t vocab{0}, width{0}, layers{0}, heads{0}, state{0}, inner{0},
       short_len{0}, hcs_len{0}, hcm_len{0}, hcs_groups{0}, hcm_groups{0};
@@ -383,28 +457,133 @@ const Tensor *need(const Model &m, const std::string &name,
   return &it->second;
 }
 
+// ---- QGMMA (tests/test_cuda_ops.cu:119-187): per group of `group_k` terms,
+// the accumulator and every nonzero product are aligned to the largest
+// binade among them with 13 fractional bits, summed as integers, and the
+// sum becomes the new accumulator truncated to E8M13; output bf16(acc * s).
+// Decoded values and binades of both operands are tabulated once; outputs
+// run in parallel (each is the reference's sequential group walk).
+float e4m3_value(const uint8_t code) {
+  const auto magnitude = static_cast<uint8_t>(code & 0x7fU);
+  const float sign = (code & 0x80U) == 0U ? 1.0F : -1.0F;
+  if (magnitude == 0x7fU)
+    return std::copysign(std::numeric_limits<float>::quiet_NaN(), sign);
+  return std::copysign(e4m3_positive(magnitude), sign);
+}
+
+// Integer form of align_to for a product of two E4M3 values. A finite code
+// is S * 2^E with an integer significand S (8 + mantissa for normal codes,
+// the mantissa for subnormals); its binade is unbiased_exponent(value).
+// align_to(a * b, binade_a + binade_b, top, true) keeps
+// floor(|a b| * 2^(13 - top)) (the significand shifts compose into one
+// floor), i.e. |S_a S_b| shifted by E_a + E_b + 13 - top, left or right.
+struct E4m3Table {
+  int32_t signed_significand[256], exponent[256], binade[256];
+  bool finite[256];
+  E4m3Table() {
+    for (int code = 0; code < 256; ++code) {
+      const float value = e4m3_value(static_cast<uint8_t>(code));
+      finite[code] = !std::isnan(value);
+      const unsigned e = (code >> 3) & 0x0f, m = code & 0x07;
+      const int32_t significand = e == 0 ? static_cast<int32_t>(m) : static_cast<int32_t>(8 + m);
+      signed_significand[code] = (code & 0x80) != 0 ? -significand : significand;
+      exponent[code] = e == 0 ? -9 : static_cast<int>(e) - 10;
+      // Zero codes never set the group's top binade. NaN codes (0x7f, 0xff)
+      // are outside the QGMMA contract: the quantiser never produces them
+      // from finite inputs.
+      binade[code] = value == 0.0F || !finite[code] ? -4096 : unbiased_exponent(value);
+    }
+  }
+};
+
+__attribute__((target("avx2"))) void
+qgmma_group(const int32_t *sa, const int32_t *ea, const int32_t *ba,
+            const int32_t *sb, const int32_t *eb, const int32_t *bb, size_t n,
+            float *acc) {
+  int top = *acc == 0.0F ? -1024 : unbiased_exponent(*acc);
+  for (size_t k = 0; k < n; ++k)
+    top = std::max(top, ba[k] + bb[k]);
+  int32_t sum = *acc == 0.0F ? 0 : align_to(*acc, unbiased_exponent(*acc), top, false);
+  for (size_t k = 0; k < n; ++k) {
+    const int32_t product = sa[k] * sb[k];
+    const int32_t shift = ea[k] + eb[k] + 13 - top;
+    const uint32_t magnitude = static_cast<uint32_t>(product < 0 ? -product : product);
+    const uint32_t left = static_cast<uint32_t>(shift > 0 ? shift : 0);
+    const uint32_t right = static_cast<uint32_t>(shift < 0 ? -shift : 0);
+    const uint32_t aligned = right > 31 ? 0U : (magnitude << left) >> right;
+    sum += product < 0 ? -static_cast<int32_t>(aligned) : static_cast<int32_t>(aligned);
+  }
+  *acc = sum == 0 ? 0.0F
+                  : bits_to_float(float_bits(std::ldexp(static_cast<float>(sum), top - 13)) &
+                                  0xfffffc00U);
+}
+
+void qgmma_core(const uint8_t *input_codes, const uint8_t *weight_codes,
+                size_t rows, size_t inner, size_t cols, float output_scale,
+                size_t group_k, float *out, int threads) {
+  static const E4m3Table table;
+  // Decoded input rows, tabulated once: significand, exponent, binade.
+  std::vector<int32_t> sa(rows * inner), ea(rows * inner), ba(rows * inner);
+  for (size_t i = 0; i < rows * inner; ++i) {
+    sa[i] = table.signed_significand[input_codes[i]];
+    ea[i] = table.exponent[input_codes[i]];
+    ba[i] = table.binade[input_codes[i]];
+  }
+#pragma omp parallel num_threads(threads > 0 ? threads : 1)
+  {
+    std::vector<int32_t> sb(inner), eb(inner), bb(inner);
+#pragma omp for schedule(dynamic, 4)
+    for (long long c = 0; c < static_cast<long long>(cols); ++c) {
+      const size_t col = static_cast<size_t>(c);
+      for (size_t k = 0; k < inner; ++k) {
+        const uint8_t code = weight_codes[col * inner + k];
+        sb[k] = table.signed_significand[code];
+        eb[k] = table.exponent[code];
+        bb[k] = table.binade[code];
+      }
+      for (size_t row = 0; row < rows; ++row) {
+        float acc = 0.0F;
+        for (size_t start = 0; start < inner; start += group_k) {
+          const size_t at = row * inner + start;
+          qgmma_group(&sa[at], &ea[at], &ba[at], &sb[start], &eb[start], &bb[start],
+                      group_k, &acc);
+        }
+        out[row * cols + col] =
+            bf16_bits_to_float(float_to_bf16_rne(acc * output_scale));
+      }
+    }
+  }
+}
+
 // ---- Model-path primitives (src/cpu/model.cpp:284-453).
 void linear_model(const std::vector<float> &input, size_t rows, size_t in,
                   const Tensor &weight, size_t out_width, const Tensor *bias,
                   std::vector<float> *output, int threads) {
   output->assign(rows * out_width, 0.0F);
-  const long long total = static_cast<long long>(rows * out_width);
-#pragma omp parallel for schedule(static) num_threads(threads > 0 ? threads : 1)
-  for (long long item = 0; item < total; ++item) {
-    const size_t row = static_cast<size_t>(item) / out_width;
-    const size_t target = static_cast<size_t>(item) % out_width;
-    const float *source = input.data() + row * in;
-    float value;
-    if (weight.dtype == "BF16") {
-      value = dot_bf16(source, weight.bf16() + target * in, in);
-    } else {
-      value = 0.0F;
-      for (size_t index = 0; index < in; ++index)
-        value += source[index] * weight.at(target * in + index);
-    }
-    if (bias != nullptr)
-      value += bias->at(target);
-    (*output)[static_cast<size_t>(item)] = value;
+  // Tiles of 32 rows x 32 outputs keep one weight panel cache-resident while
+  // the rows sweep it; every output is still one dot in the reference order.
+  const size_t row_tiles = (rows + 31) / 32, col_tiles = (out_width + 31) / 32;
+  const long long tiles = static_cast<long long>(row_tiles * col_tiles);
+#pragma omp parallel for schedule(dynamic, 1) num_threads(threads > 0 ? threads : 1)
+  for (long long tile = 0; tile < tiles; ++tile) {
+    const size_t r0 = static_cast<size_t>(tile) / col_tiles * 32;
+    const size_t c0 = static_cast<size_t>(tile) % col_tiles * 32;
+    const size_t r1 = std::min(r0 + 32, rows), c1 = std::min(c0 + 32, out_width);
+    if (weight.dtype == "BF16")
+      dot_tile_bf16(input.data(), weight.bf16(), in, r0, r1, c0, c1,
+                    output->data(), out_width);
+    for (size_t target = c0; target < c1; ++target)
+      for (size_t row = r0; row < r1; ++row) {
+        float &value = (*output)[row * out_width + target];
+        if (weight.dtype != "BF16") {
+          const float *source = input.data() + row * in;
+          value = 0.0F;
+          for (size_t index = 0; index < in; ++index)
+            value += source[index] * weight.at(target * in + index);
+        }
+        if (bias != nullptr)
+          value += bias->at(target);
+      }
   }
 }
 
@@ -417,19 +596,15 @@ void linear_fp8(const std::vector<float> &input, size_t rows, size_t in,
   oracle_e4m3_quantize_f32(input.data(), codes.size(), input_scale,
                            codes.data());
   output->assign(rows * out_width, 0.0F);
-  const long long total = static_cast<long long>(rows);
-#pragma omp parallel for schedule(static) num_threads(threads > 0 ? threads : 1)
-  for (long long row = 0; row < total; ++row) {
-    oracle_qgmma_linear(codes.data() + static_cast<size_t>(row) * in,
-                        weight.data, 1, in, out_width, output_scale, 32,
-                        output->data() + static_cast<size_t>(row) * out_width);
-  }
+  qgmma_core(codes.data(), weight.data, rows, in, out_width, output_scale, 32,
+             output->data(), threads);
 }
 
 void rms_norm_model(const std::vector<float> &input, size_t rows, size_t width,
                     const Tensor &scale, float eps,
                     std::vector<float> *output) {
   output->resize(input.size());
+#pragma omp parallel for schedule(static)
   for (size_t row = 0; row < rows; ++row) {
     float sum = 0.0F;
     for (size_t column = 0; column < width; ++column) {
@@ -453,8 +628,11 @@ void fir_model(const std::vector<float> &input, size_t rows, size_t channels,
   const size_t history = kernel - 1;
   output->resize(input.size());
   const size_t per_group = channels / groups;
-  for (size_t row = 0; row < rows; ++row) {
-    for (size_t channel = 0; channel < channels; ++channel) {
+  // Channels are independent (each owns its history), so they run in
+  // parallel; inside a channel the rows run in order as in the reference.
+#pragma omp parallel for schedule(static)
+  for (size_t channel = 0; channel < channels; ++channel) {
+    for (size_t row = 0; row < rows; ++row) {
       const size_t group = channel / per_group;
       float total = 0.0F;
       for (size_t old = 0; old < history; ++old) {
@@ -507,8 +685,9 @@ void hyena_model(Mixer type, const std::vector<float> &projection, size_t rows,
               direct_at, true, &cache->inner_state, &mixed);
   } else {
     mixed.resize(rows * width);
-    for (size_t row = 0; row < rows; ++row) {
-      for (size_t channel = 0; channel < width; ++channel) {
+#pragma omp parallel for schedule(static)
+    for (size_t channel = 0; channel < width; ++channel) {
+      for (size_t row = 0; row < rows; ++row) {
         float modal = 0.0F;
         for (size_t mode = 0; mode < state_size; ++mode) {
           const size_t index = channel * state_size + mode;
@@ -803,35 +982,8 @@ int oracle_qgmma_linear(const uint8_t *input_codes, const uint8_t *weight_codes,
                         float output_scale, size_t group_k, float *out) {
   if (group_k == 0 || inner % group_k != 0)
     return fail("qgmma inner dimension must be a multiple of the group");
-  std::vector<float> a(inner), b(inner);
-  for (size_t row = 0; row < rows; ++row) {
-    for (size_t k = 0; k < inner; ++k)
-      a[k] = oracle_e4m3_decode(input_codes[row * inner + k]);
-    for (size_t col = 0; col < cols; ++col) {
-      for (size_t k = 0; k < inner; ++k)
-        b[k] = oracle_e4m3_decode(weight_codes[col * inner + k]);
-      float acc = 0.0F;
-      for (size_t start = 0; start < inner; start += group_k) {
-        int top = acc == 0.0F ? -1024 : unbiased_exponent(acc);
-        for (size_t k = start; k < start + group_k; ++k)
-          if (a[k] != 0.0F && b[k] != 0.0F)
-            top = std::max(top, unbiased_exponent(a[k]) + unbiased_exponent(b[k]));
-        int32_t sum =
-            acc == 0.0F ? 0 : align_to(acc, unbiased_exponent(acc), top, false);
-        for (size_t k = start; k < start + group_k; ++k)
-          if (a[k] != 0.0F && b[k] != 0.0F)
-            sum += align_to(a[k] * b[k],
-                            unbiased_exponent(a[k]) + unbiased_exponent(b[k]),
-                            top, true);
-        acc = sum == 0 ? 0.0F
-                       : bits_to_float(float_bits(std::ldexp(
-                                           static_cast<float>(sum), top - 13)) &
-                                       0xfffffc00U);
-      }
-      out[row * cols + col] =
-          bf16_bits_to_float(float_to_bf16_rne(acc * output_scale));
-    }
-  }
+  qgmma_core(input_codes, weight_codes, rows, inner, cols, output_scale, group_k,
+             out, omp_get_max_threads());
   return 0;
 }
 
@@ -967,16 +1119,18 @@ int oracle_causal_attention(const float *q, const float *k, const float *v,
 int oracle_linear_bf16w(const float *x, size_t rows, size_t in_features,
                         const uint16_t *weight, size_t out_features,
                         const uint16_t *bias, float *out, int threads) {
-  const long long total = static_cast<long long>(rows * out_features);
-#pragma omp parallel for schedule(static) num_threads(threads > 0 ? threads : 1)
-  for (long long item = 0; item < total; ++item) {
-    const size_t row = static_cast<size_t>(item) / out_features;
-    const size_t o = static_cast<size_t>(item) % out_features;
-    float value = dot_bf16(x + row * in_features, weight + o * in_features,
-                           in_features);
+  const size_t row_tiles = (rows + 31) / 32, col_tiles = (out_features + 31) / 32;
+  const long long tiles = static_cast<long long>(row_tiles * col_tiles);
+#pragma omp parallel for schedule(dynamic, 1) num_threads(threads > 0 ? threads : 1)
+  for (long long tile = 0; tile < tiles; ++tile) {
+    const size_t r0 = static_cast<size_t>(tile) / col_tiles * 32;
+    const size_t c0 = static_cast<size_t>(tile) % col_tiles * 32;
+    const size_t r1 = std::min(r0 + 32, rows), c1 = std::min(c0 + 32, out_features);
+    dot_tile_bf16(x, weight, in_features, r0, r1, c0, c1, out, out_features);
     if (bias != nullptr)
-      value += bf16_bits_to_float(bias[o]);
-    out[static_cast<size_t>(item)] = value;
+      for (size_t row = r0; row < r1; ++row)
+        for (size_t o = c0; o < c1; ++o)
+          out[row * out_features + o] += bf16_bits_to_float(bias[o]);
   }
   return 0;
 }
@@ -1027,6 +1181,45 @@ void *oracle_model_load(const char *path, char *error, size_t error_size) {
 }
 
 void oracle_model_free(void *model) { delete static_cast<Model *>(model); }
+// Load-time software-FP8 conversion of every BF16 Hyena input projection
+// with the converter's per-tensor rule (evo.cpp tools/evo/checkpoint.py:
+// 393-396): weight_scale = 448 / amax(W) over finite values, codes =
+// E4M3(W * weight_scale), input_scale = 448 / input_amax, output_scale =
+// 1 / (input_scale * weight_scale).
+int oracle_model_convert_fp8(void *model_handle, float input_amax) {
+  auto &m = *static_cast<Model *>(model_handle);
+  for (size_t i = 0; i < m.layers; ++i) {
+    Layer &layer = m.layer[i];
+    if (layer.type == Mixer::kAttention || layer.projection->dtype != "BF16")
+      continue;
+    const Tensor &source = *layer.projection;
+    const size_t count = source.elements();
+    uint16_t top = 0;
+    for (size_t e = 0; e < count; ++e) {
+      const uint16_t magnitude = source.bf16()[e] & 0x7fffU;
+      if (magnitude <= 0x7f80U)
+        top = std::max(top, magnitude);
+    }
+    const float amax = bf16_bits_to_float(top);
+    if (!(amax > 0.0F) || !std::isfinite(amax))
+      return fail("projection has no finite nonzero amax");
+    const float weight_scale = 448.0F / amax;
+    m.converted_bytes.emplace_back(count);
+    oracle_e4m3_quantize_bf16(source.bf16(), count, weight_scale,
+                              m.converted_bytes.back().data());
+    Tensor codes;
+    codes.dtype = "F8_E4M3";
+    codes.shape = source.shape;
+    codes.data = m.converted_bytes.back().data();
+    codes.bytes = count;
+    m.converted.push_back(codes);
+    layer.projection = &m.converted.back();
+    layer.fp8_input_scale = 448.0F / input_amax;
+    layer.fp8_output_scale = 1.0F / (layer.fp8_input_scale * weight_scale);
+  }
+  return 0;
+}
+
 size_t oracle_model_width(const void *m) {
   return static_cast<const Model *>(m)->width;
 }
@@ -1117,8 +1310,11 @@ int oracle_model_prefill(void *model_handle, const uint32_t *tokens, size_t n,
                    threads);
       for (size_t i = 0; i < hidden.size(); ++i)
         hidden[i] += residual[i];
+      // capture_layer == SIZE_MAX captures every block: [layers][n][w].
       if (capture != nullptr && capture_layer == index)
         std::copy(hidden.begin(), hidden.end(), capture + offset * w);
+      else if (capture != nullptr && capture_layer == static_cast<size_t>(-1))
+        std::copy(hidden.begin(), hidden.end(), capture + (index * n + offset) * w);
     }
     rms_norm_model(hidden, rows, w, *m.final_norm, m.eps, &normalized);
     std::vector<float> chunk_logits;

@@ -106,6 +106,15 @@ size_t oracle_model_layers(const void *model);
 int oracle_model_prefill(void *model, const uint32_t *tokens, size_t n,
                          size_t chunk, float *logits, size_t capture_layer,
                          float *capture, int threads);
+/* capture_layer == SIZE_MAX copies every block's output: capture holds
+ * [layers][n][width]. */
+/* Load-time FP8 conversion of the BF16 Hyena projections (the converter's
+ * rule, evo.cpp tools/evo/checkpoint.py:393-396): weight_scale = 448 /
+ * amax(W), codes = E4M3(W * weight_scale), input_scale = 448 / input_amax,
+ * output_scale = 1 / (input_scale * weight_scale).
+ * Pinned by: the same model written with codes and scales computed by the
+ * artifact writer's independent numpy encoder (tests/test_oracle.py). */
+int oracle_model_convert_fp8(void *model, float input_amax);
 const char *oracle_last_error(void);
 
 #ifdef __cplusplus

@@ -44,6 +44,7 @@ def lib() -> ctypes.CDLL:
         "oracle_model_vocab": (S, [P]),
         "oracle_model_layers": (S, [P]),
         "oracle_model_prefill": (I, [P, P, S, S, P, S, P, I]),
+        "oracle_model_convert_fp8": (I, [P, F]),
         "oracle_last_error": (ctypes.c_char_p, []),
     }
     for name, (res, args) in sig.items():
@@ -75,6 +76,13 @@ class OracleModel:
         self.vocab = lib().oracle_model_vocab(self.handle)
         self.layers = lib().oracle_model_layers(self.handle)
 
+    def convert_fp8(self, input_amax: float = 8.0) -> "OracleModel":
+        """Convert every BF16 Hyena projection to E4M3 codes with the
+        converter's amax rule (what libevo_hip.so does at load under
+        EVO_MODEL_FLAG_HIP_FP8_PROJECTIONS)."""
+        check(lib().oracle_model_convert_fp8(self.handle, input_amax))
+        return self
+
     def __del__(self):
         if getattr(self, "handle", None):
             lib().oracle_model_free(self.handle)
@@ -84,11 +92,15 @@ class OracleModel:
         tokens = np.ascontiguousarray(tokens, dtype=np.uint32)
         logits = np.zeros((len(tokens), self.vocab), np.float32)
         capture = None
-        if capture_layer is not None:
+        layer = 2 ** 62
+        if capture_layer == "all":  # every block's output: [layers, n, width]
+            capture = np.zeros((self.layers, len(tokens), self.width), np.float32)
+            layer = 2 ** 64 - 1
+        elif capture_layer is not None:
             capture = np.zeros((len(tokens), self.width), np.float32)
+            layer = capture_layer
         check(lib().oracle_model_prefill(
-            self.handle, ptr(tokens), len(tokens), chunk, ptr(logits),
-            capture_layer if capture_layer is not None else 2 ** 62,
+            self.handle, ptr(tokens), len(tokens), chunk, ptr(logits), layer,
             ptr(capture), threads))
         return (logits, capture) if capture_layer is not None else logits
 

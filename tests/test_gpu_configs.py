@@ -1,0 +1,245 @@
+"""GPU parity at the benchmark configurations' own sizes (configs 2-5 of the
+benchmark plan; config 1 is in test_gpu_model.py), called through the C ABI.
+
+* Config 2: one Hyena operator at 7B width, L = 8192, W = 4096, 256 filter
+  groups, BF16 projection N(0, 1) in, split planes out (the model path),
+  against the oracle mixer on the same BF16 projection: max error <= 2e-5 of
+  the output scale.
+* Config 3: the FP8 projection GEMM M = 1024, K = 4096, N = 12288 with amax
+  scales: E4M3 codes bit-exact on every element; exact (QGMMA) mode
+  bit-exact on 64 sampled rows x all 12288 columns; the MFMA K32 / K128
+  modes within the RMS / max bounds of test_gpu_ops.py on those rows.
+* Config 4: a 7B-width model with one block of each mixer type (HCS, HCM,
+  HCL, attention; FFN 11264, 32 heads, 256 filter groups) at 8192 tokens
+  against the oracle: logits and every block output within 1e-3 of the
+  output scale, top-1 100 %. The full 32-block 7B shape at 8192 tokens:
+  arena 1024 equals arena 8192 within 1e-5, repeated runs are bit-identical,
+  logits finite.
+* Config 5: 131072 tokens through the 32-block 7B shape, arena 4096 against
+  arena 8192 within 1e-5, finite.
+
+Inputs follow the benchmark distributions ("survey" init: linears N(0, 0.02),
+taps and D N(0, 0.02), log-poles log U[0.5, 0.99], residues N(0, 0.02)).
+"""
+import ctypes
+import os
+import time
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from evo_hip import artifact as A
+from evo_hip import capi
+from evo_hip import native as N
+from evo_hip.artifact import bf16_bits, bf16_to_f32
+from gpu_util import dev, empty, host, p, stream
+from test_gpu_ops import hyena_gpu, hyena_oracle, rel_err
+
+pytestmark = pytest.mark.gpu
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB = os.path.join(ROOT, "evo.cpp_amd", "lib", "libevo_hip.so")
+THREADS = 16  # the oracle's OpenMP threads (the GPU box's CPU share)
+
+
+def rng(seed):
+    return np.random.Generator(np.random.PCG64(seed))
+
+
+def say(message):
+    print(message, flush=True)
+
+
+# -------------------------------------------------------------- config 2
+@pytest.mark.parametrize("kind", [N.HYENA_HCS, N.HYENA_HCM, N.HYENA_HCL])
+def test_config2_hyena_operator_7b_width(kind):
+    length, width, groups = 8192, 4096, 256
+    r = rng(2000 + kind)
+    proj = bf16_to_f32(bf16_bits(r.standard_normal((length, 3 * width), dtype=np.float32)))
+    case = dict(projection=proj, width=width,
+                short=bf16_bits(r.standard_normal((3 * width, 3), dtype=np.float32) * 0.02))
+    if kind != N.HYENA_HCL:
+        taps = 7 if kind == N.HYENA_HCS else 128
+        case["inner"] = bf16_to_f32(bf16_bits(
+            r.standard_normal((groups, taps), dtype=np.float32) * 0.02))
+        case["groups"], case["inner_len"] = groups, taps
+    if kind != N.HYENA_HCS:
+        case["direct"] = bf16_to_f32(bf16_bits(r.standard_normal(width, dtype=np.float32) * 0.02))
+    if kind == N.HYENA_HCL:
+        case["log_poles"] = np.log(r.uniform(0.5, 0.99, (width, 16))).astype(np.float32)
+        case["residues"] = (r.standard_normal((width, 16)) * 0.02).astype(np.float32)
+        case["state"] = 16
+    expected = hyena_oracle(kind, case)
+    actual = hyena_gpu(kind, case, dtype=N.DTYPE_BF16_SPLIT, bf16_taps=True, guard=8)
+    error = rel_err(actual, expected)
+    say(f"config 2 kind {kind}: max err {error:.3g} of the output scale")
+    assert error < 2e-5
+
+
+# -------------------------------------------------------------- config 3
+def test_config3_fp8_projection_gemm():
+    m, k, n = 1024, 4096, 12288
+    r = rng(3000)
+    a_bits = bf16_bits(r.standard_normal((m, k), dtype=np.float32))
+    w = bf16_to_f32(bf16_bits(r.standard_normal((n, k), dtype=np.float32) * 0.02))
+    in_scale = np.float32(448.0) / np.float32(np.abs(bf16_to_f32(a_bits)).max())
+    w_scale = np.float32(448.0) / np.float32(np.abs(w).max())
+    out_scale = float(np.float32(1.0) / (in_scale * w_scale))
+    w_codes = O.quantize_f32(w, float(w_scale))
+
+    # activation codes on the GPU, bit-exact on all 4 Mi elements
+    a_dev = dev(a_bits)
+    codes = empty((m, k), np.uint8)
+    N.call("evo_hip_e4m3_quantize", N.DTYPE_BF16, p(a_dev), m * k, float(in_scale), p(codes),
+           stream())
+    expected_codes = np.zeros((m, k), np.uint8)
+    O.lib().oracle_e4m3_quantize_bf16(O.ptr(a_bits), m * k, float(in_scale),
+                                      O.ptr(expected_codes))
+    a_codes = host(codes)
+    assert np.array_equal(a_codes, expected_codes)
+
+    import torch
+    w_dev = dev(w_codes)
+    results = {}
+    for mode in (N.FP8_EXACT, N.FP8_MFMA_K32, N.FP8_MFMA_K128):
+        out = empty((m, n))
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        N.call("evo_hip_fp8_linear", p(codes), p(w_dev), p(out), m, n, k, out_scale, mode,
+               stream())
+        end.record()
+        torch.cuda.synchronize()
+        results[mode] = host(out)
+        say(f"config 3 mode {mode}: {start.elapsed_time(end):.3f} ms (first call)")
+
+    rows = np.unique(np.concatenate([[0, m - 1], rng(3001).choice(m, 62, replace=False)]))
+    expected = O.qgmma(expected_codes[rows], w_codes, out_scale)
+    assert np.array_equal(results[N.FP8_EXACT][rows].view(np.uint32), expected.view(np.uint32))
+    rms = np.sqrt(np.mean(expected.astype(np.float64) ** 2))
+    for mode, bound in ((N.FP8_MFMA_K32, 2.0 ** -7), (N.FP8_MFMA_K128, 2.0 ** -8)):
+        diff = results[mode][rows].astype(np.float64) - expected
+        say(f"config 3 mode {mode}: rms dev {np.sqrt(np.mean(diff ** 2)) / rms:.3g} of rms, "
+            f"max {np.abs(diff).max() / np.abs(expected).max():.3g} of max")
+        assert np.sqrt(np.mean(diff ** 2)) <= bound * rms
+        assert np.abs(diff).max() <= 2.0 ** -6 * np.abs(expected).max()
+
+
+# -------------------------------------------------------------- config 4
+@pytest.fixture(scope="module")
+def hip():
+    return capi.EvoLibrary(LIB)
+
+
+def open_context(hip, path, capacity, flags=0, model_flags=0, arena=None):
+    if arena:
+        os.environ["EVO_HIP_ARENA_ROWS"] = str(arena)
+    try:
+        model = hip.load(path, capi.BACKEND_HIP, flags=model_flags)
+        params = hip.lib.evo_context_default_params()
+        params.context_size = capacity
+        params.flags = flags
+        handle = ctypes.c_void_p()
+        hip.check(hip.lib.evo_context_create(model.handle, ctypes.byref(params),
+                                             ctypes.byref(handle)))
+        return capi.Context(model, handle)
+    finally:
+        os.environ.pop("EVO_HIP_ARENA_ROWS", None)
+
+
+def relmax(a, b):
+    return float(np.abs(a.astype(np.float64) - b).max() / np.abs(b).max())
+
+
+@pytest.fixture(scope="module")
+def one_of_each_7b(tmp_path_factory):
+    """7B-width blocks: 0 HCS, 1 HCM, 2 HCL, 3 attention."""
+    shape = A.tiny_shape(width=4096, layers=4, heads=32, inner=11264, groups=256, attn=(3,),
+                         rope_scale=128.0, model_id="random-init-evo2-7b-width-4-blocks")
+    path = str(tmp_path_factory.mktemp("w4096") / "one_of_each.safetensors")
+    A.random_artifact(shape, seed=4, init="survey").write(path)
+    return path
+
+
+def test_config4_one_block_of_each_mixer_at_7b_width(hip, one_of_each_7b):
+    tokens = A.acgt_tokens(8192, seed=4)
+    sequence = tokens.astype(np.uint8).tobytes()
+    t0 = time.time()
+    expected, blocks = O.OracleModel(one_of_each_7b).prefill(
+        tokens, chunk=8192, threads=THREADS, capture_layer="all")
+    say(f"config 4 (4 blocks, 8192 tokens): oracle {time.time() - t0:.1f} s")
+    logits = open_context(hip, one_of_each_7b, 8192).prefill(sequence)
+    error = relmax(logits, expected)
+    say(f"  logits max err {error:.3g}, top-1 {np.mean(logits.argmax(1) == expected.argmax(1))}")
+    assert error <= 1e-3
+    assert np.array_equal(logits.argmax(1), expected.argmax(1))
+    previous = None
+    for layer in range(4):
+        hidden = open_context(hip, one_of_each_7b, 8192).embed(sequence, layer)
+        block_error = relmax(hidden, blocks[layer])
+        line = f"  block {layer}: output max err {block_error:.3g}"
+        assert block_error <= 1e-3
+        if previous is not None:
+            # the block's own contribution to the residual stream
+            delta_error = relmax(hidden - previous[0], blocks[layer] - previous[1])
+            line += f", contribution max err {delta_error:.3g}"
+            assert delta_error <= 1e-3
+        say(line)
+        previous = (hidden, blocks[layer])
+
+
+@pytest.fixture(scope="module")
+def evo2_7b(tmp_path_factory):
+    path = str(tmp_path_factory.mktemp("evo2_7b") / "evo2_7b.safetensors")
+    t0 = time.time()
+    A.random_artifact(A.evo2_7b_shape(), seed=7, init="survey").write(path)
+    say(f"7B artifact written in {time.time() - t0:.0f} s")
+    return path
+
+
+def resident_prefill(hip, path, tokens, arena=None, flags=0, model_flags=0):
+    """Logits of one prefill with tokens and logits in device memory."""
+    ctx = open_context(hip, path, len(tokens), flags=flags, model_flags=model_flags,
+                       arena=arena)
+    ids = dev(tokens.astype(np.uint32))
+    logits = empty((len(tokens), 512))
+    N.call("evo_hip_context_prefill_resident", ctx.handle, p(ids), len(tokens), p(logits))
+    return host(logits)
+
+
+@pytest.mark.parametrize("length", [1024, 8192])
+def test_config4_full_7b_arena_and_determinism(hip, evo2_7b, length):
+    tokens = A.acgt_tokens(length, seed=length)
+    whole = resident_prefill(hip, evo2_7b, tokens)
+    again = resident_prefill(hip, evo2_7b, tokens)
+    chunked = resident_prefill(hip, evo2_7b, tokens, arena=1024 if length > 1024 else 256)
+    assert np.isfinite(whole).all()
+    assert np.array_equal(whole.view(np.uint32), again.view(np.uint32))
+    error = relmax(chunked, whole)
+    say(f"config 4 full 7B, {length} tokens: arena max err {error:.3g}")
+    assert error <= 1e-5
+
+
+def test_config4_full_7b_fp8_projections(hip, evo2_7b):
+    """The benchmarked configuration (FP8 projections converted at load, MFMA
+    K128): deterministic, finite, and close to the hip-f32 profile."""
+    tokens = A.acgt_tokens(8192, seed=8)
+    fp8 = resident_prefill(hip, evo2_7b, tokens, model_flags=1 << 8)
+    assert np.isfinite(fp8).all()
+    assert np.array_equal(fp8.view(np.uint32),
+                          resident_prefill(hip, evo2_7b, tokens, model_flags=1 << 8)
+                          .view(np.uint32))
+    f32 = resident_prefill(hip, evo2_7b, tokens)
+    agree = float(np.mean(fp8.argmax(1) == f32.argmax(1)))
+    say(f"config 4 FP8 K128 vs hip-f32: max err {relmax(fp8, f32):.3g}, top-1 {agree}")
+    assert agree == 1.0
+
+
+# -------------------------------------------------------------- config 5
+def test_config5_131072_tokens_arena_consistency(hip, evo2_7b):
+    tokens = A.acgt_tokens(131072, seed=5)
+    whole = resident_prefill(hip, evo2_7b, tokens)
+    assert np.isfinite(whole).all()
+    chunked = resident_prefill(hip, evo2_7b, tokens, arena=4096)
+    error = relmax(chunked, whole)
+    say(f"config 5 (131072 tokens): arena 4096 vs 8192 max err {error:.3g}")
+    assert error <= 1e-5

@@ -322,8 +322,24 @@ def planar(proj):
                                 .reshape(rows, cols))
 
 
+CANARY = 0x7FC0DEAD  # a NaN payload no kernel writes
+
+
+def guarded(shape, dtype, guard):
+    """Output buffer with `guard` canary rows after it; returns (full, view)."""
+    rows = int(np.prod(shape[:-1]))
+    full = dev(np.full((rows + guard) * shape[-1] * np.dtype(dtype).itemsize // 4, CANARY,
+                       np.uint32))
+    return full, full.view(dev_dtype(dtype))[:rows * shape[-1]].view(shape)
+
+
+def dev_dtype(dtype):
+    import torch
+    return {np.float32: torch.float32, np.uint16: torch.int16}[np.dtype(dtype).type]
+
+
 def hyena_gpu(kind, case, dtype=N.DTYPE_F32, rows=None, caches=None, projection=None,
-              planar_layout=False, bf16_taps=False):
+              planar_layout=False, bf16_taps=False, guard=0):
     proj = case["projection"] if projection is None else projection
     if planar_layout:
         proj = planar(proj)
@@ -333,18 +349,17 @@ def hyena_gpu(kind, case, dtype=N.DTYPE_F32, rows=None, caches=None, projection=
     poles = np.exp(case["log_poles"]).astype(np.float32) if "log_poles" in case else None
     ws_bytes = N.call("evo_hip_hyena_workspace_bytes", kind, length, width, state)
     ws = empty((max(ws_bytes, 256),), np.uint8)
+    out_shape, out_type = ((length, width), np.float32)
     if dtype == N.DTYPE_BF16:
-        proj_d = dev(bf16_bits(proj))
-        out = empty((length, width), np.uint16)
-    elif dtype == N.DTYPE_SPLIT:
-        proj_d = dev(proj)
-        out = empty((2, length, width), np.uint16)
-    elif dtype == N.DTYPE_BF16_SPLIT:
-        proj_d = dev(bf16_bits(proj))
-        out = empty((2, length, width), np.uint16)
+        out_shape, out_type = (length, width), np.uint16
+    elif dtype in (N.DTYPE_SPLIT, N.DTYPE_BF16_SPLIT):
+        out_shape, out_type = (2, length, width), np.uint16
+    proj_d = dev(bf16_bits(proj) if dtype in (N.DTYPE_BF16, N.DTYPE_BF16_SPLIT) else proj)
+    full = None
+    if guard:
+        full, out = guarded(out_shape, out_type, guard)
     else:
-        proj_d = dev(proj)
-        out = empty((length, width))
+        out = empty(out_shape, out_type)
     caches = caches or {}
     flags = (N.DTYPE_PLANAR if planar_layout else 0) | (N.DTYPE_BF16_TAPS if bf16_taps else 0)
     N.call("evo_hip_hyena_forward", kind, dtype | flags,
@@ -357,6 +372,9 @@ def hyena_gpu(kind, case, dtype=N.DTYPE_F32, rows=None, caches=None, projection=
            p(caches.get("short")), p(caches.get("inner")), p(caches.get("modal")),
            p(ws), ws_bytes, p(out), stream())
     result = host(out)
+    if guard:
+        tail = host(full)[out.numel() * np.dtype(out_type).itemsize // 4:]
+        assert np.all(tail == CANARY), "rows past the output were written"
     if dtype in (N.DTYPE_SPLIT, N.DTYPE_BF16_SPLIT):
         planes = bf16_to_f32(result.view(np.uint16))
         return planes[0].astype(np.float64) + planes[1]
@@ -393,6 +411,27 @@ def test_hyena_fir_mfma_matches_oracle(kind, inner_len, length, width, groups):
     actual = hyena_gpu(kind, case, dtype=N.DTYPE_BF16_SPLIT, projection=proj,
                        planar_layout=True)
     assert rel_err(actual, expected) < 2e-5
+
+
+@pytest.mark.parametrize("kind,inner_len", KINDS)
+@pytest.mark.parametrize("dtype", [N.DTYPE_F32, N.DTYPE_BF16, N.DTYPE_SPLIT,
+                                   N.DTYPE_BF16_SPLIT])
+@pytest.mark.parametrize("length", [2, 3, 295, 1025, 1031])
+def test_hyena_leaves_rows_past_the_output(kind, inner_len, dtype, length):
+    """Rows past the sequence end (the last chunk / segment / store pair is
+    ragged: lengths not a multiple of 4) are never written: 64 canary rows
+    after the output stay intact, and the rows inside match the oracle.
+    Lengths 2 and 3 reach the prefill kernels' smallest chunks (a single row
+    runs the decode kernel)."""
+    case = hyena_case(3 * length + kind, kind, length, 64, groups=4, inner_len=inner_len or 7)
+    proj = case["projection"]
+    if dtype in (N.DTYPE_BF16, N.DTYPE_BF16_SPLIT):
+        proj = bf16_to_f32(bf16_bits(proj))
+    expected = hyena_oracle(kind, case, projection=proj)
+    actual = hyena_gpu(kind, case, dtype=dtype, projection=proj, guard=64,
+                       bf16_taps=kind == N.HYENA_HCM)
+    bound = 2.0 ** -8 if dtype == N.DTYPE_BF16 else 2e-5
+    assert rel_err(actual, expected) < bound
 
 
 @pytest.mark.parametrize("kind,inner_len", KINDS)

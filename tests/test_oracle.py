@@ -329,3 +329,55 @@ def test_oracle_capture_matches_next_layer_input(tmp_path):
     logits, hidden = model.prefill(tokens, capture_layer=3)
     assert hidden.shape == (20, 64) and np.isfinite(hidden).all()
     assert np.array_equal(model.prefill(tokens), logits)
+
+
+def test_qgmma_matches_bruteforce_on_quantised_normals():
+    """Codes of quantised N(0, 1) activations and N(0, 0.02) weights (the
+    config-3 distributions: many binades, subnormal codes, accumulators that
+    grow across 16 groups of 32), against the rational restatement."""
+    r = np.random.Generator(np.random.PCG64(12))
+    x = r.standard_normal((4, 512)).astype(np.float32)
+    w = (r.standard_normal((6, 512)) * 0.02).astype(np.float32)
+    x[:, ::37] *= 1e-4  # a few values in the subnormal code range
+    w[:, ::41] *= 1e-4
+    a = O.quantize_f32(x, 448.0 / float(np.abs(x).max()))
+    b = O.quantize_f32(w, 448.0 / float(np.abs(w).max()))
+    assert np.any((a & 0x78) == 0) and np.any((b & 0x78) == 0)  # subnormal codes present
+    out = O.qgmma(a, b, 0.0078125)
+    da, dw = _decode(a), _decode(b)
+    for i in range(4):
+        for j in range(6):
+            assert out[i, j] == _qgmma_bruteforce(da[i], dw[j], 0.0078125)
+
+
+def test_oracle_fp8_conversion_matches_artifact_codes(tmp_path):
+    """oracle_model_convert_fp8 (load-time conversion of BF16 projections)
+    equals the same model written with codes and scales from the numpy
+    encoder: weight_scale = 448 / amax(W), codes = E4M3(W * scale), input
+    scale 448 / 8, output scale 1 / (input * weight)."""
+    from evo_hip.fp8 import e4m3_encode
+    shape = A.tiny_shape(width=64, layers=4, heads=4, inner=64, groups=16, attn=(3,))
+    art = A.random_artifact(shape, seed=9)
+    bf16_path = str(tmp_path / "bf16.safetensors")
+    art.write(bf16_path)
+    for index, spec in enumerate(list(art.specs)):
+        if not spec.name.endswith(".projections.weight"):
+            continue
+        bits = art._make(index)
+        weight = A.bf16_to_f32(bits)
+        weight_scale = np.float32(448.0) / np.float32(np.abs(weight).max())
+        input_scale = np.float32(448.0 / 8.0)
+        codes = e4m3_encode(weight * weight_scale)
+        scales = np.array([input_scale, np.float32(1) / (input_scale * weight_scale)],
+                          np.float32)
+        art.specs[index] = A.TensorSpec(spec.name, "F8_E4M3", spec.shape,
+                                        lambda rng, c=codes: c)
+        art.add(spec.name.replace(".weight", ".fp8_runtime_scales"), "F32", (2,),
+                lambda rng, s=scales: s)
+    fp8_path = str(tmp_path / "fp8.safetensors")
+    art.write(fp8_path)
+    tokens = A.acgt_tokens(40, seed=9)
+    converted = O.OracleModel(bf16_path).convert_fp8(8.0).prefill(tokens)
+    written = O.OracleModel(fp8_path).prefill(tokens)
+    assert np.array_equal(converted.view(np.uint32), written.view(np.uint32))
+    assert not np.array_equal(converted, O.OracleModel(bf16_path).prefill(tokens))
