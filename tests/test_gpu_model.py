@@ -6,8 +6,9 @@ artifacts, and against logits the reference's own CPU build produced
 Tolerance (stated once, used below): logits and captured block outputs
 satisfy max|hip - ref| <= 1e-3 * max|ref| ("hip-f32" profile), top-1
 agreement 100 %. FP8-projection models compare with the oracle's
-FP8 semantics (codes bit-exact, QGMMA accumulation) at 1e-2 * max|ref|,
-because an E8M13 ulp difference can flip a downstream E4M3 code.
+FP8 semantics (codes bit-exact, QGMMA accumulation) at the measured envelope
+stated per test, because an E8M13 ulp difference can flip a downstream E4M3
+code.
 """
 import os
 
@@ -97,21 +98,33 @@ def test_fp8_projection_model_exact(hip, tmp_path):
     path, tokens, expected = fp8_model(tmp_path)
     actual, profile = run_hip(hip, path, tokens, flags=1 << 9)
     assert profile == "hip-f32+fp8-exact"
-    assert relmax(actual, expected) <= 1e-2
-    assert np.mean(actual.argmax(1) == expected.argmax(1)) >= 0.99
+    # Measured: relmax 0.0097, top-1 100 %. The "unit" init gives every
+    # block an O(1) contribution, so each E4M3 code that a one-ulp F32
+    # difference upstream flips moves the logits visibly (at 7B width with
+    # the benchmark init the same mode is within 4e-5: test_gpu_configs.py).
+    assert relmax(actual, expected) <= 1.5e-2
+    assert np.array_equal(actual.argmax(1), expected.argmax(1))
 
 
 def test_fp8_projection_model_mfma(hip, tmp_path):
-    """E4M3 MFMA path (approximate profile): one-ulp BF16 differences of the
-    projection flip downstream E4M3 codes, so the envelope is the reference's
-    approximate-profile style: logits cosine >= 0.999, top-1 >= 95 %."""
+    """E4M3 MFMA path with promotion every 128 K (the benchmarked mode): the
+    MFMA does not reproduce QGMMA's per-term truncation, so projections differ
+    by about one BF16 ulp and downstream E4M3 codes flip; with the "unit"
+    init each flip moves the logits visibly. Measured: relmax 0.0345, cosine
+    0.99966, top-1 98.7 % (2 of 150 rows, near ties). Bounds: that envelope
+    with margin (relmax 0.06, cosine 0.9993, top-1 97 %). At 7B width with the
+    benchmark init this mode is within 4e-5 and top-1 100 %
+    (test_gpu_configs.py::test_fp8_projection_modes_at_7b_width)."""
     path, tokens, expected = fp8_model(tmp_path)
     actual, profile = run_hip(hip, path, tokens)
     cosine = float((actual.ravel() @ expected.ravel()) /
                    (np.linalg.norm(actual) * np.linalg.norm(expected)))
-    print(f"fp8 mfma model: relmax {relmax(actual, expected):.3g} cosine {cosine:.6f}")
-    assert cosine >= 0.999
-    assert np.mean(actual.argmax(1) == expected.argmax(1)) >= 0.95
+    top1 = float(np.mean(actual.argmax(1) == expected.argmax(1)))
+    print(f"fp8 mfma model: relmax {relmax(actual, expected):.3g} cosine {cosine:.6f} "
+          f"top-1 {top1}")
+    assert relmax(actual, expected) <= 0.06
+    assert cosine >= 0.9993
+    assert top1 >= 0.97
 
 
 def test_golden_reference_logits(hip, tmp_path):
@@ -126,11 +139,14 @@ def test_golden_reference_logits(hip, tmp_path):
     assert np.array_equal(actual.argmax(1), golden["logits"].argmax(1))
 
 
-def test_evo2_1b_shape_config1(hip, tmp_path):
-    """1B-shaped SH2 (25 blocks, W 1920, 15 heads, FFN 5120),
-    128 ACGT tokens, seeded random-init weights."""
+@pytest.mark.parametrize("init", ["survey", "unit"])
+def test_evo2_1b_shape_config1(hip, tmp_path, init):
+    """Config 1: 1B-shaped SH2 (25 blocks, W 1920, 15 heads, FFN 5120), 128
+    ACGT tokens, seeded random-init weights: the benchmark distributions
+    ("survey") and the "unit" init, whose O(1) block contributions make any
+    kernel error visible in the logits."""
     shape = A.evo2_1b_shape()
-    path = make(tmp_path, shape, seed=1, init="unit")
+    path = make(tmp_path, shape, seed=1, init=init)
     tokens = A.acgt_tokens(128, seed=1)
     expected = O.OracleModel(path).prefill(tokens, threads=16)
     actual, _ = run_hip(hip, path, tokens)
