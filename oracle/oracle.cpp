@@ -150,15 +150,17 @@ float dot_bf16(const float *const input, const uint16_t *const weight,
 }
 
 // Dots of a tile of rows x targets, each bit-identical to dot_bf16 of that
-// pair: the AVX2 path runs 4 rows x 2 targets as eight independent chains of
+// pair: the AVX2 path runs 6 rows x 2 targets as twelve independent chains of
 // the same FMA sequence (one chain per output, so FMA latency is hidden
 // without changing any output's order of operations).
+constexpr int kDotRows = 6;
+constexpr size_t kTileRows = 8 * kDotRows;
 #if defined(__x86_64__)
 __attribute__((target("avx2,fma"))) void
-dot_block_4x2_avx2(const float *const *input, const uint16_t *const *weight,
-                   const std::size_t size, float result[4][2]) {
-  __m256 total[4][2];
-  for (int r = 0; r < 4; ++r)
+dot_block_avx2(const float *const *input, const uint16_t *const *weight,
+                   const std::size_t size, float result[kDotRows][2]) {
+  __m256 total[kDotRows][2];
+  for (int r = 0; r < kDotRows; ++r)
     for (int t = 0; t < 2; ++t)
       total[r][t] = _mm256_setzero_ps();
   std::size_t index = 0;
@@ -169,13 +171,13 @@ dot_block_4x2_avx2(const float *const *input, const uint16_t *const *weight,
           _mm_loadu_si128(reinterpret_cast<const __m128i *>(weight[t] + index));
       w[t] = _mm256_castsi256_ps(_mm256_slli_epi32(_mm256_cvtepu16_epi32(packed), 16));
     }
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < kDotRows; ++r) {
       const __m256 x = _mm256_loadu_ps(input[r] + index);
       for (int t = 0; t < 2; ++t)
         total[r][t] = _mm256_fmadd_ps(x, w[t], total[r][t]);
     }
   }
-  for (int r = 0; r < 4; ++r)
+  for (int r = 0; r < kDotRows; ++r)
     for (int t = 0; t < 2; ++t) {
       alignas(32) float lanes[8];
       _mm256_store_ps(lanes, total[r][t]);
@@ -196,20 +198,21 @@ void dot_tile_bf16(const float *x, const uint16_t *w, size_t in, size_t r0,
 #if defined(__x86_64__)
   static const bool avx2 = cpu_has_avx2_fma();
   if (avx2) {
-    for (; row + 4 <= r1; row += 4) {
+    for (; row + kDotRows <= r1; row += kDotRows) {
       size_t target = c0;
       for (; target + 2 <= c1; target += 2) {
-        const float *inputs[4] = {x + row * in, x + (row + 1) * in,
-                                  x + (row + 2) * in, x + (row + 3) * in};
+        const float *inputs[kDotRows];
+        for (int r = 0; r < kDotRows; ++r)
+          inputs[r] = x + (row + r) * in;
         const uint16_t *weights[2] = {w + target * in, w + (target + 1) * in};
-        float result[4][2];
-        dot_block_4x2_avx2(inputs, weights, in, result);
-        for (int r = 0; r < 4; ++r)
+        float result[kDotRows][2];
+        dot_block_avx2(inputs, weights, in, result);
+        for (int r = 0; r < kDotRows; ++r)
           for (int t = 0; t < 2; ++t)
             out[(row + r) * ldo + target + t] = result[r][t];
       }
       for (; target < c1; ++target)
-        for (size_t r = row; r < row + 4; ++r)
+        for (size_t r = row; r < row + kDotRows; ++r)
           out[r * ldo + target] = dot_bf16(x + r * in, w + target * in, in);
     }
   }
@@ -560,15 +563,16 @@ void linear_model(const std::vector<float> &input, size_t rows, size_t in,
                   const Tensor &weight, size_t out_width, const Tensor *bias,
                   std::vector<float> *output, int threads) {
   output->assign(rows * out_width, 0.0F);
-  // Tiles of 32 rows x 32 outputs keep one weight panel cache-resident while
+  // Tiles of 48 rows x 32 outputs keep one weight panel cache-resident while
   // the rows sweep it; every output is still one dot in the reference order.
-  const size_t row_tiles = (rows + 31) / 32, col_tiles = (out_width + 31) / 32;
+  const size_t row_tiles = (rows + kTileRows - 1) / kTileRows,
+               col_tiles = (out_width + 31) / 32;
   const long long tiles = static_cast<long long>(row_tiles * col_tiles);
 #pragma omp parallel for schedule(dynamic, 1) num_threads(threads > 0 ? threads : 1)
   for (long long tile = 0; tile < tiles; ++tile) {
-    const size_t r0 = static_cast<size_t>(tile) / col_tiles * 32;
+    const size_t r0 = static_cast<size_t>(tile) / col_tiles * kTileRows;
     const size_t c0 = static_cast<size_t>(tile) % col_tiles * 32;
-    const size_t r1 = std::min(r0 + 32, rows), c1 = std::min(c0 + 32, out_width);
+    const size_t r1 = std::min(r0 + kTileRows, rows), c1 = std::min(c0 + 32, out_width);
     if (weight.dtype == "BF16")
       dot_tile_bf16(input.data(), weight.bf16(), in, r0, r1, c0, c1,
                     output->data(), out_width);
@@ -751,6 +755,10 @@ void attention_model(const Model &m, const std::vector<float> &projected,
   output->assign(rows * width, 0.0F);
   const float score_scale = 1.0F / std::sqrt(static_cast<float>(head_dim));
   const long long jobs = static_cast<long long>(rows * m.heads);
+  // Each score and each output element keeps the reference's sequential
+  // order; independent chains are interleaved (eight keys per step for the
+  // scores, all head dimensions per key for P.V) so that latency, not the
+  // order of operations, is what changes.
 #pragma omp parallel for schedule(dynamic, 1)
   for (long long job = 0; job < jobs; ++job) {
     const size_t row = static_cast<size_t>(job) / m.heads;
@@ -758,26 +766,38 @@ void attention_model(const Model &m, const std::vector<float> &projected,
     const size_t sources = prefix + row + 1;
     std::vector<float> scores(sources);
     const size_t query_base = row * width + head * head_dim;
+    const float *q = query.data() + query_base;
     float maximum = -std::numeric_limits<float>::infinity();
-    for (size_t source = 0; source < sources; ++source) {
+    size_t source = 0;
+    for (; source + 8 <= sources; source += 8) {
+      float score[8] = {};
+      const float *k = cache->key.data() + source * width + head * head_dim;
+      for (size_t dimension = 0; dimension < head_dim; ++dimension)
+        for (size_t j = 0; j < 8; ++j)
+          score[j] += q[dimension] * k[j * width + dimension];
+      for (size_t j = 0; j < 8; ++j)
+        scores[source + j] = score[j] * score_scale;
+    }
+    for (; source < sources; ++source) {
       float score = 0.0F;
       const size_t key_base = source * width + head * head_dim;
       for (size_t dimension = 0; dimension < head_dim; ++dimension)
-        score += query[query_base + dimension] * cache->key[key_base + dimension];
+        score += q[dimension] * cache->key[key_base + dimension];
       scores[source] = score * score_scale;
-      maximum = std::max(maximum, scores[source]);
     }
+    for (source = 0; source < sources; ++source)
+      maximum = std::max(maximum, scores[source]);
     float denominator = 0.0F;
     for (auto &score : scores) {
       score = std::exp(score - maximum);
       denominator += score;
     }
-    for (size_t dimension = 0; dimension < head_dim; ++dimension) {
-      float total = 0.0F;
-      for (size_t source = 0; source < sources; ++source)
-        total += scores[source] / denominator *
-                 cache->value[source * width + head * head_dim + dimension];
-      (*output)[query_base + dimension] = total;
+    float *total = output->data() + query_base;  // zero-initialised above
+    for (source = 0; source < sources; ++source) {
+      const float weight = scores[source] / denominator;
+      const float *v = cache->value.data() + source * width + head * head_dim;
+      for (size_t dimension = 0; dimension < head_dim; ++dimension)
+        total[dimension] += weight * v[dimension];
     }
   }
 }
@@ -1119,13 +1139,14 @@ int oracle_causal_attention(const float *q, const float *k, const float *v,
 int oracle_linear_bf16w(const float *x, size_t rows, size_t in_features,
                         const uint16_t *weight, size_t out_features,
                         const uint16_t *bias, float *out, int threads) {
-  const size_t row_tiles = (rows + 31) / 32, col_tiles = (out_features + 31) / 32;
+  const size_t row_tiles = (rows + kTileRows - 1) / kTileRows,
+               col_tiles = (out_features + 31) / 32;
   const long long tiles = static_cast<long long>(row_tiles * col_tiles);
 #pragma omp parallel for schedule(dynamic, 1) num_threads(threads > 0 ? threads : 1)
   for (long long tile = 0; tile < tiles; ++tile) {
-    const size_t r0 = static_cast<size_t>(tile) / col_tiles * 32;
+    const size_t r0 = static_cast<size_t>(tile) / col_tiles * kTileRows;
     const size_t c0 = static_cast<size_t>(tile) % col_tiles * 32;
-    const size_t r1 = std::min(r0 + 32, rows), c1 = std::min(c0 + 32, out_features);
+    const size_t r1 = std::min(r0 + kTileRows, rows), c1 = std::min(c0 + 32, out_features);
     dot_tile_bf16(x, weight, in_features, r0, r1, c0, c1, out, out_features);
     if (bias != nullptr)
       for (size_t row = r0; row < r1; ++row)
