@@ -588,6 +588,39 @@ size_t evo_hip_hyena_workspace_bytes(evo_hip_hyena_kind kind, size_t length, siz
   return evo::hip::hyena_workspace_bytes(static_cast<int>(kind), length, width, state_size);
 }
 
+namespace {
+// Typed dispatch shared by the workspace and the static-scratch entry points.
+evo::Status hyena_dispatch(evo_hip_hyena_kind kind, evo_hip_dtype dtype,
+                           const void *projection, size_t length, size_t width,
+                           const evo::hip::HyenaWeights &w, float *short_history,
+                           float *inner_history, float *modal_state, void *workspace,
+                           size_t workspace_bytes, void *output, hipStream_t s) {
+  const bool planar = (static_cast<int>(dtype) & EVO_HIP_PLANAR) != 0;
+  dtype = static_cast<evo_hip_dtype>(static_cast<int>(dtype) &
+                                     ~(EVO_HIP_PLANAR | EVO_HIP_BF16_TAPS));
+  if (dtype == EVO_HIP_F32)
+    return evo::hip::hyena_forward<float, float *>(
+        kind, static_cast<const float *>(projection), length, width, planar, w, short_history,
+        inner_history, modal_state, workspace, workspace_bytes, static_cast<float *>(output), s);
+  if (dtype == EVO_HIP_BF16)
+    return evo::hip::hyena_forward<uint16_t, uint16_t *>(
+        kind, static_cast<const uint16_t *>(projection), length, width, planar, w, short_history,
+        inner_history, modal_state, workspace, workspace_bytes,
+        static_cast<uint16_t *>(output), s);
+  auto *hi = static_cast<uint16_t *>(output);
+  const evo::hip::SplitOut split{hi, hi == nullptr ? nullptr : hi + length * width};
+  if (dtype == EVO_HIP_SPLIT)
+    return evo::hip::hyena_forward<float, evo::hip::SplitOut>(
+        kind, static_cast<const float *>(projection), length, width, planar, w, short_history,
+        inner_history, modal_state, workspace, workspace_bytes, split, s);
+  if (dtype == EVO_HIP_BF16_SPLIT)
+    return evo::hip::hyena_forward<uint16_t, evo::hip::SplitOut>(
+        kind, static_cast<const uint16_t *>(projection), length, width, planar, w, short_history,
+        inner_history, modal_state, workspace, workspace_bytes, split, s);
+  return {evo::ErrorCode::kInvalidArgument, "invalid_argument: unknown dtype"};
+}
+}  // namespace
+
 evo_status evo_hip_hyena_forward(evo_hip_hyena_kind kind, evo_hip_dtype dtype,
                                  const void *projection, size_t length, size_t width,
                                  const uint16_t *short_filter, size_t short_len,
@@ -598,38 +631,46 @@ evo_status evo_hip_hyena_forward(evo_hip_hyena_kind kind, evo_hip_dtype dtype,
                                  float *modal_state, void *workspace, size_t workspace_bytes,
                                  void *output, void *stream) {
   return protect([&]() -> evo_status {
-    const bool planar = (static_cast<int>(dtype) & EVO_HIP_PLANAR) != 0;
     const bool taps_bf16 = (static_cast<int>(dtype) & EVO_HIP_BF16_TAPS) != 0;
-    evo::hip::HyenaWeights w{short_filter, short_len, inner_filter, groups, inner_len,
-                             direct, poles, residues, state_size, taps_bf16};
-    const auto s = static_cast<hipStream_t>(stream);
-    dtype = static_cast<evo_hip_dtype>(static_cast<int>(dtype) &
-                                       ~(EVO_HIP_PLANAR | EVO_HIP_BF16_TAPS));
-    if (dtype == EVO_HIP_F32)
-      return publish(evo::hip::hyena_forward<float, float *>(
-          kind, static_cast<const float *>(projection), length, width, planar, w, short_history,
-          inner_history, modal_state, workspace, workspace_bytes,
-          static_cast<float *>(output), s));
-    if (dtype == EVO_HIP_BF16)
-      return publish(evo::hip::hyena_forward<uint16_t, uint16_t *>(
-          kind, static_cast<const uint16_t *>(projection), length, width, planar, w, short_history,
-          inner_history, modal_state, workspace, workspace_bytes,
-          static_cast<uint16_t *>(output), s));
-    if (dtype == EVO_HIP_SPLIT) {
-      auto *hi = static_cast<uint16_t *>(output);
-      return publish(evo::hip::hyena_forward<float, evo::hip::SplitOut>(
-          kind, static_cast<const float *>(projection), length, width, planar, w, short_history,
-          inner_history, modal_state, workspace, workspace_bytes,
-          evo::hip::SplitOut{hi, hi == nullptr ? nullptr : hi + length * width}, s));
-    }
-    if (dtype == EVO_HIP_BF16_SPLIT) {
-      auto *hi = static_cast<uint16_t *>(output);
-      return publish(evo::hip::hyena_forward<uint16_t, evo::hip::SplitOut>(
-          kind, static_cast<const uint16_t *>(projection), length, width, planar, w, short_history,
-          inner_history, modal_state, workspace, workspace_bytes,
-          evo::hip::SplitOut{hi, hi == nullptr ? nullptr : hi + length * width}, s));
-    }
-    return publish(EVO_STATUS_INVALID_ARGUMENT, "invalid_argument: unknown dtype");
+    const evo::hip::HyenaWeights w{short_filter, short_len, inner_filter, groups, inner_len,
+                                   direct, poles, residues, state_size, taps_bf16};
+    return publish(hyena_dispatch(kind, dtype, projection, length, width, w, short_history,
+                                  inner_history, modal_state, workspace, workspace_bytes,
+                                  output, static_cast<hipStream_t>(stream)));
+  });
+}
+
+size_t evo_hip_hyena_static_scratch_bytes(void) { return evo::hip::kHyenaStaticScratchBytes; }
+
+evo_status evo_hip_hyena_forward_static(evo_hip_hyena_kind kind, evo_hip_dtype dtype,
+                                        const void *projection, size_t length, size_t width,
+                                        const uint16_t *short_filter, size_t short_len,
+                                        const float *inner_filter, size_t groups,
+                                        size_t inner_len, const float *direct,
+                                        const float *poles, const float *residues,
+                                        size_t state_size, float *short_history,
+                                        float *inner_history, float *modal_state, void *output,
+                                        void *stream) {
+  return protect([&]() -> evo_status {
+    const size_t needed = evo::hip::hyena_workspace_bytes(static_cast<int>(kind), length,
+                                                          width, state_size);
+    if (needed > evo::hip::kHyenaStaticScratchBytes)
+      return publish(EVO_STATUS_INVALID_ARGUMENT,
+                     "invalid_argument: operator needs " + std::to_string(needed) +
+                         " bytes of workspace, more than the static scratch's " +
+                         std::to_string(evo::hip::kHyenaStaticScratchBytes) +
+                         "; use evo_hip_hyena_forward with a workspace");
+    void *scratch = nullptr;
+    const auto found = evo::hip::hyena_static_scratch(&scratch);
+    if (!found.ok())
+      return publish(found);
+    const bool taps_bf16 = (static_cast<int>(dtype) & EVO_HIP_BF16_TAPS) != 0;
+    const evo::hip::HyenaWeights w{short_filter, short_len, inner_filter, groups, inner_len,
+                                   direct, poles, residues, state_size, taps_bf16};
+    return publish(hyena_dispatch(kind, dtype, projection, length, width, w, short_history,
+                                  inner_history, modal_state, scratch,
+                                  evo::hip::kHyenaStaticScratchBytes, output,
+                                  static_cast<hipStream_t>(stream)));
   });
 }
 

@@ -21,6 +21,8 @@
 #include "common.hpp"
 #include "ops.hpp"
 
+#include <mutex>
+
 namespace evo::hip {
 namespace {
 
@@ -2076,5 +2078,30 @@ template Status hyena_forward<float, SplitOut>(int, const float *, size_t, size_
                                                const HyenaWeights &, float *, float *,
                                                float *, void *, size_t, SplitOut,
                                                hipStream_t);
+
+// ---- Fixed scratch of the allocation-free operator entry point.
+// One array per device, alive until the process ends. Its host-side name is
+// not a device address: host code only ever uses the address that
+// hipGetSymbolAddress returns for the current device.
+static __device__ __align__(256) unsigned char scratch[kHyenaStaticScratchBytes];
+
+Status hyena_static_scratch(void **address) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mutex;
+  static void *per_device[kMaxDevices] = {};
+  int device = 0;
+  EVO_TRY(hip_status(hipGetDevice(&device), "hyena static scratch: current device"));
+  if (device < 0 || device >= kMaxDevices)
+    return {ErrorCode::kInvalidArgument, "hyena static scratch: device index out of range"};
+  std::lock_guard<std::mutex> lock(mutex);
+  if (per_device[device] == nullptr) {
+    void *ptr = nullptr;
+    EVO_TRY(hip_status(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)),
+                       "hyena static scratch: symbol address"));
+    per_device[device] = ptr;
+  }
+  *address = per_device[device];
+  return Status::Ok();
+}
 
 }  // namespace evo::hip

@@ -110,6 +110,10 @@ struct HyenaWeights {
   size_t state;
   bool taps_bf16;                // every inner tap is a BF16 value (artifact filters)
 };
+// Size of the fixed device scratch behind the allocation-free Hyena entry
+// point, and its address on the current device (resolved once per device).
+constexpr size_t kHyenaStaticScratchBytes = size_t{32} << 20;
+Status hyena_static_scratch(void **address);
 size_t hyena_workspace_bytes(int kind, size_t length, size_t width,
                              size_t state);
 // O: float* (F32 out), uint16_t* (BF16 out) or SplitOut (GEMM planes).

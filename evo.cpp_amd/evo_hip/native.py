@@ -28,6 +28,11 @@ _OPS = {
                                       c_size, c_void, c_size, c_size, c_void, c_void,
                                       c_void, c_size, c_void, c_void, c_void, c_void,
                                       c_size, c_void, c_void]),
+    "evo_hip_hyena_static_scratch_bytes": (c_size, []),
+    "evo_hip_hyena_forward_static": (c_int, [c_int, c_int, c_void, c_size, c_size, c_void,
+                                             c_size, c_void, c_size, c_size, c_void, c_void,
+                                             c_void, c_size, c_void, c_void, c_void, c_void,
+                                             c_void]),
     "evo_hip_e4m3_quantize": (c_int, [c_int, c_void, c_size, c_float, c_void, c_void]),
     "evo_hip_fp8_linear": (c_int, [c_void, c_void, c_void, c_size, c_size, c_size,
                                    c_float, c_int, c_void]),

@@ -94,6 +94,27 @@ EVO_API evo_status evo_hip_hyena_forward(
     float *inner_history, float *modal_state, void *workspace,
     size_t workspace_bytes, void *output, void *stream);
 
+/* Allocation-free variant of evo_hip_hyena_forward: same arguments minus
+ * the workspace, same kernels and results. The workspace comes from a fixed
+ * device array of evo_hip_hyena_static_scratch_bytes() (32 MiB) in the
+ * library, one per device, held until the process ends; the call fails with
+ * EVO_STATUS_INVALID_ARGUMENT when evo_hip_hyena_workspace_bytes() of the
+ * shape exceeds it (HCL at W = 4096, 16 states: up to 16384 rows per call).
+ * The call makes no device allocation (no hipMalloc/hipFree), so callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops) can
+ * use it. Every call on a device shares that device's array: calls that
+ * overlap on one device (different streams, threads) race; serialise them.
+ * No counterpart in the reference: evo.cpp's operators always receive their
+ * scratch from the caller or allocate it. */
+EVO_API size_t evo_hip_hyena_static_scratch_bytes(void);
+EVO_API evo_status evo_hip_hyena_forward_static(
+    evo_hip_hyena_kind kind, evo_hip_dtype dtype, const void *projection,
+    size_t length, size_t width, const uint16_t *short_filter,
+    size_t short_len, const float *inner_filter, size_t groups,
+    size_t inner_len, const float *direct, const float *poles,
+    const float *residues, size_t state_size, float *short_history,
+    float *inner_history, float *modal_state, void *output, void *stream);
+
 /* codes[i] = E4M3FN(float(bf16(x[i])) * scale), RNE, satfinite.
  * Replaces `software_e4m3_quantize_bf16_codes` (`include/evo/cuda/ops.hpp:92-96`). */
 EVO_API evo_status evo_hip_e4m3_quantize(evo_hip_dtype dtype, const void *x,
