@@ -14,9 +14,12 @@
 // ~2^-17) for twice the MFMA work; without lo (profile hip-bf16) one pass.
 //
 // Tiling for CDNA4: block tile 256 x 256, K step 32. The main kernel runs
-// 512 threads = 8 waves as 2 (M) x 4 (N), each owning 128 x 64 = 8 x 4 MFMA
+// 512 threads = 8 waves as 4 (M) x 2 (N), each owning 64 x 128 = 4 x 8 MFMA
 // 16x16x32 tiles (128 F32 accumulators per lane), two waves per SIMD so one
-// wave's MFMAs cover the other's LDS reads and barrier waits. Operands reach
+// wave's MFMAs cover the other's LDS reads and barrier waits. The short,
+// wide wave tile reads 16 fragments per K step for 64 MFMAs in split mode
+// (128 x 64 would read 20: A counts twice): 5-14 % faster on the 7B
+// shapes. Operands reach
 // LDS by DMA (global_load_lds_dwordx4) into XOR-swizzled, unpadded rows,
 // triple-buffered. The fallback kernel (K % 32 != 0) runs 4 waves of
 // 128 x 128 with register-staged, padded LDS rows.
@@ -218,6 +221,16 @@ __device__ inline int swizzled_unit(int row, int seg) {
   return row * 4 + (seg ^ ((row >> 2) & 3));
 }
 
+#ifndef EVO_GEMM_WAVES_M
+#define EVO_GEMM_WAVES_M 4
+#endif
+// Wave layout of the 8 waves over the 256 x 256 block tile: kGemmWavesM (M)
+// x 8 / kGemmWavesM (N). Per K step a wave reads (2 TM + TN) / 16 fragments
+// (A has two planes in split mode) for 2 TM TN / 256 MFMAs, so the split
+// product favours short, wide wave tiles: 64 x 128 reads 16 fragments per 64
+// MFMAs, 128 x 64 reads 20.
+constexpr int kGemmWavesM = EVO_GEMM_WAVES_M;
+
 // Split K: block row blockIdx.y multiplies K range [y K, (y + 1) K) (K is
 // the per-split length, ldw the weight row stride) into C + y c_split.
 template <bool kSplit>
@@ -234,6 +247,9 @@ __global__ __launch_bounds__(512) void gemm_kernel(
     W += k_first;
     C += blockIdx.y * c_split;
   }
+  constexpr int kWavesN = 8 / kGemmWavesM;
+  constexpr int kTM = kBM / kGemmWavesM, kTN = kBN / kWavesN;  // wave tile
+  constexpr int kMI = kTM / 16, kNJ = kTN / 16;                // 16 x 16 MFMA tiles
   constexpr int kPlanes = kSplit ? 3 : 2;  // A hi, (A lo), W
   constexpr int kStage = kPlanes * kPlane;
   __shared__ __attribute__((aligned(16))) uint16_t lds[kStages * kStage];
@@ -241,14 +257,14 @@ __global__ __launch_bounds__(512) void gemm_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wave_m = wave >> 2;  // 0..1
-  const int wave_n = wave & 3;   // 0..3
+  const int wave_m = wave / kWavesN;
+  const int wave_n = wave % kWavesN;
   const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
   int tm, tn;
   tile_of(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
   const int block_m = tm * kBM, block_n = tn * kBN;
 
-  // This lane's four DMA rows (instructions t = wave*4 + i) and segments.
+  // This lane's DMA rows (instructions t = wave*2 + i) and segments.
   const uint16_t *src_a_hi[2], *src_a_lo[2], *src_w[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
@@ -273,11 +289,11 @@ __global__ __launch_bounds__(512) void gemm_kernel(
     }
   };
 
-  f32x4 acc[8][4];
+  f32x4 acc[kMI][kNJ];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < kMI; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < kNJ; ++j)
 #pragma unroll
       for (int e = 0; e < 4; ++e)
         acc[i][j][e] = 0.0F;
@@ -307,65 +323,106 @@ __global__ __launch_bounds__(512) void gemm_kernel(
     const uint16_t *sa_lo = stage + kPlane;
     const uint16_t *sw = stage + (kPlanes - 1) * kPlane;
     // One 16x16x32 fragment covers the whole K step: lane l reads row l%16
-    // of its tile, 16-byte unit l/16. B and the A tiles 0-3 are read first;
-    // the reads of tiles 4-7 interleave with the MFMAs of tiles 0-3 (one
-    // LDS read, then four MFMAs).
-    bf16x8 b[4], ah[8], al[8];
-    auto read_a = [&](int i0) {
-#pragma unroll
-      for (int i = i0; i < i0 + 4; ++i) {
-        ah[i] = *reinterpret_cast<const bf16x8 *>(
-            sa_hi + swizzled_unit(wave_m * 128 + i * 16 + r16, seg) * 8);
-        if (kSplit)
-          al[i] = *reinterpret_cast<const bf16x8 *>(
-              sa_lo + swizzled_unit(wave_m * 128 + i * 16 + r16, seg) * 8);
-      }
+    // of its tile, 16-byte unit l/16. The fragments of the first half of
+    // the longer dimension are read first; the reads of the second half
+    // interleave with the MFMAs of the first (one LDS read, then a group of
+    // MFMAs).
+    bf16x8 b[kNJ], ah[kMI], al[kMI];
+    auto read_a = [&](int i) {
+      ah[i] = *reinterpret_cast<const bf16x8 *>(
+          sa_hi + swizzled_unit(wave_m * kTM + i * 16 + r16, seg) * 8);
+      if (kSplit)
+        al[i] = *reinterpret_cast<const bf16x8 *>(
+            sa_lo + swizzled_unit(wave_m * kTM + i * 16 + r16, seg) * 8);
     };
-    auto multiply = [&](int i0) {
-#pragma unroll
-      for (int i = i0; i < i0 + 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], b[j], acc[i][j], 0, 0, 0);
-      if (kSplit) {
-#pragma unroll
-        for (int i = i0; i < i0 + 4; ++i)
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], b[j], acc[i][j], 0, 0, 0);
-      }
-    };
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
+    auto read_b = [&](int j) {
       b[j] = *reinterpret_cast<const bf16x8 *>(
-          sw + swizzled_unit(wave_n * 64 + j * 16 + r16, seg) * 8);
-    read_a(0);
-    __builtin_amdgcn_sched_barrier(0);
-    read_a(4);
-    multiply(0);
+          sw + swizzled_unit(wave_n * kTN + j * 16 + r16, seg) * 8);
+    };
+    auto mfma = [&](int i, int j) {
+      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], b[j], acc[i][j], 0, 0, 0);
+      if (kSplit)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], b[j], acc[i][j], 0, 0, 0);
+    };
+    if constexpr (kMI >= kNJ) {
+      // tall wave tile: B whole, A in two halves
 #pragma unroll
-    for (int q = 0; q < (kSplit ? 8 : 4); ++q) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+      for (int j = 0; j < kNJ; ++j)
+        read_b(j);
+#pragma unroll
+      for (int i = 0; i < kMI / 2; ++i)
+        read_a(i);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = kMI / 2; i < kMI; ++i)
+        read_a(i);
+#pragma unroll
+      for (int i = 0; i < kMI / 2; ++i)
+#pragma unroll
+        for (int j = 0; j < kNJ; ++j)
+          mfma(i, j);
+      constexpr int kReads = (kMI / 2) * (kSplit ? 2 : 1);
+      constexpr int kMfmas = (kMI / 2) * kNJ * (kSplit ? 2 : 1);
+#pragma unroll
+      for (int q = 0; q < kReads; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, kMfmas / kReads, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = kMI / 2; i < kMI; ++i)
+#pragma unroll
+        for (int j = 0; j < kNJ; ++j)
+          mfma(i, j);
+    } else {
+      // wide wave tile: A whole, B in two halves
+#pragma unroll
+      for (int i = 0; i < kMI; ++i)
+        read_a(i);
+#pragma unroll
+      for (int j = 0; j < kNJ / 2; ++j)
+        read_b(j);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = kNJ / 2; j < kNJ; ++j)
+        read_b(j);
+#pragma unroll
+      for (int j = 0; j < kNJ / 2; ++j)
+#pragma unroll
+        for (int i = 0; i < kMI; ++i)
+          mfma(i, j);
+      constexpr int kReads = kNJ / 2;
+      constexpr int kMfmas = kMI * (kNJ / 2) * (kSplit ? 2 : 1);
+#pragma unroll
+      for (int q = 0; q < kReads; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, kMfmas / kReads, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = kNJ / 2; j < kNJ; ++j)
+#pragma unroll
+        for (int i = 0; i < kMI; ++i)
+          mfma(i, j);
     }
-    __builtin_amdgcn_sched_barrier(0);
-    multiply(4);
   }
 
   // Accumulator e of tile (i, j): row i*16 + 4*(lane/16) + e, column
-  // j*16 + lane%16 of the wave's 128 x 64 sub-tile. Gated mode: columns
+  // j*16 + lane%16 of the wave's TM x TN sub-tile. Gated mode: columns
   // [64q, 64q+32) hold l1 rows and [64q+32, 64q+64) the matching l2 rows,
-  // so tiles j and j+2 pair up in-lane.
-  const int wave_col = block_n + wave_n * 64;
-  const int wave_row = block_m + wave_m * 128 + (lane >> 4) * 4;
+  // so tiles j and j+2 of each 64-column group pair up in-lane.
+  const int wave_col = block_n + wave_n * kTN;
+  const int wave_row = block_m + wave_m * kTM + (lane >> 4) * 4;
   const bool bias_mode = epi.mode == kGemmBias || epi.mode == kGemmBiasResidual;
   const bool res_mode = epi.mode == kGemmResidual || epi.mode == kGemmBiasResidual;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < kMI; ++i) {
     if (epi.mode == kGemmGated) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int col = wave_col / 2 + j * 16 + r16;
+      for (int j = 0; j < kNJ; ++j) {
+        if ((j & 3) >= 2)
+          continue;  // l2 tiles: consumed with their l1 partner
+        const int col = wave_col / 2 + (j >> 2) * 32 + (j & 3) * 16 + r16;
         if (col >= epi.gated_width)
           continue;
 #pragma unroll
@@ -384,7 +441,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(
       }
     } else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < kNJ; ++j) {
         const int col = wave_col + j * 16 + r16;
         if (col >= N)
           continue;
