@@ -22,6 +22,7 @@
 #include "ops.hpp"
 
 #include <mutex>
+#include <type_traits>
 
 namespace evo::hip {
 namespace {
@@ -1627,6 +1628,470 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void hyena_fir_mfma_st
   flush(steps - 1);
 }
 
+// ---- HCL (modal long filter) in one pass on MFMA.
+// Per channel c (modes m < 16: pole p_m, residue R_m, direct D) and 16-row
+// block b with inputs u_{16b+j}, the recurrence s_t = p s_{t-1} + u_t,
+// y_t = sum_m R_m s_t + D u_t becomes three 16 x 16 products:
+//   Z = W U          W[m][j] = p_m^(15-j)        local block-end states
+//   S_b = p^16 S_{b-1} + Z_b                     a 16-lane scan over blocks
+//   Y = H U + V S'   H[r][j] = h[r-j] (j <= r) + D [j = r], h[n] = sum_m R_m p_m^n,
+//                    V[r][m] = R_m p_m^(r+1), S'_b = S_{b-1}
+// with U[j][b] = u_{16b+j} of one channel as the B operand, so one
+// v_mfma_f32_16x16x16_bf16 covers 256 rows of a channel. Each product runs
+// on split BF16 planes (hi*hi + hi*lo + lo*hi), the scan in F32.
+// A block owns 16 channels and walks the whole sequence in steps of kStep
+// rows (256 for BF16 projections, 128 for F32), so the projection is read
+// once and the modal state never leaves the block: production (short FIR,
+// gates, u as split planes into LDS [channel][row], x2 into LDS [row][ch])
+// from DMA-staged projection rows, the products (wave w: channels 2w, 2w+1;
+// y = x2 * Y in place of x2), and a flush of whole 16-channel rows, software
+// pipelined as in the HCM stream kernel (phase s: flush s-1, produce s+1,
+// multiply s). Consecutive channel groups are placed on one XCD, so the
+// four blocks that share each 128-byte line of a projection or output row
+// meet in one L2.
+constexpr int kHmChannels = 16;
+constexpr int kHmThreads = 512;
+
+template <typename T> struct HmShape {
+  static constexpr int kStep = sizeof(T) == 2 ? 256 : 128;   // rows per step
+  static constexpr int kBlocks = kStep / 16;                 // MFMA columns used
+  static constexpr int kWin = 3;                             // short FIR length
+  static constexpr int kRowBytes = kHmChannels * 3 * static_cast<int>(sizeof(T));
+  static constexpr int kStageRows = kStep + kWin - 1;
+  static constexpr int kStageBytes = kStageRows * kRowBytes;
+  static constexpr int kUnitsPerRow = kRowBytes / 16;
+  static constexpr int kUnits = kStageBytes / 16;
+  static constexpr int kDma = (kUnits + kHmThreads - 1) / kHmThreads;
+  static constexpr int kRowsPerThread = kStep / 64;           // production
+  static constexpr int kUStride = kStep + 8;                  // BF16 per u row
+  static constexpr int kFlushTasks = kStep * 2;               // 8 channels each
+  // x2 / y stage [channel][row]: a product lane's four rows are one 16-byte
+  // access, and the stride puts the two 8-channel halves of the flush 32
+  // banks apart.
+  static constexpr int kYStride = kStep + 4;
+};
+
+typedef short hm_s4 __attribute__((ext_vector_type(4)));
+constexpr int kHmStages = 3;
+
+// s_waitcnt vmcnt(n) for a run-time n (wave-uniform, 0 .. 9).
+__device__ inline void hm_wait(int n) {
+  switch (n) {
+    case 0: wait_dma<0>(); break;
+    case 1: wait_dma<1>(); break;
+    case 2: wait_dma<2>(); break;
+    case 3: wait_dma<3>(); break;
+    case 4: wait_dma<4>(); break;
+    case 5: wait_dma<5>(); break;
+    case 6: wait_dma<6>(); break;
+    case 7: wait_dma<7>(); break;
+    case 8: wait_dma<8>(); break;
+    default: wait_dma<9>(); break;
+  }
+}
+
+// Split of four values into BF16 hi / lo fragments.
+__device__ inline void hm_split4(const float (&v)[4], hm_s4 &hi, hm_s4 &lo) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint16_t h = f32_to_bf16(v[i]);
+    hi[i] = static_cast<short>(h);
+    lo[i] = static_cast<short>(f32_to_bf16(v[i] - bf16_to_f32(h)));
+  }
+}
+// x^n (0 <= n < 32) by repeated squaring.
+__device__ inline double hm_pow(double x, int n) {
+  double r = 1.0;
+#pragma unroll
+  for (int bit = 0; bit < 5; ++bit) {
+    if (n & (1 << bit))
+      r *= x;
+    x *= x;
+  }
+  return r;
+}
+// Value of lane l - d within its row of 16 lanes (0 for the first d lanes).
+template <int kD> __device__ inline float hm_shift(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+      0, __builtin_bit_cast(int, v), 0x110 + kD, 0xf, 0xf, true));
+}
+__device__ inline f32x4 hm_mfma3(const hm_s4 &ah, const hm_s4 &al, const hm_s4 &bh,
+                                 const hm_s4 &bl, f32x4 acc) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bh, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bl, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(al, bh, acc, 0, 0, 0);
+  return acc;
+}
+
+// Output of 8 channels of one row (16- or 32-byte pieces). Plain stores,
+// unlike the stream kernels' non-temporal ones: a block writes only 32 bytes
+// of each 128-byte output line, and the L2 merges the four blocks' pieces
+// into whole lines before they reach HBM.
+template <typename O> struct HmOut;
+template <> struct HmOut<float *> {
+  __device__ static int stores(float *) { return 2; }
+  __device__ static void put(const float (&v)[8], float *out, size_t index) {
+    *reinterpret_cast<f32x4 *>(out + index) = f32x4{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<f32x4 *>(out + index + 4) = f32x4{v[4], v[5], v[6], v[7]};
+  }
+};
+template <> struct HmOut<uint16_t *> {
+  __device__ static int stores(uint16_t *) { return 1; }
+  __device__ static void put(const float (&v)[8], uint16_t *out, size_t index) {
+    u32x4 w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = pack_bf16(v[2 * i], v[2 * i + 1]);
+    *reinterpret_cast<u32x4 *>(out + index) = w;
+  }
+};
+template <> struct HmOut<SplitOut> {
+  __device__ static int stores(const SplitOut &out) { return out.lo != nullptr ? 2 : 1; }
+  __device__ static void put(const float (&v)[8], const SplitOut &out, size_t index) {
+    uint32_t hi[4], lo[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      hi[i] = pack_bf16(v[2 * i], v[2 * i + 1]);
+      lo[i] = pack_bf16(v[2 * i] - __builtin_bit_cast(float, hi[i] << 16),
+                        v[2 * i + 1] - __builtin_bit_cast(float, hi[i] & 0xffff0000U));
+    }
+    *reinterpret_cast<u32x4 *>(out.hi + index) = u32x4{hi[0], hi[1], hi[2], hi[3]};
+    if (out.lo != nullptr)
+      *reinterpret_cast<u32x4 *>(out.lo + index) = u32x4{lo[0], lo[1], lo[2], lo[3]};
+  }
+};
+
+template <typename T, typename O>
+__global__ __launch_bounds__(kHmThreads, 1) void hcl_mfma_kernel(
+    const T *__restrict__ P, const float *__restrict__ short_history,
+    const uint16_t *__restrict__ short_filter, size_t L, size_t W,
+    const float *__restrict__ poles, const float *__restrict__ residues,
+    const float *__restrict__ direct, int S, float *__restrict__ modal_state, O out) {
+  using Shape = HmShape<T>;
+  constexpr int kStep = Shape::kStep, kWin = Shape::kWin, kPR = Shape::kRowsPerThread;
+  __shared__ __attribute__((aligned(16))) unsigned char p_s[kHmStages][Shape::kStageBytes];
+  __shared__ __attribute__((aligned(16))) uint16_t u_s[2][2][kHmChannels][Shape::kUStride];
+  __shared__ __attribute__((aligned(16))) float xy_s[3][kHmChannels][Shape::kYStride];
+
+  const unsigned groups = static_cast<unsigned>(W / kHmChannels);
+  const unsigned xcd = blockIdx.x % 8, per_xcd = groups / 8, extra = groups % 8;
+  const size_t c0 =
+      static_cast<size_t>(xcd * per_xcd + min(xcd, extra) + blockIdx.x / 8) * kHmChannels;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const size_t cols3 = 3 * W;
+  const int steps = static_cast<int>((L + kStep - 1) / kStep);
+
+  // ---- DMA of the projection rows of step `step` (rows 32 step - 2 ..):
+  // rows clamp to [0, L); rows before 0 come from the short history, rows
+  // past L feed only outputs that are dropped (their u is zeroed).
+  const unsigned char *p_block = reinterpret_cast<const unsigned char *>(P + 3 * c0);
+  uint32_t unit_row[Shape::kDma], unit_part[Shape::kDma];
+#pragma unroll
+  for (int j = 0; j < Shape::kDma; ++j) {
+    const int unit = min(j * kHmThreads + tid, Shape::kUnits - 1);
+    unit_row[j] = static_cast<uint32_t>(unit / Shape::kUnitsPerRow);
+    unit_part[j] = static_cast<uint32_t>(16 * (unit % Shape::kUnitsPerRow));
+  }
+  auto issue = [&](int step) {
+    const long r_first = static_cast<long>(step) * kStep - (kWin - 1);
+    unsigned char *stage = p_s[step % kHmStages];
+#pragma unroll
+    for (int j = 0; j < Shape::kDma; ++j) {
+      if (j * kHmThreads + wave * 64 < Shape::kUnits && j * kHmThreads + tid < Shape::kUnits) {
+        const long row = min(max(r_first + static_cast<long>(unit_row[j]), 0L),
+                             static_cast<long>(L) - 1);
+        dma16(p_block + static_cast<size_t>(row) * cols3 * sizeof(T) + unit_part[j],
+              stage + 16 * (j * kHmThreads + wave * 64));
+      }
+    }
+  };
+
+  // ---- Production lane: channels 2 pr, 2 pr + 1 and rows kPR rg .. + kPR-1.
+  const int pr = tid & 7, rg = tid >> 3;
+  const size_t cp = c0 + 2 * pr;
+  float stap[6][kWin];
+#pragma unroll
+  for (int ch = 0; ch < 2; ++ch) {
+    float t3[3][kWin];
+    load_window_taps(short_filter, kWin, cp + ch, t3);
+#pragma unroll
+    for (int s = 0; s < 3; ++s)
+#pragma unroll
+      for (int i = 0; i < kWin; ++i)
+        stap[3 * ch + s][i] = t3[s][i];
+  }
+  auto stage_row = [&](int step, int i, PairRow<T> &dst) {
+    const uint32_t *src = reinterpret_cast<const uint32_t *>(
+        p_s[step % kHmStages] + i * Shape::kRowBytes + 2 * pr * 3 * sizeof(T));
+#pragma unroll
+    for (int w = 0; w < PairRow<T>::kWords; ++w)
+      dst.word[w] = src[w];
+  };
+  auto history_row = [&](long row, PairRow<T> &dst) {  // row in [-2, -1]
+    const long hrow = static_cast<long>(kWin - 1) + row;
+#pragma unroll
+    for (int i = 0; i < PairRow<T>::kWords; ++i)
+      dst.word[i] = 0;
+    if (short_history != nullptr) {
+      float v[6];
+#pragma unroll
+      for (int col = 0; col < 6; ++col)
+        v[col] = short_history[static_cast<size_t>(hrow) * cols3 + 3 * cp + col];
+      if constexpr (sizeof(T) == 2) {
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+          dst.word[i] = (__builtin_bit_cast(uint32_t, v[2 * i]) >> 16) |
+                        (__builtin_bit_cast(uint32_t, v[2 * i + 1]) & 0xffff0000U);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 6; ++i)
+          dst.word[i] = __builtin_bit_cast(uint32_t, v[i]);
+      }
+    }
+  };
+  // Only step 0 reads rows before 0 (from the short history): the steady
+  // state has no global loads here, so the compiler's wait for their data
+  // cannot stall the DMA and store streams of the main loop.
+  auto produce = [&](int step, auto first_step) __attribute__((always_inline)) {
+    PairRow<T> cur[kPR + kWin - 1];
+    const long first = static_cast<long>(step) * kStep + kPR * rg - (kWin - 1);
+#pragma unroll
+    for (int i = 0; i < kPR + kWin - 1; ++i) {
+      if (!decltype(first_step)::value || first + i >= 0)
+        stage_row(step, kPR * rg + i, cur[i]);
+      else
+        history_row(first + i, cur[i]);
+    }
+    float u[2][kPR], x2[2][kPR];
+#pragma unroll
+    for (int j = 0; j < kPR; ++j) {
+      float fir[6];
+#pragma unroll
+      for (int c6 = 0; c6 < 6; ++c6) {
+        float total = 0.0F;
+#pragma unroll
+        for (int i = 0; i < kWin; ++i)
+          total += cur[j + i].at(c6) * stap[c6][i];
+        fir[c6] = total;
+      }
+      const bool valid = first + kWin - 1 + j < static_cast<long>(L);
+      u[0][j] = valid ? fir[1] * fir[2] : 0.0F;
+      u[1][j] = valid ? fir[4] * fir[5] : 0.0F;
+      x2[0][j] = fir[0];
+      x2[1][j] = fir[3];
+    }
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) {
+      float *dst = &xy_s[step % 3][2 * pr + ch][kPR * rg];
+      if constexpr (kPR == 4)
+        *reinterpret_cast<f32x4 *>(dst) = f32x4{x2[ch][0], x2[ch][1], x2[ch][2], x2[ch][3]};
+      else
+        *reinterpret_cast<float2 *>(dst) = make_float2(x2[ch][0], x2[ch][1]);
+    }
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) {
+      uint32_t hi[kPR / 2], lo[kPR / 2];
+#pragma unroll
+      for (int w = 0; w < kPR / 2; ++w) {
+        hi[w] = pack_bf16(u[ch][2 * w], u[ch][2 * w + 1]);
+        lo[w] = pack_bf16(u[ch][2 * w] - __builtin_bit_cast(float, hi[w] << 16),
+                          u[ch][2 * w + 1] - __builtin_bit_cast(float, hi[w] & 0xffff0000U));
+      }
+      uint16_t *dst_hi = &u_s[step & 1][0][2 * pr + ch][kPR * rg];
+      uint16_t *dst_lo = &u_s[step & 1][1][2 * pr + ch][kPR * rg];
+      if constexpr (kPR == 4) {
+        *reinterpret_cast<uint2 *>(dst_hi) = make_uint2(hi[0], hi[1]);
+        *reinterpret_cast<uint2 *>(dst_lo) = make_uint2(lo[0], lo[1]);
+      } else {
+        *reinterpret_cast<uint32_t *>(dst_hi) = hi[0];
+        *reinterpret_cast<uint32_t *>(dst_lo) = lo[0];
+      }
+    }
+  };
+
+  // ---- Product lane: channels 2 wave + k (k = 0, 1); column (block) b,
+  // fragment group g. The constant fragments are computed once per channel
+  // in double precision (powers by repeated squaring), and the filter
+  // h[n] = sum_m R_m p_m^n by four lanes per n (modes 4g .. 4g+3 each)
+  // reduced across the lane groups.
+  const int b = lane & 15, g = lane >> 4;
+  hm_s4 w_hi[2], w_lo[2], h_hi[2], h_lo[2], v_hi[2], v_lo[2];
+  float q1[2][4], q2[2][4], q4[2][4], q8[2][4], qb[2][4], carry[2][4];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const size_t c = c0 + 2 * wave + k;
+    // Loads first (one round trip): p of mode b, p and R of modes 4g + v.
+    const float p_b = b < S ? poles[c * S + b] : 0.0F;
+    float p_g[4], r_g[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int m = 4 * g + v;
+      p_g[v] = m < S ? poles[c * S + m] : 0.0F;
+      r_g[v] = m < S ? residues[c * S + m] : 0.0F;
+      carry[k][v] = (modal_state != nullptr && m < S) ? modal_state[c * S + m] : 0.0F;
+    }
+    const double d = direct[c];
+    // h[b] over this lane's four modes, then summed over the four groups.
+    double h_part = 0.0;
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      h_part += static_cast<double>(r_g[v]) * hm_pow(p_g[v], b);
+    float h_n = static_cast<float>(h_part);
+    h_n += __shfl_xor(h_n, 16);
+    h_n += __shfl_xor(h_n, 32);
+    float wv[4], hv[4], vv[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int j = 4 * g + v;  // A-operand K index; the A row is b
+      wv[v] = static_cast<float>(hm_pow(p_b, 15 - j));
+      const float h = __shfl(h_n, (b - j) & 15);
+      hv[v] = j <= b ? (j == b ? static_cast<float>(static_cast<double>(h) + d) : h) : 0.0F;
+      vv[v] = static_cast<float>(static_cast<double>(r_g[v]) * hm_pow(p_g[v], b + 1));
+      const double q = hm_pow(p_g[v], 16);  // block multiplier of mode 4g + v
+      const double q2d = q * q, q4d = q2d * q2d;
+      q1[k][v] = static_cast<float>(q);
+      q2[k][v] = static_cast<float>(q2d);
+      q4[k][v] = static_cast<float>(q4d);
+      q8[k][v] = static_cast<float>(q4d * q4d);
+      qb[k][v] = static_cast<float>(hm_pow(q, b + 1));
+    }
+    hm_split4(wv, w_hi[k], w_lo[k]);
+    hm_split4(hv, h_hi[k], h_lo[k]);
+    hm_split4(vv, v_hi[k], v_lo[k]);
+  }
+
+  float sp_last[2][4];
+  auto multiply = [&](int step) __attribute__((always_inline)) {
+    const uint16_t *uh = &u_s[step & 1][0][0][0];
+    const uint16_t *ul = &u_s[step & 1][1][0][0];
+    const bool col_ok = b < Shape::kBlocks;
+    const int row0 = 16 * (col_ok ? b : 0) + 4 * g;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int ch = 2 * wave + k;
+      hm_s4 ub_hi = *reinterpret_cast<const hm_s4 *>(uh + ch * Shape::kUStride + row0);
+      hm_s4 ub_lo = *reinterpret_cast<const hm_s4 *>(ul + ch * Shape::kUStride + row0);
+      if (!col_ok) {
+        ub_hi = hm_s4{0, 0, 0, 0};
+        ub_lo = hm_s4{0, 0, 0, 0};
+      }
+      f32x4 z = {0.0F, 0.0F, 0.0F, 0.0F};
+      z = hm_mfma3(w_hi[k], w_lo[k], ub_hi, ub_lo, z);
+      // Inclusive scan over the blocks (lanes b of each row of 16).
+      float sc[4], sp[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float v = z[e];
+        v = fmaf(q1[k][e], hm_shift<1>(v), v);
+        v = fmaf(q2[k][e], hm_shift<2>(v), v);
+        v = fmaf(q4[k][e], hm_shift<4>(v), v);
+        v = fmaf(q8[k][e], hm_shift<8>(v), v);
+        v = fmaf(qb[k][e], carry[k][e], v);
+        sc[e] = v;
+        sp[e] = hm_shift<1>(v) + (b == 0 ? carry[k][e] : 0.0F);
+      }
+      hm_s4 s_hi, s_lo;
+      hm_split4(sp, s_hi, s_lo);
+      f32x4 y = {0.0F, 0.0F, 0.0F, 0.0F};
+      y = hm_mfma3(h_hi[k], h_lo[k], ub_hi, ub_lo, y);
+      y = hm_mfma3(v_hi[k], v_lo[k], s_hi, s_lo, y);
+      // Kept for the final modal state (no memory access here: a global load
+      // or store in the step loop would make every step wait for the DMA
+      // and store streams).
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        sp_last[k][e] = sp[e];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        carry[k][e] = __shfl(sc[e], 16 * g + Shape::kBlocks - 1);
+      if (col_ok) {
+        f32x4 *xy = reinterpret_cast<f32x4 *>(&xy_s[step % 3][ch][row0]);
+        const f32x4 x2 = *xy;
+        *xy = f32x4{x2[0] * y[0], x2[1] * y[1], x2[2] * y[2], x2[3] * y[3]};
+      }
+    }
+  };
+
+  // ---- Flush lane: row fr of a step, channels 8 fh .. 8 fh + 7.
+  const bool flusher = tid < Shape::kFlushTasks;
+  const int fr = tid >> 1, fh = tid & 1;
+  const int stores = flusher ? HmOut<O>::stores(out) : 0;
+  auto flush = [&](int step) __attribute__((always_inline)) {
+    const size_t row = static_cast<size_t>(step) * kStep + fr;
+    if (flusher && row < L) {
+      float v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        v[i] = xy_s[step % 3][8 * fh + i][fr];
+      HmOut<O>::put(v, out, row * W + c0 + 8 * fh);
+    }
+  };
+
+  // Three projection stages: phase s issues the DMA of step s + 3 and must
+  // see step s + 2 landed before its closing barrier (the DMA of s + 3 and
+  // the flush stores of this and the previous phase may stay in flight). Every wave issues at least
+  // kDmaMin DMAs per step, so waiting down to that many younger ones is
+  // conservative.
+  constexpr int kDmaMin = Shape::kUnits / kHmThreads;
+  for (int step = 0; step < kHmStages && step < steps; ++step)
+    issue(step);
+  hm_wait(min(steps - 1, kHmStages - 1) * kDmaMin);
+  __syncthreads();
+  produce(0, std::true_type{});
+  hm_wait(steps > 2 ? kDmaMin : 0);
+  __syncthreads();
+  for (int step = 0; step < steps; ++step) {
+    const bool more = step + kHmStages < steps;
+    if (more)
+      issue(step + kHmStages);
+    if (step + 1 < steps)
+      produce(step + 1, std::false_type{});
+    multiply(step);
+    // The flush stores go last: issued first, they held up the phase's LDS
+    // and DMA work behind the store data path (136 -> 99 us at 7B/8k).
+    if (step >= 1)
+      flush(step - 1);
+    // Younger than the DMA of step + 2 (issued in the previous phase): the
+    // previous phase's flush stores, this phase's DMA and flush stores.
+    // Vector memory operations complete in issue order, so the stores may
+    // stay in flight across barriers.
+    if (step + 2 < steps)
+      hm_wait((more ? kDmaMin : 0) + (step >= 1 ? stores : 0) + (step >= 2 ? stores : 0));
+    __syncthreads();
+  }
+  flush(steps - 1);
+  // State after row L-1: the last step's block bl holds that row at rl;
+  // the lanes of column bl continue from S_{bl-1} over rows 0..rl.
+  if (modal_state != nullptr) {
+    const int step = steps - 1;
+    const int rows = static_cast<int>(L - static_cast<size_t>(step) * kStep);
+    const int bl = (rows - 1) / 16, rl = (rows - 1) % 16;
+    if (b == bl) {
+      const uint16_t *uh = &u_s[step & 1][0][0][0];
+      const uint16_t *ul = &u_s[step & 1][1][0][0];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int ch = 2 * wave + k;
+        const size_t c = c0 + ch;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int m = 4 * g + e;
+          if (m < S) {
+            const float pm = poles[c * S + m];
+            float st = sp_last[k][e];
+            for (int j = 0; j <= rl; ++j) {
+              const int at = ch * Shape::kUStride + 16 * bl + j;
+              st = fmaf(pm, st, bf16_to_f32(uh[at]) + bf16_to_f32(ul[at]));
+            }
+            modal_state[c * S + m] = st;
+          }
+        }
+      }
+    }
+  }
+}
+
 // Rewrites the inner (u) history with the last k-1 rows of [history ; u].
 // Runs after the main kernel and before the short history moves on.
 template <typename T>
@@ -1950,6 +2415,21 @@ Status hyena_forward(int kind, const T *projection, size_t length,
     if (wt.poles == nullptr || wt.residues == nullptr || wt.direct == nullptr ||
         wt.state == 0 || wt.state > kMaxState)
       return {ErrorCode::kInvalidArgument, "hyena_forward: HCL needs poles, residues, D, 1..16 states"};
+    if (short_len == 3 && planar == 0 && width % kHmChannels == 0) {
+      // One pass on MFMA; the modal state stays in the block (no workspace).
+      const unsigned blocks = static_cast<unsigned>(width / kHmChannels);
+      hipLaunchKernelGGL((hcl_mfma_kernel<T, O>), dim3(blocks), dim3(kHmThreads), 0, stream,
+                         projection, short_history, wt.short_filter, length, width, wt.poles,
+                         wt.residues, wt.direct, static_cast<int>(wt.state), modal_state, out);
+      EVO_TRY(launch_status("hcl_mfma_kernel"));
+      if (short_history != nullptr) {
+        hipLaunchKernelGGL(short_history_kernel<T>, dim3(ceil_div(3 * width, 256)), dim3(256),
+                           0, stream, projection, length, 3 * width, short_history,
+                           short_len - 1);
+        EVO_TRY(launch_status("short_history_kernel"));
+      }
+      return Status::Ok();
+    }
     const size_t G = hcl_chunks(length);
     if (workspace == nullptr ||
         workspace_bytes < hyena_workspace_bytes(kind, length, width, wt.state))
