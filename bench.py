@@ -9,8 +9,9 @@ resident in HBM (evo_hip_context_prefill_resident).
 
 Also measured live (HIP events on the launching stream, algorithmic work
 only): the dominant kernel (MLP l1/l2 GEMM, M=8192 N=2x11264 K=4096), the
-fused Hyena long-conv operator (config 2, BF16 I/O, L=8192 W=4096) and the
-FP8 projection GEMM (config 3, M=1024 K=4096 N=12288); and, on the host
+three Hyena operators (config 2, BF16 projection in, L=8192 W=4096; the
+headline `hyena_roofline` is the slowest of them) and the FP8 projection
+GEMM (config 3, M=1024 K=4096 N=12288); and, on the host
 cores, evo.cpp's own CPU library (oracle/_ref) on a bounded 16-token sample
 of the same artifact.
 
@@ -131,8 +132,7 @@ def kernel_rooflines(split):
     out["hyena"] = []
     for kind, name, taps in ((1, "HCM FIR, 128 taps (hyena_fir_mfma_stream_kernel)", 128),
                              (0, "HCS FIR, 7 taps (hyena_fir_stream_kernel)", 7),
-                             (2, "HCL, 16 modal states (hcl_state_pair + hcl_carry_seg + "
-                                 "hcl_output_pair)", 0)):
+                             (2, "HCL, 16 modal states (hcl_mfma_kernel)", 0)):
         filt = (torch.randn(groups, max(taps, 1), device="cuda", generator=g)
                 / max(taps, 1) ** 0.5).to(torch.bfloat16).float()
         st = state if kind == 2 else 0
@@ -180,7 +180,71 @@ def cpu_baseline(path, sample_tokens):
     return {"value": sample_tokens / seconds, "unit": "tok/s", "cores": 1, "kind": kind,
             "sample": f"{sample_tokens}-token prefill of the same 7B-shaped artifact "
                       f"(BF16 projections; reference cpu-f32 path, {seconds:.1f} s; "
-                      f"host has {os.cpu_count()} cores)"}
+                      f"host has {os.cpu_count()} cores); the full 1024-token and "
+                      "composed 8192-token figures are in "
+                      "profiles/reference_cpu_7b_prefill.md"}
+
+
+def reference_cpu(part, directory):
+    """evo.cpp's own CPU library (single-threaded F32 path) at the headline
+    workload, timed on this host: `full1k` runs a 1024-token prefill of the
+    7B-shaped artifact in full; `composed8k` times 8192-token prefills of
+    one-block 7B-width models (one per mixer type, plus a two-block HCS model
+    to separate the per-call embedding / final norm / unembedding) and
+    composes the 32-block time as 9 HCS + 9 HCM + 9 HCL + 5 attention blocks
+    plus one shared part."""
+    library = capi.EvoLibrary(REF_LIB)
+    out = {"host_cores": os.cpu_count(), "threads": 1}
+
+    def time_prefill(path, length):
+        model = library.load(path, capi.BACKEND_CPU)
+        # untimed warm-up: maps the weights in and loads the library's state
+        warm = model.context(64)
+        warm.prefill(A.acgt_tokens(64, seed=9).astype(np.uint8).tobytes())
+        warm.close()
+        ctx = model.context(length)
+        tokens = A.acgt_tokens(length, seed=1).astype(np.uint8).tobytes()
+        start = time.time()
+        ctx.prefill(tokens)
+        seconds = time.time() - start
+        ctx.close()
+        model.close()
+        log(f"{os.path.basename(path)} {length} tokens: {seconds:.1f} s")
+        return seconds
+
+    if part == "full1k":
+        path, _ = artifact_path(directory)
+        seconds = time_prefill(path, 1024)
+        out.update(workload="7B-shaped, 32 blocks, 1024 ACGT tokens", seconds=round(seconds, 1),
+                   tok_s=round(1024 / seconds, 4))
+        return out
+    base = A.evo2_7b_shape()
+    layouts = {"hcs": dict(hcs=[0], hcm=[], hcl=[], attn=[]),
+               "hcm": dict(hcs=[], hcm=[0], hcl=[], attn=[]),
+               "hcl": dict(hcs=[], hcm=[], hcl=[0], attn=[]),
+               "attn": dict(hcs=[], hcm=[], hcl=[], attn=[0]),
+               "hcs2": dict(hcs=[0, 1], hcm=[], hcl=[], attn=[])}
+    times = {}
+    for name, lists in layouts.items():
+        shape = A.ModelShape(width=base.width, layers=len(sum(lists.values(), [])),
+                             heads=base.heads, inner=base.inner, rope_scale=base.rope_scale,
+                             hcs_groups=base.hcs_groups, hcm_groups=base.hcm_groups,
+                             hcs_len=base.hcs_len, hcm_len=base.hcm_len,
+                             max_seqlen=base.max_seqlen,
+                             model_id=f"random-init-evo2-7b-width-{name}", **lists)
+        path = os.path.join(directory, f"evo2_7b_width_{name}.safetensors")
+        if not os.path.exists(path):
+            A.random_artifact(shape, seed=0, init="survey").write(path)
+        times[name] = time_prefill(path, 8192)
+    shared = times["hcs"] - (times["hcs2"] - times["hcs"])
+    block = {k: times[k] - shared for k in ("hcs", "hcm", "hcl", "attn")}
+    composed = 9 * block["hcs"] + 9 * block["hcm"] + 9 * block["hcl"] + 5 * block["attn"] + shared
+    out.update(workload="7B-shaped, 32 blocks, 8192 ACGT tokens (composed)",
+               measured_seconds={k: round(v, 1) for k, v in times.items()},
+               block_seconds={k: round(v, 1) for k, v in block.items()},
+               shared_seconds=round(shared, 1), seconds=round(composed, 1),
+               tok_s=round(8192 / composed, 4))
+    return out
 
 
 def main():
@@ -199,7 +263,12 @@ def main():
     parser.add_argument("--decode-steps", type=int, default=32)
     parser.add_argument("--only-kernels", action="store_true",
                         help="run only the roofline launches (for rocprofv3 counter passes)")
+    parser.add_argument("--reference-cpu", choices=["full1k", "composed8k"],
+                        help="time only evo.cpp's CPU library at the headline workload")
     args = parser.parse_args()
+    if args.reference_cpu:
+        print(json.dumps(reference_cpu(args.reference_cpu, args.artifact_dir)), flush=True)
+        return
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build runs on one "
               "MI355X; the multi-GPU layout is described in DESIGN.md", file=sys.stderr)
@@ -338,13 +407,22 @@ def main():
                               "unit": "TFLOP/s", "frac": round(g["tflops"] / BF16_PEAK_TFLOPS, 4),
                               "traffic": measured_traffic(g["kernel"]), "ms": round(g["ms"], 4),
                               "per_launch": "2*8192*22528*4096 flop (MLP l1/l2 of one block)"}
-        hyena = [{"kernel": h["kernel"], "achieved": round(h["gbs"], 1),
-                  "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                  "frac": round(h["gbs"] / HBM_PEAK_GBS, 4), "ms": round(h["ms"], 4)}
-                 for h in kernels["hyena"]]
-        per_launch = ("335544320 B: read BF16 [8192, 12288] projection, write split "
-                      "BF16 planes [2, 8192, 4096]")
-        result["hyena_roofline"] = dict(hyena[0], bound="hbm", per_launch=per_launch)
+        # Two byte counts per launch: the operator's own unit (BF16 [8192,
+        # 12288] in, BF16 [8192, 4096] out: 268435456 B) -- the headline
+        # `frac` -- and what the model path moves (split-plane output,
+        # 335544320 B) as `frac_split_planes`.
+        unit_bytes = 8192 * 3 * 4096 * 2 + 8192 * 4096 * 2
+        hyena = []
+        for h in kernels["hyena"]:
+            gbs = unit_bytes / h["ms"] / 1e6
+            hyena.append({"kernel": h["kernel"], "achieved": round(gbs, 1),
+                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                          "frac": round(gbs / HBM_PEAK_GBS, 4), "ms": round(h["ms"], 4),
+                          "frac_split_planes": round(h["gbs"] / HBM_PEAK_GBS, 4)})
+        per_launch = ("268435456 B: read BF16 [8192, 12288] projection, write BF16 "
+                      "[8192, 4096] (the launch writes split planes, 335544320 B)")
+        worst = min(hyena, key=lambda h: h["frac"])
+        result["hyena_roofline"] = dict(worst, bound="hbm", per_launch=per_launch)
         result["hyena_kernels"] = hyena
         for name in ("fp8_k32", "fp8_k128"):
             f = kernels[name]
