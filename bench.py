@@ -193,8 +193,16 @@ def reference_cpu(part, directory):
     to separate the per-call embedding / final norm / unembedding) and
     composes the 32-block time as 9 HCS + 9 HCM + 9 HCL + 5 attention blocks
     plus one shared part."""
+    import threading
     library = capi.EvoLibrary(REF_LIB)
     out = {"host_cores": os.cpu_count(), "threads": 1}
+    # Progress line every minute (a single CPU prefill runs for minutes).
+    started, done = time.time(), threading.Event()
+
+    def heartbeat():
+        while not done.wait(60):
+            log(f"reference CPU run: {time.time() - started:.0f} s")
+    threading.Thread(target=heartbeat, daemon=True).start()
 
     def time_prefill(path, length):
         model = library.load(path, capi.BACKEND_CPU)
@@ -217,6 +225,7 @@ def reference_cpu(part, directory):
         seconds = time_prefill(path, 1024)
         out.update(workload="7B-shaped, 32 blocks, 1024 ACGT tokens", seconds=round(seconds, 1),
                    tok_s=round(1024 / seconds, 4))
+        done.set()
         return out
     base = A.evo2_7b_shape()
     layouts = {"hcs": dict(hcs=[0], hcm=[], hcl=[], attn=[]),
@@ -244,6 +253,7 @@ def reference_cpu(part, directory):
                block_seconds={k: round(v, 1) for k, v in block.items()},
                shared_seconds=round(shared, 1), seconds=round(composed, 1),
                tok_s=round(8192 / composed, 4))
+    done.set()
     return out
 
 
