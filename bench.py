@@ -185,7 +185,7 @@ def cpu_baseline(path, sample_tokens):
                       "profiles/reference_cpu_7b_prefill.md"}
 
 
-def reference_cpu(part, directory):
+def reference_cpu(part, directory, only=None):
     """evo.cpp's own CPU library (single-threaded F32 path) at the headline
     workload, timed on this host: `full1k` runs a 1024-token prefill of the
     7B-shaped artifact in full; `composed8k` times 8192-token prefills of
@@ -235,6 +235,8 @@ def reference_cpu(part, directory):
                "hcs2": dict(hcs=[0, 1], hcm=[], hcl=[], attn=[])}
     times = {}
     for name, lists in layouts.items():
+        if only and name not in only:
+            continue
         shape = A.ModelShape(width=base.width, layers=len(sum(lists.values(), [])),
                              heads=base.heads, inner=base.inner, rope_scale=base.rope_scale,
                              hcs_groups=base.hcs_groups, hcm_groups=base.hcm_groups,
@@ -245,6 +247,11 @@ def reference_cpu(part, directory):
         if not os.path.exists(path):
             A.random_artifact(shape, seed=0, init="survey").write(path)
         times[name] = time_prefill(path, 8192)
+    if set(times) != set(layouts):
+        out.update(workload="one- and two-block 7B-width models, 8192 ACGT tokens",
+                   measured_seconds={k: round(v, 1) for k, v in times.items()})
+        done.set()
+        return out
     shared = times["hcs"] - (times["hcs2"] - times["hcs"])
     block = {k: times[k] - shared for k in ("hcs", "hcm", "hcl", "attn")}
     composed = 9 * block["hcs"] + 9 * block["hcm"] + 9 * block["hcl"] + 5 * block["attn"] + shared
@@ -275,9 +282,14 @@ def main():
                         help="run only the roofline launches (for rocprofv3 counter passes)")
     parser.add_argument("--reference-cpu", choices=["full1k", "composed8k"],
                         help="time only evo.cpp's CPU library at the headline workload")
+    parser.add_argument("--reference-models", default="",
+                        help="composed8k: comma-separated subset of hcs,hcm,hcl,attn,hcs2 "
+                             "(to split the runs over several jobs)")
     args = parser.parse_args()
     if args.reference_cpu:
-        print(json.dumps(reference_cpu(args.reference_cpu, args.artifact_dir)), flush=True)
+        only = set(filter(None, args.reference_models.split(",")))
+        print(json.dumps(reference_cpu(args.reference_cpu, args.artifact_dir, only)),
+              flush=True)
         return
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build runs on one "

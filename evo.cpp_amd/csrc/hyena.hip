@@ -1786,23 +1786,33 @@ __global__ __launch_bounds__(kHmThreads, 1) void hcl_mfma_kernel(
   // rows clamp to [0, L); rows before 0 come from the short history, rows
   // past L feed only outputs that are dropped (their u is zeroed).
   const unsigned char *p_block = reinterpret_cast<const unsigned char *>(P + 3 * c0);
-  uint32_t unit_row[Shape::kDma], unit_part[Shape::kDma];
+  uint32_t unit_row[Shape::kDma], unit_part[Shape::kDma], unit_byte[Shape::kDma];
 #pragma unroll
   for (int j = 0; j < Shape::kDma; ++j) {
     const int unit = min(j * kHmThreads + tid, Shape::kUnits - 1);
     unit_row[j] = static_cast<uint32_t>(unit / Shape::kUnitsPerRow);
     unit_part[j] = static_cast<uint32_t>(16 * (unit % Shape::kUnitsPerRow));
+    unit_byte[j] = static_cast<uint32_t>(unit_row[j] * cols3 * sizeof(T)) + unit_part[j];
   }
   auto issue = [&](int step) {
     const long r_first = static_cast<long>(step) * kStep - (kWin - 1);
     unsigned char *stage = p_s[step % kHmStages];
+    // Steps whose rows all lie in [0, L) use a uniform base and fixed
+    // per-lane offsets; the first and last steps clamp each row.
+    const bool inside = r_first >= 0 && r_first + Shape::kStageRows <= static_cast<long>(L);
+    const unsigned char *base =
+        p_block + static_cast<size_t>(max(r_first, 0L)) * cols3 * sizeof(T);
 #pragma unroll
     for (int j = 0; j < Shape::kDma; ++j) {
       if (j * kHmThreads + wave * 64 < Shape::kUnits && j * kHmThreads + tid < Shape::kUnits) {
-        const long row = min(max(r_first + static_cast<long>(unit_row[j]), 0L),
-                             static_cast<long>(L) - 1);
-        dma16(p_block + static_cast<size_t>(row) * cols3 * sizeof(T) + unit_part[j],
-              stage + 16 * (j * kHmThreads + wave * 64));
+        if (inside) {
+          dma16(base, unit_byte[j], stage + 16 * (j * kHmThreads + wave * 64));
+        } else {
+          const long row = min(max(r_first + static_cast<long>(unit_row[j]), 0L),
+                               static_cast<long>(L) - 1);
+          dma16(p_block + static_cast<size_t>(row) * cols3 * sizeof(T) + unit_part[j],
+                stage + 16 * (j * kHmThreads + wave * 64));
+        }
       }
     }
   };
@@ -2017,15 +2027,19 @@ __global__ __launch_bounds__(kHmThreads, 1) void hcl_mfma_kernel(
   const bool flusher = tid < Shape::kFlushTasks;
   const int fr = tid >> 1, fh = tid & 1;
   const int stores = flusher ? HmOut<O>::stores(out) : 0;
+  // The flush lane's output index advances by one step of rows per call.
+  size_t flush_index = static_cast<size_t>(fr) * W + c0 + 8 * fh;
+  size_t flush_row = static_cast<size_t>(fr);
   auto flush = [&](int step) __attribute__((always_inline)) {
-    const size_t row = static_cast<size_t>(step) * kStep + fr;
-    if (flusher && row < L) {
+    if (flusher && flush_row < L) {
       float v[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i)
         v[i] = xy_s[step % 3][8 * fh + i][fr];
-      HmOut<O>::put(v, out, row * W + c0 + 8 * fh);
+      HmOut<O>::put(v, out, flush_index);
     }
+    flush_index += static_cast<size_t>(kStep) * W;
+    flush_row += kStep;
   };
 
   // Three projection stages: phase s issues the DMA of step s + 3 and must
