@@ -227,6 +227,7 @@ def reference_cpu(part, directory, only=None):
                    tok_s=round(1024 / seconds, 4))
         done.set()
         return out
+    os.makedirs(directory, exist_ok=True)
     base = A.evo2_7b_shape()
     layouts = {"hcs": dict(hcs=[0], hcm=[], hcl=[], attn=[]),
                "hcm": dict(hcs=[], hcm=[0], hcl=[], attn=[]),
