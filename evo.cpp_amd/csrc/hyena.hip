@@ -360,18 +360,24 @@ __global__ __launch_bounds__(256) void hyena_fir_kernel(
 // Each lane owns two adjacent channels: their six interleaved projection
 // columns are 12 (BF16) or 24 (F32) contiguous bytes of a row, and the two
 // outputs are one packed 32-bit store per plane. A wave streams a segment of
-// kStreamRows rows; it starts kLead rows early so that its short-FIR window
-// and its FIR window of u are full when the segment begins (the lead rows are
-// recomputed, not stored). Both windows hold their taps right-aligned with
-// zeros in front, so every sum runs oldest first as in the reference; with
-// kWin == short_len and kTaps == k there are no zero taps. Rows are fetched
+// 64 or 128 rows (kStreamRows, kStreamMaxRows); it starts kLead rows early
+// so that its short-FIR window and its FIR window of u are full when the
+// segment begins (the lead rows are recomputed, not stored). Both windows
+// hold their taps right-aligned with zeros in front, so every sum runs oldest
+// first as in the reference; with kWin == short_len and kTaps == k there are
+// no zero taps. Rows are fetched
 // in batches of kStreamBatch with the next batch in flight while the current
 // one is evaluated. Stores go through a buffer resource bounded to the
 // segment, so rows past the sequence end are dropped by the hardware, and
 // are non-temporal: the outputs are never re-read here, and streaming them
 // past the L2 keeps it for the projection rows (-23 % kernel time on the 7B
 // shape).
+// Segment length: 64 rows, doubled to 128 when the grid keeps at least
+// kStreamMinBlocks blocks (two per CU): longer segments recompute fewer lead
+// rows (7B, L = 8192: 58 -> 54 us; 256 rows measured no better).
 constexpr int kStreamRows = 64;
+constexpr int kStreamMaxRows = 128;
+constexpr unsigned kStreamMinBlocks = 512;
 constexpr int kStreamBatch = 4;
 constexpr int kStreamWaves = 4;              // waves per block
 constexpr int kStreamChannels = kStreamWaves * 64 * 2;
@@ -498,7 +504,7 @@ __global__ __launch_bounds__(kStreamWaves * 64) void hyena_fir_stream_kernel(
     const uint16_t *__restrict__ short_filter, int short_len,
     const float *__restrict__ inner_history, const float *__restrict__ filter,
     size_t group_size, int k, int causal, const float *__restrict__ direct,
-    size_t L, size_t W, unsigned channel_blocks, unsigned segments, O out) {
+    size_t L, size_t W, unsigned channel_blocks, unsigned segments, unsigned seg_len, O out) {
   constexpr int kLead = (kTaps - 1) + (kWin - 1);
   // XCD-aware order: consecutive hardware ids go to different XCDs, so each
   // XCD takes a contiguous band of segments (neighbouring segments share
@@ -513,8 +519,8 @@ __global__ __launch_bounds__(kStreamWaves * 64) void hyena_fir_stream_kernel(
                    (threadIdx.x >> 6) * 128 + 2 * lane;
   if (c >= W)
     return;
-  const size_t t0 = static_cast<size_t>(segment) * kStreamRows;
-  const uint32_t seg_rows = static_cast<uint32_t>(min(L - t0, static_cast<size_t>(kStreamRows)));
+  const size_t t0 = static_cast<size_t>(segment) * seg_len;
+  const uint32_t seg_rows = static_cast<uint32_t>(min(L - t0, static_cast<size_t>(seg_len)));
   const size_t cols3 = 3 * W;
 
   PairFir<T, kWin, kTaps, kDirect> fir;
@@ -1673,6 +1679,12 @@ template <typename T> struct HmShape {
 
 typedef short hm_s4 __attribute__((ext_vector_type(4)));
 constexpr int kHmStages = 3;
+// Phase variants of the HCL kernel: the first step (rows before 0 from the
+// short history), any step (every bound checked), and the interior steps,
+// whose rows, DMA and flush all lie inside the sequence (no checks, so the
+// whole phase is one basic block the compiler can schedule across).
+constexpr int kHmGeneric = 0, kHmFirst = 1, kHmSteady = 2;
+template <int kMode> using HmMode = std::integral_constant<int, kMode>;
 
 // s_waitcnt vmcnt(n) for a run-time n (wave-uniform, 0 .. 9).
 __device__ inline void hm_wait(int n) {
@@ -1794,12 +1806,13 @@ __global__ __launch_bounds__(kHmThreads, 1) void hcl_mfma_kernel(
     unit_part[j] = static_cast<uint32_t>(16 * (unit % Shape::kUnitsPerRow));
     unit_byte[j] = static_cast<uint32_t>(unit_row[j] * cols3 * sizeof(T)) + unit_part[j];
   }
-  auto issue = [&](int step) {
+  auto issue = [&](int step, auto steady) __attribute__((always_inline)) {
     const long r_first = static_cast<long>(step) * kStep - (kWin - 1);
     unsigned char *stage = p_s[step % kHmStages];
     // Steps whose rows all lie in [0, L) use a uniform base and fixed
     // per-lane offsets; the first and last steps clamp each row.
-    const bool inside = r_first >= 0 && r_first + Shape::kStageRows <= static_cast<long>(L);
+    const bool inside = decltype(steady)::value ||
+                        (r_first >= 0 && r_first + Shape::kStageRows <= static_cast<long>(L));
     const unsigned char *base =
         p_block + static_cast<size_t>(max(r_first, 0L)) * cols3 * sizeof(T);
 #pragma unroll
@@ -1863,12 +1876,12 @@ __global__ __launch_bounds__(kHmThreads, 1) void hcl_mfma_kernel(
   // Only step 0 reads rows before 0 (from the short history): the steady
   // state has no global loads here, so the compiler's wait for their data
   // cannot stall the DMA and store streams of the main loop.
-  auto produce = [&](int step, auto first_step) __attribute__((always_inline)) {
+  auto produce = [&](int step, auto mode) __attribute__((always_inline)) {
     PairRow<T> cur[kPR + kWin - 1];
     const long first = static_cast<long>(step) * kStep + kPR * rg - (kWin - 1);
 #pragma unroll
     for (int i = 0; i < kPR + kWin - 1; ++i) {
-      if (!decltype(first_step)::value || first + i >= 0)
+      if (decltype(mode)::value != kHmFirst || first + i >= 0)
         stage_row(step, kPR * rg + i, cur[i]);
       else
         history_row(first + i, cur[i]);
@@ -1885,7 +1898,8 @@ __global__ __launch_bounds__(kHmThreads, 1) void hcl_mfma_kernel(
           total += cur[j + i].at(c6) * stap[c6][i];
         fir[c6] = total;
       }
-      const bool valid = first + kWin - 1 + j < static_cast<long>(L);
+      const bool valid = decltype(mode)::value == kHmSteady ||
+                         first + kWin - 1 + j < static_cast<long>(L);
       u[0][j] = valid ? fir[1] * fir[2] : 0.0F;
       u[1][j] = valid ? fir[4] * fir[5] : 0.0F;
       x2[0][j] = fir[0];
@@ -1972,7 +1986,14 @@ __global__ __launch_bounds__(kHmThreads, 1) void hcl_mfma_kernel(
   }
 
   float sp_last[2][4];
-  auto multiply = [&](int step) __attribute__((always_inline)) {
+  // The products of step `step` in two parts, so the phase can run the
+  // production of the next step between them: part one reads U and issues
+  // Z = W U and H U for both channels (the matrix cores work while the
+  // production's VALU runs); part two scans Z (eight independent chains per
+  // lane: two channels x four modes), adds V S' and applies the gate.
+  hm_s4 ub_hi[2], ub_lo[2];
+  f32x4 z_acc[2], y_acc[2];
+  auto multiply_a = [&](int step) __attribute__((always_inline)) {
     const uint16_t *uh = &u_s[step & 1][0][0][0];
     const uint16_t *ul = &u_s[step & 1][1][0][0];
     const bool col_ok = b < Shape::kBlocks;
@@ -1980,32 +2001,65 @@ __global__ __launch_bounds__(kHmThreads, 1) void hcl_mfma_kernel(
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
       const int ch = 2 * wave + k;
-      hm_s4 ub_hi = *reinterpret_cast<const hm_s4 *>(uh + ch * Shape::kUStride + row0);
-      hm_s4 ub_lo = *reinterpret_cast<const hm_s4 *>(ul + ch * Shape::kUStride + row0);
+      ub_hi[k] = *reinterpret_cast<const hm_s4 *>(uh + ch * Shape::kUStride + row0);
+      ub_lo[k] = *reinterpret_cast<const hm_s4 *>(ul + ch * Shape::kUStride + row0);
       if (!col_ok) {
-        ub_hi = hm_s4{0, 0, 0, 0};
-        ub_lo = hm_s4{0, 0, 0, 0};
+        ub_hi[k] = hm_s4{0, 0, 0, 0};
+        ub_lo[k] = hm_s4{0, 0, 0, 0};
       }
-      f32x4 z = {0.0F, 0.0F, 0.0F, 0.0F};
-      z = hm_mfma3(w_hi[k], w_lo[k], ub_hi, ub_lo, z);
-      // Inclusive scan over the blocks (lanes b of each row of 16).
-      float sc[4], sp[4];
+    }
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float v = z[e];
-        v = fmaf(q1[k][e], hm_shift<1>(v), v);
-        v = fmaf(q2[k][e], hm_shift<2>(v), v);
-        v = fmaf(q4[k][e], hm_shift<4>(v), v);
-        v = fmaf(q8[k][e], hm_shift<8>(v), v);
-        v = fmaf(qb[k][e], carry[k][e], v);
-        sc[e] = v;
-        sp[e] = hm_shift<1>(v) + (b == 0 ? carry[k][e] : 0.0F);
-      }
+    for (int k = 0; k < 2; ++k)
+      z_acc[k] = hm_mfma3(w_hi[k], w_lo[k], ub_hi[k], ub_lo[k], f32x4{0.0F, 0.0F, 0.0F, 0.0F});
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+      y_acc[k] = hm_mfma3(h_hi[k], h_lo[k], ub_hi[k], ub_lo[k], f32x4{0.0F, 0.0F, 0.0F, 0.0F});
+  };
+  auto multiply_b = [&](int step) __attribute__((always_inline)) {
+    const bool col_ok = b < Shape::kBlocks;
+    const int row0 = 16 * (col_ok ? b : 0) + 4 * g;
+    // Inclusive scan over the blocks (lanes b of each row of 16), level by
+    // level across the eight chains.
+    float v[2][4];
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        v[k][e] = z_acc[k][e];
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        v[k][e] = fmaf(q1[k][e], hm_shift<1>(v[k][e]), v[k][e]);
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        v[k][e] = fmaf(q2[k][e], hm_shift<2>(v[k][e]), v[k][e]);
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        v[k][e] = fmaf(q4[k][e], hm_shift<4>(v[k][e]), v[k][e]);
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        v[k][e] = fmaf(q8[k][e], hm_shift<8>(v[k][e]), v[k][e]);
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        v[k][e] = fmaf(qb[k][e], carry[k][e], v[k][e]);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      float sp[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        sp[e] = hm_shift<1>(v[k][e]) + (b == 0 ? carry[k][e] : 0.0F);
       hm_s4 s_hi, s_lo;
       hm_split4(sp, s_hi, s_lo);
-      f32x4 y = {0.0F, 0.0F, 0.0F, 0.0F};
-      y = hm_mfma3(h_hi[k], h_lo[k], ub_hi, ub_lo, y);
-      y = hm_mfma3(v_hi[k], v_lo[k], s_hi, s_lo, y);
+      y_acc[k] = hm_mfma3(v_hi[k], v_lo[k], s_hi, s_lo, y_acc[k]);
       // Kept for the final modal state (no memory access here: a global load
       // or store in the step loop would make every step wait for the DMA
       // and store streams).
@@ -2014,10 +2068,14 @@ __global__ __launch_bounds__(kHmThreads, 1) void hcl_mfma_kernel(
         sp_last[k][e] = sp[e];
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        carry[k][e] = __shfl(sc[e], 16 * g + Shape::kBlocks - 1);
-      if (col_ok) {
-        f32x4 *xy = reinterpret_cast<f32x4 *>(&xy_s[step % 3][ch][row0]);
+        carry[k][e] = __shfl(v[k][e], 16 * g + Shape::kBlocks - 1);
+    }
+    if (col_ok) {
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        f32x4 *xy = reinterpret_cast<f32x4 *>(&xy_s[step % 3][2 * wave + k][row0]);
         const f32x4 x2 = *xy;
+        const f32x4 y = y_acc[k];
         *xy = f32x4{x2[0] * y[0], x2[1] * y[1], x2[2] * y[2], x2[3] * y[3]};
       }
     }
@@ -2030,8 +2088,8 @@ __global__ __launch_bounds__(kHmThreads, 1) void hcl_mfma_kernel(
   // The flush lane's output index advances by one step of rows per call.
   size_t flush_index = static_cast<size_t>(fr) * W + c0 + 8 * fh;
   size_t flush_row = static_cast<size_t>(fr);
-  auto flush = [&](int step) __attribute__((always_inline)) {
-    if (flusher && flush_row < L) {
+  auto flush = [&](int step, auto steady) __attribute__((always_inline)) {
+    if (flusher && (decltype(steady)::value || flush_row < L)) {
       float v[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i)
@@ -2049,32 +2107,44 @@ __global__ __launch_bounds__(kHmThreads, 1) void hcl_mfma_kernel(
   // conservative.
   constexpr int kDmaMin = Shape::kUnits / kHmThreads;
   for (int step = 0; step < kHmStages && step < steps; ++step)
-    issue(step);
+    issue(step, std::false_type{});
   hm_wait(min(steps - 1, kHmStages - 1) * kDmaMin);
   __syncthreads();
-  produce(0, std::true_type{});
+  produce(0, HmMode<kHmFirst>{});
   hm_wait(steps > 2 ? kDmaMin : 0);
   __syncthreads();
-  for (int step = 0; step < steps; ++step) {
-    const bool more = step + kHmStages < steps;
+  auto phase = [&](int step, auto steady) __attribute__((always_inline)) {
+    constexpr bool kSteady = decltype(steady)::value;
+    const bool more = kSteady || step + kHmStages < steps;
     if (more)
-      issue(step + kHmStages);
-    if (step + 1 < steps)
-      produce(step + 1, std::false_type{});
-    multiply(step);
+      issue(step + kHmStages, steady);
+    multiply_a(step);
+    if (kSteady || step + 1 < steps)
+      produce(step + 1, HmMode<kSteady ? kHmSteady : kHmGeneric>{});
+    multiply_b(step);
     // The flush stores go last: issued first, they held up the phase's LDS
     // and DMA work behind the store data path (136 -> 99 us at 7B/8k).
-    if (step >= 1)
-      flush(step - 1);
+    if (kSteady || step >= 1)
+      flush(step - 1, steady);
     // Younger than the DMA of step + 2 (issued in the previous phase): the
     // previous phase's flush stores, this phase's DMA and flush stores.
     // Vector memory operations complete in issue order, so the stores may
     // stay in flight across barriers.
-    if (step + 2 < steps)
+    if (kSteady || step + 2 < steps)
       hm_wait((more ? kDmaMin : 0) + (step >= 1 ? stores : 0) + (step >= 2 ? stores : 0));
     __syncthreads();
-  }
-  flush(steps - 1);
+  };
+  // Interior steps 2 <= step < L / kStep - 3: the DMA of step + 3, the
+  // production of step + 1 and the flush of step - 1 lie inside [0, L).
+  const int steady_end = static_cast<int>(L / kStep) - 3;
+  int step = 0;
+  for (; step < steps && step < 2; ++step)
+    phase(step, std::false_type{});
+  for (; step < steady_end; ++step)
+    phase(step, std::true_type{});
+  for (; step < steps; ++step)
+    phase(step, std::false_type{});
+  flush(steps - 1, std::false_type{});
   // State after row L-1: the last step's block bl holds that row at rl;
   // the lanes of column bl continue from S_{bl-1} over rows 0..rl.
   if (modal_state != nullptr) {
@@ -2310,18 +2380,22 @@ void launch_fir_stream_taps(const T *projection, const float *short_history,
                             size_t group_size, int k, int causal, const float *direct,
                             size_t length, size_t width, O out, hipStream_t stream) {
   const unsigned cblocks = ceil_div(width, kStreamChannels);
-  const unsigned segments = ceil_div(length, kStreamRows);
+  unsigned seg_len = kStreamRows;
+  while (seg_len < kStreamMaxRows &&
+         cblocks * ceil_div(length, 2 * static_cast<size_t>(seg_len)) >= kStreamMinBlocks)
+    seg_len *= 2;
+  const unsigned segments = ceil_div(length, seg_len);
   const dim3 grid(cblocks * segments), block(kStreamWaves * 64);
   if (direct != nullptr)
     hipLaunchKernelGGL((hyena_fir_stream_kernel<T, O, kWin, kTaps, true>), grid, block, 0, stream,
                        projection, short_history, wt.short_filter, short_len, inner_history,
                        wt.inner_filter, group_size, k, causal, direct, length, width, cblocks,
-                       segments, out);
+                       segments, seg_len, out);
   else
     hipLaunchKernelGGL((hyena_fir_stream_kernel<T, O, kWin, kTaps, false>), grid, block, 0,
                        stream, projection, short_history, wt.short_filter, short_len,
                        inner_history, wt.inner_filter, group_size, k, causal, direct, length,
-                       width, cblocks, segments, out);
+                       width, cblocks, segments, seg_len, out);
 }
 
 // Exact window widths for the 7B shape (short FIR 3, HCS 7 taps); other

@@ -80,6 +80,17 @@ def test_config2_hyena_operator_7b_width(kind):
     error = rel_err(actual, expected)
     say(f"config 2 kind {kind}: max err {error:.3g} of the output scale")
     assert error < 2e-5
+    # The operator's own format (BF16 in, BF16 out, as evo.cpp's
+    # bf16_hcs/hcm/hcl_prefill write it): each output is the F32 result
+    # rounded once to BF16, so every element lies within half a BF16 ulp of
+    # the oracle (|y| in [2^(E-1), 2^E): ulp 2^(E-8)), plus the F32 error above.
+    out16 = hyena_gpu(kind, case, dtype=N.DTYPE_BF16, bf16_taps=True, guard=8)
+    half_ulp = np.ldexp(1.0, np.frexp(expected)[1] - 9)
+    excess = np.abs(out16 - expected) - half_ulp
+    scale = np.abs(expected).max()
+    say(f"config 2 kind {kind} BF16 out: worst excess over half an ulp "
+        f"{excess.max() / scale:.3g} of the output scale")
+    assert excess.max() < 2e-5 * scale
 
 
 # -------------------------------------------------------------- config 3
