@@ -131,9 +131,13 @@ def kernel_rooflines(split):
     hbm_bytes = length * 3 * width * 2 + length * width * 4
     bf16_bytes = length * 3 * width * 2 + length * width * 2
     out["hyena"] = []
-    for kind, name, taps in ((1, "HCM FIR, 128 taps (hyena_fir_mfma_stream_kernel)", 128),
-                             (0, "HCS FIR, 7 taps (hyena_fir_stream_kernel)", 7),
-                             (2, "HCL, 16 modal states (hcl_mfma_kernel)", 0)):
+    for kind, name, taps, profiled in (
+            (1, "HCM FIR, 128 taps (hyena_fir_mfma_stream_kernel)", 128,
+             "hyena_fir_mfma_stream_kernel<unsigned short, unsigned short*>"),
+            (0, "HCS FIR, 7 taps (hyena_fir_stream_kernel)", 7,
+             "hyena_fir_stream_kernel<unsigned short, unsigned short*, 3, 7, false>"),
+            (2, "HCL, 16 modal states (hcl_mfma_kernel)", 0,
+             "hcl_mfma_kernel<unsigned short, unsigned short*>")):
         filt = (torch.randn(groups, max(taps, 1), device="cuda", generator=g)
                 / max(taps, 1) ** 0.5).to(torch.bfloat16).float()
         st = state if kind == 2 else 0
@@ -148,7 +152,7 @@ def kernel_rooflines(split):
                 poles.data_ptr(), residues.data_ptr(), st, None, None, None, ws.data_ptr(),
                 ws_bytes, planes_out.data_ptr(), stream), 10)
         ms, ms_split = times[native.DTYPE_BF16], times[native.DTYPE_BF16_SPLIT]
-        out["hyena"].append(dict(kernel=name, ms=ms, bytes=bf16_bytes, gbs=bf16_bytes / ms / 1e6,
+        out["hyena"].append(dict(kernel=name, profiled=profiled, ms=ms, bytes=bf16_bytes, gbs=bf16_bytes / ms / 1e6,
                                  ms_split=ms_split, bytes_split=hbm_bytes,
                                  gbs_split=hbm_bytes / ms_split / 1e6))
     del proj, planes_out
@@ -443,7 +447,8 @@ def main():
         for h in kernels["hyena"]:
             hyena.append({"kernel": h["kernel"], "achieved": round(h["gbs"], 1),
                           "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                          "frac": round(h["gbs"] / HBM_PEAK_GBS, 4), "ms": round(h["ms"], 4),
+                          "frac": round(h["gbs"] / HBM_PEAK_GBS, 4),
+                          "traffic": measured_traffic(h["profiled"]), "ms": round(h["ms"], 4),
                           "ms_split_planes": round(h["ms_split"], 4),
                           "frac_split_planes": round(h["gbs_split"] / HBM_PEAK_GBS, 4)})
         per_launch = ("268435456 B: read BF16 [8192, 12288] projection, write BF16 "

@@ -1655,8 +1655,13 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void hyena_fir_mfma_st
 // multiply s). Consecutive channel groups are placed on one XCD, so the
 // four blocks that share each 128-byte line of a projection or output row
 // meet in one L2.
+// 16 channels per block (8 per block, two blocks per CU: 82 -> 83 us with
+// BF16 output, 98 -> 149 us with split planes, whose 16-byte row pieces
+// the L2 merges badly).
 constexpr int kHmChannels = 16;
-constexpr int kHmThreads = 512;
+constexpr int kHmThreads = 32 * kHmChannels;   // two channels per wave
+constexpr int kHmPairs = kHmChannels / 2;      // production channel pairs
+constexpr int kHmFlushParts = kHmChannels / 8; // flush lanes per row
 
 template <typename T> struct HmShape {
   static constexpr int kStep = sizeof(T) == 2 ? 256 : 128;   // rows per step
@@ -1670,7 +1675,7 @@ template <typename T> struct HmShape {
   static constexpr int kDma = (kUnits + kHmThreads - 1) / kHmThreads;
   static constexpr int kRowsPerThread = kStep / 64;           // production
   static constexpr int kUStride = kStep + 8;                  // BF16 per u row
-  static constexpr int kFlushTasks = kStep * 2;               // 8 channels each
+  static constexpr int kFlushTasks = kStep * kHmFlushParts;   // 8 channels each
   // x2 / y stage [channel][row]: a product lane's four rows are one 16-byte
   // access, and the stride puts the two 8-channel halves of the flush 32
   // banks apart.
@@ -1774,7 +1779,7 @@ template <> struct HmOut<SplitOut> {
 };
 
 template <typename T, typename O>
-__global__ __launch_bounds__(kHmThreads, 1) void hcl_mfma_kernel(
+__global__ __launch_bounds__(kHmThreads, 16 / kHmChannels) void hcl_mfma_kernel(
     const T *__restrict__ P, const float *__restrict__ short_history,
     const uint16_t *__restrict__ short_filter, size_t L, size_t W,
     const float *__restrict__ poles, const float *__restrict__ residues,
@@ -1831,7 +1836,7 @@ __global__ __launch_bounds__(kHmThreads, 1) void hcl_mfma_kernel(
   };
 
   // ---- Production lane: channels 2 pr, 2 pr + 1 and rows kPR rg .. + kPR-1.
-  const int pr = tid & 7, rg = tid >> 3;
+  const int pr = tid % kHmPairs, rg = tid / kHmPairs;
   const size_t cp = c0 + 2 * pr;
   float stap[6][kWin];
 #pragma unroll
@@ -2083,7 +2088,7 @@ __global__ __launch_bounds__(kHmThreads, 1) void hcl_mfma_kernel(
 
   // ---- Flush lane: row fr of a step, channels 8 fh .. 8 fh + 7.
   const bool flusher = tid < Shape::kFlushTasks;
-  const int fr = tid >> 1, fh = tid & 1;
+  const int fr = tid / kHmFlushParts, fh = tid % kHmFlushParts;
   const int stores = flusher ? HmOut<O>::stores(out) : 0;
   // The flush lane's output index advances by one step of rows per call.
   size_t flush_index = static_cast<size_t>(fr) * W + c0 + 8 * fh;
