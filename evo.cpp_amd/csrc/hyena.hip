@@ -1674,16 +1674,23 @@ template <typename T> struct HmShape {
   static constexpr int kUnits = kStageBytes / 16;
   static constexpr int kDma = (kUnits + kHmThreads - 1) / kHmThreads;
   static constexpr int kRowsPerThread = kStep / 64;           // production
-  static constexpr int kUStride = kStep + 8;                  // BF16 per u row
+  // u stage [channel][row] (BF16) and x2 / y stage [channel][row] (F32):
+  // row r sits at hm_upos(r) / hm_ypos(r), which pad 8 BF16 every 128 rows
+  // and 4 floats every 64 rows, so that the product lanes' 16 blocks (rows
+  // 16 b + 4 g) fall on distinct bank groups; the strides keep the
+  // production lanes' writes (8 channel pairs x 4-row groups) distinct too.
+  static constexpr int kUStride = sizeof(T) == 2 ? 280 : 136;
   static constexpr int kFlushTasks = kStep * kHmFlushParts;   // 8 channels each
   // x2 / y stage [channel][row]: a product lane's four rows are one 16-byte
   // access, and the stride puts the two 8-channel halves of the flush 32
   // banks apart.
-  static constexpr int kYStride = kStep + 4;
+  static constexpr int kYStride = kStep + 4 * (kStep / 64) + 4;
 };
 
 typedef short hm_s4 __attribute__((ext_vector_type(4)));
 constexpr int kHmStages = 3;
+__device__ inline int hm_upos(int row) { return row + 8 * (row >> 7); }
+__device__ inline int hm_ypos(int row) { return row + 4 * (row >> 6); }
 // Phase variants of the HCL kernel: the first step (rows before 0 from the
 // short history), any step (every bound checked), and the interior steps,
 // whose rows, DMA and flush all lie inside the sequence (no checks, so the
@@ -1881,8 +1888,10 @@ __global__ __launch_bounds__(kHmThreads, 16 / kHmChannels) void hcl_mfma_kernel(
   // Only step 0 reads rows before 0 (from the short history): the steady
   // state has no global loads here, so the compiler's wait for their data
   // cannot stall the DMA and store streams of the main loop.
-  auto produce = [&](int step, auto mode) __attribute__((always_inline)) {
-    PairRow<T> cur[kPR + kWin - 1];
+  // Production in two parts (the phase issues every LDS read first): the
+  // staged rows of the lane's window, then the arithmetic and the LDS writes.
+  PairRow<T> cur[kPR + kWin - 1];
+  auto produce_load = [&](int step, auto mode) __attribute__((always_inline)) {
     const long first = static_cast<long>(step) * kStep + kPR * rg - (kWin - 1);
 #pragma unroll
     for (int i = 0; i < kPR + kWin - 1; ++i) {
@@ -1891,6 +1900,9 @@ __global__ __launch_bounds__(kHmThreads, 16 / kHmChannels) void hcl_mfma_kernel(
       else
         history_row(first + i, cur[i]);
     }
+  };
+  auto produce_compute = [&](int step, auto mode) __attribute__((always_inline)) {
+    const long first = static_cast<long>(step) * kStep + kPR * rg - (kWin - 1);
     float u[2][kPR], x2[2][kPR];
 #pragma unroll
     for (int j = 0; j < kPR; ++j) {
@@ -1912,7 +1924,7 @@ __global__ __launch_bounds__(kHmThreads, 16 / kHmChannels) void hcl_mfma_kernel(
     }
 #pragma unroll
     for (int ch = 0; ch < 2; ++ch) {
-      float *dst = &xy_s[step % 3][2 * pr + ch][kPR * rg];
+      float *dst = &xy_s[step % 3][2 * pr + ch][hm_ypos(kPR * rg)];
       if constexpr (kPR == 4)
         *reinterpret_cast<f32x4 *>(dst) = f32x4{x2[ch][0], x2[ch][1], x2[ch][2], x2[ch][3]};
       else
@@ -1927,8 +1939,8 @@ __global__ __launch_bounds__(kHmThreads, 16 / kHmChannels) void hcl_mfma_kernel(
         lo[w] = pack_bf16(u[ch][2 * w] - __builtin_bit_cast(float, hi[w] << 16),
                           u[ch][2 * w + 1] - __builtin_bit_cast(float, hi[w] & 0xffff0000U));
       }
-      uint16_t *dst_hi = &u_s[step & 1][0][2 * pr + ch][kPR * rg];
-      uint16_t *dst_lo = &u_s[step & 1][1][2 * pr + ch][kPR * rg];
+      uint16_t *dst_hi = &u_s[step & 1][0][2 * pr + ch][hm_upos(kPR * rg)];
+      uint16_t *dst_lo = &u_s[step & 1][1][2 * pr + ch][hm_upos(kPR * rg)];
       if constexpr (kPR == 4) {
         *reinterpret_cast<uint2 *>(dst_hi) = make_uint2(hi[0], hi[1]);
         *reinterpret_cast<uint2 *>(dst_lo) = make_uint2(lo[0], lo[1]);
@@ -1937,6 +1949,10 @@ __global__ __launch_bounds__(kHmThreads, 16 / kHmChannels) void hcl_mfma_kernel(
         *reinterpret_cast<uint32_t *>(dst_lo) = lo[0];
       }
     }
+  };
+  auto produce = [&](int step, auto mode) __attribute__((always_inline)) {
+    produce_load(step, mode);
+    produce_compute(step, mode);
   };
 
   // ---- Product lane: channels 2 wave + k (k = 0, 1); column (block) b,
@@ -1997,8 +2013,9 @@ __global__ __launch_bounds__(kHmThreads, 16 / kHmChannels) void hcl_mfma_kernel(
   // production's VALU runs); part two scans Z (eight independent chains per
   // lane: two channels x four modes), adds V S' and applies the gate.
   hm_s4 ub_hi[2], ub_lo[2];
-  f32x4 z_acc[2], y_acc[2];
-  auto multiply_a = [&](int step) __attribute__((always_inline)) {
+  f32x4 z_acc[2], y_acc[2], x2_frag[2];
+  // LDS reads of the products: U of step `step` and its gate x2.
+  auto multiply_load = [&](int step) __attribute__((always_inline)) {
     const uint16_t *uh = &u_s[step & 1][0][0][0];
     const uint16_t *ul = &u_s[step & 1][1][0][0];
     const bool col_ok = b < Shape::kBlocks;
@@ -2006,13 +2023,16 @@ __global__ __launch_bounds__(kHmThreads, 16 / kHmChannels) void hcl_mfma_kernel(
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
       const int ch = 2 * wave + k;
-      ub_hi[k] = *reinterpret_cast<const hm_s4 *>(uh + ch * Shape::kUStride + row0);
-      ub_lo[k] = *reinterpret_cast<const hm_s4 *>(ul + ch * Shape::kUStride + row0);
+      ub_hi[k] = *reinterpret_cast<const hm_s4 *>(uh + ch * Shape::kUStride + hm_upos(row0));
+      ub_lo[k] = *reinterpret_cast<const hm_s4 *>(ul + ch * Shape::kUStride + hm_upos(row0));
+      x2_frag[k] = *reinterpret_cast<const f32x4 *>(&xy_s[step % 3][ch][hm_ypos(row0)]);
       if (!col_ok) {
         ub_hi[k] = hm_s4{0, 0, 0, 0};
         ub_lo[k] = hm_s4{0, 0, 0, 0};
       }
     }
+  };
+  auto multiply_a = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int k = 0; k < 2; ++k)
       z_acc[k] = hm_mfma3(w_hi[k], w_lo[k], ub_hi[k], ub_lo[k], f32x4{0.0F, 0.0F, 0.0F, 0.0F});
@@ -2078,8 +2098,8 @@ __global__ __launch_bounds__(kHmThreads, 16 / kHmChannels) void hcl_mfma_kernel(
     if (col_ok) {
 #pragma unroll
       for (int k = 0; k < 2; ++k) {
-        f32x4 *xy = reinterpret_cast<f32x4 *>(&xy_s[step % 3][2 * wave + k][row0]);
-        const f32x4 x2 = *xy;
+        f32x4 *xy = reinterpret_cast<f32x4 *>(&xy_s[step % 3][2 * wave + k][hm_ypos(row0)]);
+        const f32x4 x2 = x2_frag[k];
         const f32x4 y = y_acc[k];
         *xy = f32x4{x2[0] * y[0], x2[1] * y[1], x2[2] * y[2], x2[3] * y[3]};
       }
@@ -2093,16 +2113,21 @@ __global__ __launch_bounds__(kHmThreads, 16 / kHmChannels) void hcl_mfma_kernel(
   // The flush lane's output index advances by one step of rows per call.
   size_t flush_index = static_cast<size_t>(fr) * W + c0 + 8 * fh;
   size_t flush_row = static_cast<size_t>(fr);
-  auto flush = [&](int step, auto steady) __attribute__((always_inline)) {
-    if (flusher && (decltype(steady)::value || flush_row < L)) {
-      float v[8];
+  float flush_v[8];
+  auto flush_load = [&](int step) __attribute__((always_inline)) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        v[i] = xy_s[step % 3][8 * fh + i][fr];
-      HmOut<O>::put(v, out, flush_index);
-    }
+    for (int i = 0; i < 8; ++i)
+      flush_v[i] = xy_s[step % 3][8 * fh + i][hm_ypos(fr)];
+  };
+  auto flush_store = [&](auto steady) __attribute__((always_inline)) {
+    if (flusher && (decltype(steady)::value || flush_row < L))
+      HmOut<O>::put(flush_v, out, flush_index);
     flush_index += static_cast<size_t>(kStep) * W;
     flush_row += kStep;
+  };
+  auto flush = [&](int step, auto steady) __attribute__((always_inline)) {
+    flush_load(step);
+    flush_store(steady);
   };
 
   // Three projection stages: phase s issues the DMA of step s + 3 and must
@@ -2121,16 +2146,25 @@ __global__ __launch_bounds__(kHmThreads, 16 / kHmChannels) void hcl_mfma_kernel(
   auto phase = [&](int step, auto steady) __attribute__((always_inline)) {
     constexpr bool kSteady = decltype(steady)::value;
     const bool more = kSteady || step + kHmStages < steps;
+    const bool next = kSteady || step + 1 < steps;
+    const bool flushes = kSteady || step >= 1;
+    constexpr auto mode = HmMode<kSteady ? kHmSteady : kHmGeneric>{};
     if (more)
       issue(step + kHmStages, steady);
-    multiply_a(step);
-    if (kSteady || step + 1 < steps)
-      produce(step + 1, HmMode<kSteady ? kHmSteady : kHmGeneric>{});
+    // Every LDS read of the phase first (one round trip), then the work.
+    multiply_load(step);
+    if (next)
+      produce_load(step + 1, mode);
+    if (flushes)
+      flush_load(step - 1);
+    multiply_a();
+    if (next)
+      produce_compute(step + 1, mode);
     multiply_b(step);
     // The flush stores go last: issued first, they held up the phase's LDS
     // and DMA work behind the store data path (136 -> 99 us at 7B/8k).
-    if (kSteady || step >= 1)
-      flush(step - 1, steady);
+    if (flushes)
+      flush_store(steady);
     // Younger than the DMA of step + 2 (issued in the previous phase): the
     // previous phase's flush stores, this phase's DMA and flush stores.
     // Vector memory operations complete in issue order, so the stores may
@@ -2170,7 +2204,7 @@ __global__ __launch_bounds__(kHmThreads, 16 / kHmChannels) void hcl_mfma_kernel(
             const float pm = poles[c * S + m];
             float st = sp_last[k][e];
             for (int j = 0; j <= rl; ++j) {
-              const int at = ch * Shape::kUStride + 16 * bl + j;
+              const int at = ch * Shape::kUStride + hm_upos(16 * bl + j);
               st = fmaf(pm, st, bf16_to_f32(uh[at]) + bf16_to_f32(ul[at]));
             }
             modal_state[c * S + m] = st;
