@@ -1659,11 +1659,24 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void hyena_fir_mfma_st
 // BF16 output, 98 -> 149 us with split planes, whose 16-byte row pieces
 // the L2 merges badly).
 constexpr int kHmChannels = 16;
-constexpr int kHmThreads = 32 * kHmChannels;   // two channels per wave
 constexpr int kHmPairs = kHmChannels / 2;      // production channel pairs
 constexpr int kHmFlushParts = kHmChannels / 8; // flush lanes per row
+// Wave roles. With kRoles, 4 producer waves (DMA and production, two row
+// groups per lane) and 8 consumer waves (two channels each: products, scan,
+// gate, flush), three waves per SIMD: 80 -> 70 us at config 2 with BF16
+// output. Split-plane output keeps 8 waves that each do both (with roles its
+// projection reads were fetched 1.4x from HBM, the L2 losing the lines that
+// neighbouring blocks share before they read them: 98 -> 120 us).
+template <bool kRoles> struct HmRoles {
+  static constexpr int kProducerWaves = kRoles ? 4 : kHmChannels / 2;
+  static constexpr int kThreads = 64 * (kRoles ? 4 + kHmChannels / 2 : kHmChannels / 2);
+  static constexpr int kProducers = 64 * kProducerWaves;
+  static constexpr int kTasks = 64 * kHmPairs / kProducers;  // row groups per producer lane
+};
+template <typename O> constexpr bool kHmRoles = !std::is_same<O, SplitOut>::value;
+template <typename O> constexpr int kHmThreads = HmRoles<kHmRoles<O>>::kThreads;
 
-template <typename T> struct HmShape {
+template <typename T, int kProducers> struct HmShape {
   static constexpr int kStep = sizeof(T) == 2 ? 256 : 128;   // rows per step
   static constexpr int kBlocks = kStep / 16;                 // MFMA columns used
   static constexpr int kWin = 3;                             // short FIR length
@@ -1672,7 +1685,7 @@ template <typename T> struct HmShape {
   static constexpr int kStageBytes = kStageRows * kRowBytes;
   static constexpr int kUnitsPerRow = kRowBytes / 16;
   static constexpr int kUnits = kStageBytes / 16;
-  static constexpr int kDma = (kUnits + kHmThreads - 1) / kHmThreads;
+  static constexpr int kDma = (kUnits + kProducers - 1) / kProducers;
   static constexpr int kRowsPerThread = kStep / 64;           // production
   // u stage [channel][row] (BF16) and x2 / y stage [channel][row] (F32):
   // row r sits at hm_upos(r) / hm_ypos(r), which pad 8 BF16 every 128 rows
@@ -1786,12 +1799,15 @@ template <> struct HmOut<SplitOut> {
 };
 
 template <typename T, typename O>
-__global__ __launch_bounds__(kHmThreads, 16 / kHmChannels) void hcl_mfma_kernel(
+__global__ __launch_bounds__(kHmThreads<O>, 1) void hcl_mfma_kernel(
     const T *__restrict__ P, const float *__restrict__ short_history,
     const uint16_t *__restrict__ short_filter, size_t L, size_t W,
     const float *__restrict__ poles, const float *__restrict__ residues,
     const float *__restrict__ direct, int S, float *__restrict__ modal_state, O out) {
-  using Shape = HmShape<T>;
+  constexpr bool kRoles = kHmRoles<O>;
+  using Roles = HmRoles<kRoles>;
+  constexpr int kHmProducers = Roles::kProducers, kHmTasks = Roles::kTasks;
+  using Shape = HmShape<T, kHmProducers>;
   constexpr int kStep = Shape::kStep, kWin = Shape::kWin, kPR = Shape::kRowsPerThread;
   __shared__ __attribute__((aligned(16))) unsigned char p_s[kHmStages][Shape::kStageBytes];
   __shared__ __attribute__((aligned(16))) uint16_t u_s[2][2][kHmChannels][Shape::kUStride];
@@ -1803,6 +1819,8 @@ __global__ __launch_bounds__(kHmThreads, 16 / kHmChannels) void hcl_mfma_kernel(
       static_cast<size_t>(xcd * per_xcd + min(xcd, extra) + blockIdx.x / 8) * kHmChannels;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool producer = !kRoles || wave < Roles::kProducerWaves;
+  const bool consumer = !kRoles || !producer;
   const size_t cols3 = 3 * W;
   const int steps = static_cast<int>((L + kStep - 1) / kStep);
 
@@ -1810,13 +1828,12 @@ __global__ __launch_bounds__(kHmThreads, 16 / kHmChannels) void hcl_mfma_kernel(
   // rows clamp to [0, L); rows before 0 come from the short history, rows
   // past L feed only outputs that are dropped (their u is zeroed).
   const unsigned char *p_block = reinterpret_cast<const unsigned char *>(P + 3 * c0);
-  uint32_t unit_row[Shape::kDma], unit_part[Shape::kDma], unit_byte[Shape::kDma];
+  uint32_t unit_byte[Shape::kDma];
 #pragma unroll
   for (int j = 0; j < Shape::kDma; ++j) {
-    const int unit = min(j * kHmThreads + tid, Shape::kUnits - 1);
-    unit_row[j] = static_cast<uint32_t>(unit / Shape::kUnitsPerRow);
-    unit_part[j] = static_cast<uint32_t>(16 * (unit % Shape::kUnitsPerRow));
-    unit_byte[j] = static_cast<uint32_t>(unit_row[j] * cols3 * sizeof(T)) + unit_part[j];
+    const int unit = min(j * kHmProducers + tid, Shape::kUnits - 1);
+    unit_byte[j] = static_cast<uint32_t>(unit / Shape::kUnitsPerRow * cols3 * sizeof(T) +
+                                         16 * (unit % Shape::kUnitsPerRow));
   }
   auto issue = [&](int step, auto steady) __attribute__((always_inline)) {
     const long r_first = static_cast<long>(step) * kStep - (kWin - 1);
@@ -1829,21 +1846,25 @@ __global__ __launch_bounds__(kHmThreads, 16 / kHmChannels) void hcl_mfma_kernel(
         p_block + static_cast<size_t>(max(r_first, 0L)) * cols3 * sizeof(T);
 #pragma unroll
     for (int j = 0; j < Shape::kDma; ++j) {
-      if (j * kHmThreads + wave * 64 < Shape::kUnits && j * kHmThreads + tid < Shape::kUnits) {
+      if (j * kHmProducers + wave * 64 < Shape::kUnits &&
+          j * kHmProducers + tid < Shape::kUnits) {
         if (inside) {
-          dma16(base, unit_byte[j], stage + 16 * (j * kHmThreads + wave * 64));
+          dma16(base, unit_byte[j], stage + 16 * (j * kHmProducers + wave * 64));
         } else {
-          const long row = min(max(r_first + static_cast<long>(unit_row[j]), 0L),
+          const int unit = j * kHmProducers + tid;
+          const long row = min(max(r_first + unit / Shape::kUnitsPerRow, 0L),
                                static_cast<long>(L) - 1);
-          dma16(p_block + static_cast<size_t>(row) * cols3 * sizeof(T) + unit_part[j],
-                stage + 16 * (j * kHmThreads + wave * 64));
+          dma16(p_block + static_cast<size_t>(row) * cols3 * sizeof(T) +
+                    16 * (unit % Shape::kUnitsPerRow),
+                stage + 16 * (j * kHmProducers + wave * 64));
         }
       }
     }
   };
 
-  // ---- Production lane: channels 2 pr, 2 pr + 1 and rows kPR rg .. + kPR-1.
-  const int pr = tid % kHmPairs, rg = tid / kHmPairs;
+  // ---- Production lane (producer waves): channels 2 pr, 2 pr + 1 and, for
+  // each task t, rows kPR rg .. + kPR-1 of row group rg = rg0 + t 64 / kHmTasks.
+  const int pr = tid % kHmPairs, rg0 = (tid % kHmProducers) / kHmPairs;
   const size_t cp = c0 + 2 * pr;
   float stap[6][kWin];
 #pragma unroll
@@ -1890,18 +1911,21 @@ __global__ __launch_bounds__(kHmThreads, 16 / kHmChannels) void hcl_mfma_kernel(
   // cannot stall the DMA and store streams of the main loop.
   // Production in two parts (the phase issues every LDS read first): the
   // staged rows of the lane's window, then the arithmetic and the LDS writes.
-  PairRow<T> cur[kPR + kWin - 1];
-  auto produce_load = [&](int step, auto mode) __attribute__((always_inline)) {
+  PairRow<T> cur_rows[kHmTasks][kPR + kWin - 1];
+  auto produce_load_task = [&](int step, auto mode, int t) __attribute__((always_inline)) {
+    const int rg = rg0 + t * (64 / kHmTasks);
     const long first = static_cast<long>(step) * kStep + kPR * rg - (kWin - 1);
 #pragma unroll
     for (int i = 0; i < kPR + kWin - 1; ++i) {
       if (decltype(mode)::value != kHmFirst || first + i >= 0)
-        stage_row(step, kPR * rg + i, cur[i]);
+        stage_row(step, kPR * rg + i, cur_rows[t][i]);
       else
-        history_row(first + i, cur[i]);
+        history_row(first + i, cur_rows[t][i]);
     }
   };
-  auto produce_compute = [&](int step, auto mode) __attribute__((always_inline)) {
+  auto produce_task = [&](int step, auto mode, int t) __attribute__((always_inline)) {
+    const int rg = rg0 + t * (64 / kHmTasks);
+    const PairRow<T> (&cur)[kPR + kWin - 1] = cur_rows[t];
     const long first = static_cast<long>(step) * kStep + kPR * rg - (kWin - 1);
     float u[2][kPR], x2[2][kPR];
 #pragma unroll
@@ -1951,8 +1975,11 @@ __global__ __launch_bounds__(kHmThreads, 16 / kHmChannels) void hcl_mfma_kernel(
     }
   };
   auto produce = [&](int step, auto mode) __attribute__((always_inline)) {
-    produce_load(step, mode);
-    produce_compute(step, mode);
+#pragma unroll
+    for (int t = 0; t < kHmTasks; ++t) {
+      produce_load_task(step, mode, t);
+      produce_task(step, mode, t);
+    }
   };
 
   // ---- Product lane: channels 2 wave + k (k = 0, 1); column (block) b,
@@ -1961,11 +1988,12 @@ __global__ __launch_bounds__(kHmThreads, 16 / kHmChannels) void hcl_mfma_kernel(
   // h[n] = sum_m R_m p_m^n by four lanes per n (modes 4g .. 4g+3 each)
   // reduced across the lane groups.
   const int b = lane & 15, g = lane >> 4;
+  const int cwave = !kRoles ? wave : producer ? 0 : wave - Roles::kProducerWaves;
   hm_s4 w_hi[2], w_lo[2], h_hi[2], h_lo[2], v_hi[2], v_lo[2];
   float q1[2][4], q2[2][4], q4[2][4], q8[2][4], qb[2][4], carry[2][4];
 #pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const size_t c = c0 + 2 * wave + k;
+  for (int k = 0; k < 2 && consumer; ++k) {
+    const size_t c = c0 + 2 * cwave + k;
     // Loads first (one round trip): p of mode b, p and R of modes 4g + v.
     const float p_b = b < S ? poles[c * S + b] : 0.0F;
     float p_g[4], r_g[4];
@@ -2022,7 +2050,7 @@ __global__ __launch_bounds__(kHmThreads, 16 / kHmChannels) void hcl_mfma_kernel(
     const int row0 = 16 * (col_ok ? b : 0) + 4 * g;
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-      const int ch = 2 * wave + k;
+      const int ch = 2 * cwave + k;
       ub_hi[k] = *reinterpret_cast<const hm_s4 *>(uh + ch * Shape::kUStride + hm_upos(row0));
       ub_lo[k] = *reinterpret_cast<const hm_s4 *>(ul + ch * Shape::kUStride + hm_upos(row0));
       x2_frag[k] = *reinterpret_cast<const f32x4 *>(&xy_s[step % 3][ch][hm_ypos(row0)]);
@@ -2098,7 +2126,7 @@ __global__ __launch_bounds__(kHmThreads, 16 / kHmChannels) void hcl_mfma_kernel(
     if (col_ok) {
 #pragma unroll
       for (int k = 0; k < 2; ++k) {
-        f32x4 *xy = reinterpret_cast<f32x4 *>(&xy_s[step % 3][2 * wave + k][hm_ypos(row0)]);
+        f32x4 *xy = reinterpret_cast<f32x4 *>(&xy_s[step % 3][2 * cwave + k][hm_ypos(row0)]);
         const f32x4 x2 = x2_frag[k];
         const f32x4 y = y_acc[k];
         *xy = f32x4{x2[0] * y[0], x2[1] * y[1], x2[2] * y[2], x2[3] * y[3]};
@@ -2107,9 +2135,9 @@ __global__ __launch_bounds__(kHmThreads, 16 / kHmChannels) void hcl_mfma_kernel(
   };
 
   // ---- Flush lane: row fr of a step, channels 8 fh .. 8 fh + 7.
-  const bool flusher = tid < Shape::kFlushTasks;
-  const int fr = tid / kHmFlushParts, fh = tid % kHmFlushParts;
-  const int stores = flusher ? HmOut<O>::stores(out) : 0;
+  const int ctid = !kRoles ? tid : producer ? 0 : tid - kHmProducers;
+  const bool flusher = consumer && ctid < Shape::kFlushTasks;
+  const int fr = ctid / kHmFlushParts, fh = ctid % kHmFlushParts;
   // The flush lane's output index advances by one step of rows per call.
   size_t flush_index = static_cast<size_t>(fr) * W + c0 + 8 * fh;
   size_t flush_row = static_cast<size_t>(fr);
@@ -2131,58 +2159,95 @@ __global__ __launch_bounds__(kHmThreads, 16 / kHmChannels) void hcl_mfma_kernel(
   };
 
   // Three projection stages: phase s issues the DMA of step s + 3 and must
-  // see step s + 2 landed before its closing barrier (the DMA of s + 3 and
-  // the flush stores of this and the previous phase may stay in flight). Every wave issues at least
-  // kDmaMin DMAs per step, so waiting down to that many younger ones is
-  // conservative.
-  constexpr int kDmaMin = Shape::kUnits / kHmThreads;
-  for (int step = 0; step < kHmStages && step < steps; ++step)
-    issue(step, std::false_type{});
-  hm_wait(min(steps - 1, kHmStages - 1) * kDmaMin);
-  __syncthreads();
-  produce(0, HmMode<kHmFirst>{});
-  hm_wait(steps > 2 ? kDmaMin : 0);
-  __syncthreads();
-  auto phase = [&](int step, auto steady) __attribute__((always_inline)) {
+  // see step s + 2 landed before its closing barrier. Every producer wave
+  // issues at least kDmaMin DMAs per step, so waiting down to that many
+  // younger ones is conservative.
+  constexpr int kDmaMin = Shape::kUnits / kHmProducers;
+  // Phase s: the producers issue the DMA of step s + 3 and produce step
+  // s + 1, then wait for the DMA of step s + 2 (younger: the one just
+  // issued); the consumers read U and x2 of step s and the y of step s - 1,
+  // form the products, write y = x2 Y in place of x2 and store step s - 1.
+  // The consumers never wait for their stores, which may stay in flight
+  // across barriers. Each role runs its own loop (so that neither holds the
+  // other's registers), with the same barriers.
+  auto producer_phase = [&](int step, auto steady) __attribute__((always_inline)) {
     constexpr bool kSteady = decltype(steady)::value;
     const bool more = kSteady || step + kHmStages < steps;
-    const bool next = kSteady || step + 1 < steps;
-    const bool flushes = kSteady || step >= 1;
-    constexpr auto mode = HmMode<kSteady ? kHmSteady : kHmGeneric>{};
     if (more)
       issue(step + kHmStages, steady);
-    // Every LDS read of the phase first (one round trip), then the work.
+    if (kSteady || step + 1 < steps)
+      produce(step + 1, HmMode<kSteady ? kHmSteady : kHmGeneric>{});
+    if (kSteady || step + 2 < steps)
+      hm_wait(more ? kDmaMin : 0);
+    __syncthreads();
+  };
+  auto consumer_phase = [&](int step, auto steady) __attribute__((always_inline)) {
+    const bool flushes = decltype(steady)::value || step >= 1;
     multiply_load(step);
-    if (next)
-      produce_load(step + 1, mode);
     if (flushes)
       flush_load(step - 1);
     multiply_a();
-    if (next)
-      produce_compute(step + 1, mode);
     multiply_b(step);
-    // The flush stores go last: issued first, they held up the phase's LDS
-    // and DMA work behind the store data path (136 -> 99 us at 7B/8k).
     if (flushes)
       flush_store(steady);
-    // Younger than the DMA of step + 2 (issued in the previous phase): the
-    // previous phase's flush stores, this phase's DMA and flush stores.
-    // Vector memory operations complete in issue order, so the stores may
-    // stay in flight across barriers.
-    if (kSteady || step + 2 < steps)
-      hm_wait((more ? kDmaMin : 0) + (step >= 1 ? stores : 0) + (step >= 2 ? stores : 0));
     __syncthreads();
   };
   // Interior steps 2 <= step < L / kStep - 3: the DMA of step + 3, the
   // production of step + 1 and the flush of step - 1 lie inside [0, L).
   const int steady_end = static_cast<int>(L / kStep) - 3;
-  int step = 0;
-  for (; step < steps && step < 2; ++step)
-    phase(step, std::false_type{});
-  for (; step < steady_end; ++step)
-    phase(step, std::true_type{});
-  for (; step < steps; ++step)
-    phase(step, std::false_type{});
+  auto walk = [&](auto role_phase) __attribute__((always_inline)) {
+    int step = 0;
+    for (; step < steps && step < 2; ++step)
+      role_phase(step, std::false_type{});
+    for (; step < steady_end; ++step)
+      role_phase(step, std::true_type{});
+    for (; step < steps; ++step)
+      role_phase(step, std::false_type{});
+  };
+  // Without roles every wave does both, the consumer's LDS reads first, and
+  // waits for the DMA of step s + 2 behind this phase's DMA and the flush
+  // stores of this and the previous phase (vector memory operations complete
+  // in issue order).
+  const int stores = flusher ? HmOut<O>::stores(out) : 0;
+  auto merged_phase = [&](int step, auto steady) __attribute__((always_inline)) {
+    constexpr bool kSteady = decltype(steady)::value;
+    const bool more = kSteady || step + kHmStages < steps;
+    const bool flushes = kSteady || step >= 1;
+    if (more)
+      issue(step + kHmStages, steady);
+    multiply_load(step);
+    if (flushes)
+      flush_load(step - 1);
+    multiply_a();
+    if (kSteady || step + 1 < steps)
+      produce(step + 1, HmMode<kSteady ? kHmSteady : kHmGeneric>{});
+    multiply_b(step);
+    if (flushes)
+      flush_store(steady);
+    if (kSteady || step + 2 < steps)
+      hm_wait((more ? kDmaMin : 0) + (step >= 1 ? stores : 0) + (step >= 2 ? stores : 0));
+    __syncthreads();
+  };
+  if (producer) {
+    for (int step = 0; step < kHmStages && step < steps; ++step)
+      issue(step, std::false_type{});
+    hm_wait(min(steps - 1, kHmStages - 1) * kDmaMin);
+  }
+  __syncthreads();
+  if (producer) {
+    produce(0, HmMode<kHmFirst>{});
+    hm_wait(steps > 2 ? kDmaMin : 0);
+  }
+  __syncthreads();
+  if constexpr (kRoles) {
+    if (producer) {
+      walk(producer_phase);
+      return;
+    }
+    walk(consumer_phase);
+  } else {
+    walk(merged_phase);
+  }
   flush(steps - 1, std::false_type{});
   // State after row L-1: the last step's block bl holds that row at rl;
   // the lanes of column bl continue from S_{bl-1} over rows 0..rl.
@@ -2195,7 +2260,7 @@ __global__ __launch_bounds__(kHmThreads, 16 / kHmChannels) void hcl_mfma_kernel(
       const uint16_t *ul = &u_s[step & 1][1][0][0];
 #pragma unroll
       for (int k = 0; k < 2; ++k) {
-        const int ch = 2 * wave + k;
+        const int ch = 2 * cwave + k;
         const size_t c = c0 + ch;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -2545,7 +2610,7 @@ Status hyena_forward(int kind, const T *projection, size_t length,
     if (short_len == 3 && planar == 0 && width % kHmChannels == 0) {
       // One pass on MFMA; the modal state stays in the block (no workspace).
       const unsigned blocks = static_cast<unsigned>(width / kHmChannels);
-      hipLaunchKernelGGL((hcl_mfma_kernel<T, O>), dim3(blocks), dim3(kHmThreads), 0, stream,
+      hipLaunchKernelGGL((hcl_mfma_kernel<T, O>), dim3(blocks), dim3(kHmThreads<O>), 0, stream,
                          projection, short_history, wt.short_filter, length, width, wt.poles,
                          wt.residues, wt.direct, static_cast<int>(wt.state), modal_state, out);
       EVO_TRY(launch_status("hcl_mfma_kernel"));
