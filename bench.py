@@ -327,6 +327,8 @@ def main():
     lib.evo_hip_context_prefill_resident.argtypes = [ctypes.c_void_p, ctypes.c_void_p,
                                                       ctypes.c_size_t, ctypes.c_void_p]
 
+    samples = {}
+
     def resident_rate(length, steps, warmup):
         tokens = torch.from_numpy(A.acgt_tokens(length, seed=2).astype(np.int32)).cuda()
         logits = torch.empty(length, shape.vocab, device="cuda")
@@ -339,11 +341,16 @@ def main():
         for _ in range(warmup):
             step()
         torch.cuda.synchronize()
-        start = time.perf_counter()
+        # Each prefill synchronises the context stream at its end, so the
+        # per-step clock reads are the samples of the timed region.
+        marks = [time.perf_counter()]
         for _ in range(steps):
             step()
+            marks.append(time.perf_counter())
         torch.cuda.synchronize()
-        seconds = time.perf_counter() - start
+        seconds = time.perf_counter() - marks[0]
+        samples.setdefault(length, [round(1e3 * (b - a), 3)
+                                    for a, b in zip(marks, marks[1:])])
         return length * steps / seconds, 1e3 * seconds / steps
 
     log(f"timing {args.steps} prefills of {args.tokens} tokens")
@@ -426,6 +433,9 @@ def main():
                    "heads": shape.heads, "ffn": shape.inner,
                    "profile": context.profile, "tok_s_1k": round(rate_1k, 1),
                    "ms_per_step_1k": round(ms_1k, 3),
+                   "samples_ms": samples.get(args.tokens),
+                   "median_ms": round(float(np.median(samples[args.tokens])), 3),
+                   "samples_ms_1k": samples.get(1024),
                    "c_abi_host_logits_tok_s": round(cabi_rate, 1),
                    "decode_tok_s_after_1k": round(decode_rate, 1) if decode_rate else None,
                    "long_context_prefill": long_result},
@@ -445,7 +455,14 @@ def main():
         # out: 335544320 B) -- `frac_split_planes`, from its own launch time.
         hyena = []
         for h in kernels["hyena"]:
-            hyena.append({"kernel": h["kernel"], "achieved": round(h["gbs"], 1),
+            extra = {}
+            if "HCM" in h["kernel"]:
+                # HCM's 128-tap convolution is 2*128*8192*4096 = 8.6 GFLOP
+                # per launch, on MFMA: its fraction of the BF16 peak too.
+                tflops = 2 * 128 * 8192 * 4096 / h["ms"] / 1e9
+                extra = {"mfma_tflops": round(tflops, 1),
+                         "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4)}
+            hyena.append({"kernel": h["kernel"], "achieved": round(h["gbs"], 1), **extra,
                           "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(h["gbs"] / HBM_PEAK_GBS, 4),
                           "traffic": measured_traffic(h["profiled"]), "ms": round(h["ms"], 4),

@@ -733,6 +733,32 @@ evo_status evo_hip_linear(const uint16_t *x_hi, const uint16_t *x_lo, const uint
   });
 }
 
+evo_status evo_hip_linear_normed(const float *x, size_t m, size_t k, const float *scale,
+                                 float eps, int split, const uint16_t *w, size_t n, float *out,
+                                 void *stream) {
+  return protect([&]() -> evo_status {
+    return publish(evo::hip::gemm_bf16w_normed(
+        evo::hip::RowNorm{x, scale, eps, k}, split != 0, w,
+        evo::hip::GemmOutput{out, nullptr, nullptr, n}, m, n, k, evo::hip::kGemmStore, nullptr,
+        nullptr, false, 0, static_cast<hipStream_t>(stream)));
+  });
+}
+
+evo_status evo_hip_fp8_linear_normed(const float *x, size_t m, size_t k, const float *scale,
+                                     float eps, float input_scale, const uint8_t *w_codes,
+                                     size_t n, float output_scale, int mode, uint16_t *out,
+                                     void *stream) {
+  return protect([&]() -> evo_status {
+    if (mode != 0 && mode != 1)
+      return publish({evo::ErrorCode::kInvalidArgument,
+                      "invalid_argument: evo_hip_fp8_linear_normed takes modes 0 and 1"});
+    return publish(evo::hip::fp8_linear_normed(
+        evo::hip::RowNorm{x, scale, eps, k}, input_scale, w_codes, out, m, n, k, output_scale,
+        mode == 0 ? evo::hip::kFp8MfmaK32 : evo::hip::kFp8MfmaK128,
+        static_cast<hipStream_t>(stream)));
+  });
+}
+
 evo_status evo_hip_linear_split(const uint16_t *x_hi, const uint16_t *x_lo, const uint16_t *w,
                                 const uint16_t *bias, const float *residual, size_t m,
                                 size_t n, size_t k, float *out, float *workspace,

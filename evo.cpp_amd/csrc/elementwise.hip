@@ -7,6 +7,7 @@
 // thread reads 16-byte vectors, the sum of squares is reduced with wave
 // shuffles and one LDS exchange (F32 throughout).
 #include "common.hpp"
+#include "row_norm.hpp"
 #include "ops.hpp"
 
 namespace evo::hip {
@@ -31,13 +32,6 @@ __global__ void embed_kernel(const uint32_t *__restrict__ tokens, size_t rows,
   }
 }
 
-__device__ inline float wave_sum(float v) {
-#pragma unroll
-  for (int offset = 32; offset > 0; offset >>= 1)
-    v += __shfl_xor(v, offset, 64);
-  return v;
-}
-
 __global__ __launch_bounds__(256) void rms_norm_kernel(
     const float *__restrict__ x, size_t width, const float *__restrict__ scale,
     float eps, float *__restrict__ out, uint16_t *__restrict__ out_hi,
@@ -48,28 +42,21 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(
   float sum = 0.0F;
   const bool vec = (width % 4) == 0;
   if (vec) {
-    for (size_t c = threadIdx.x * 4; c < width; c += 256 * 4) {
-      const float4 v = *reinterpret_cast<const float4 *>(src + c);
-      sum += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-    }
+    for (size_t c = threadIdx.x * 4; c < width; c += 256 * 4)
+      sum = norm_square_sum(*reinterpret_cast<const float4 *>(src + c), sum);
   } else {
     for (size_t c = threadIdx.x; c < width; c += 256)
-      sum += src[c] * src[c];
+      sum = fmaf(src[c], src[c], sum);
   }
-  sum = wave_sum(sum);
-  if ((threadIdx.x & 63) == 0)
-    partial[threadIdx.x >> 6] = sum;
-  __syncthreads();
-  const float total = partial[0] + partial[1] + partial[2] + partial[3];
-  const float denominator = sqrtf(total / static_cast<float>(width)) + eps;
+  const float denominator = norm_denominator(sum, width, eps, partial);
   if (vec) {
     // Four values per thread per pass: 16-byte F32 and 8-byte plane stores,
     // 4-byte code stores.
     for (size_t c = threadIdx.x * 4; c < width; c += 256 * 4) {
       const float4 v = *reinterpret_cast<const float4 *>(src + c);
       const float4 g = *reinterpret_cast<const float4 *>(scale + c);
-      const float y[4] = {v.x / denominator * g.x, v.y / denominator * g.y,
-                          v.z / denominator * g.z, v.w / denominator * g.w};
+      const float y[4] = {norm_value(v.x, denominator, g.x), norm_value(v.y, denominator, g.y),
+                          norm_value(v.z, denominator, g.z), norm_value(v.w, denominator, g.w)};
       const size_t index = row * width + c;
       if (out != nullptr)
         *reinterpret_cast<float4 *>(out + index) = make_float4(y[0], y[1], y[2], y[3]);
@@ -92,7 +79,7 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(
   }
   const SplitOut planes{out_hi, out_lo};
   for (size_t c = threadIdx.x; c < width; c += 256) {
-    const float value = src[c] / denominator * scale[c];
+    const float value = norm_value(src[c], denominator, scale[c]);
     const size_t index = row * width + c;
     if (out != nullptr)
       out[index] = value;
@@ -124,22 +111,18 @@ __global__ __launch_bounds__(256) void rms_norm_reg_kernel(
   for (int j = 0; j < kVec; ++j) {
     const size_t c = threadIdx.x * 4 + j * 1024;
     v[j] = c < width ? *reinterpret_cast<const float4 *>(src + c) : make_float4(0, 0, 0, 0);
-    sum += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
+    if (c < width)
+      sum = norm_square_sum(v[j], sum);
   }
-  sum = wave_sum(sum);
-  if ((threadIdx.x & 63) == 0)
-    partial[threadIdx.x >> 6] = sum;
-  __syncthreads();
-  const float total = partial[0] + partial[1] + partial[2] + partial[3];
-  const float denominator = sqrtf(total / static_cast<float>(width)) + eps;
+  const float denominator = norm_denominator(sum, width, eps, partial);
 #pragma unroll
   for (int j = 0; j < kVec; ++j) {
     const size_t c = threadIdx.x * 4 + j * 1024;
     if (c >= width)
       break;
     const float4 g = *reinterpret_cast<const float4 *>(scale + c);
-    const float y[4] = {v[j].x / denominator * g.x, v[j].y / denominator * g.y,
-                        v[j].z / denominator * g.z, v[j].w / denominator * g.w};
+    const float y[4] = {norm_value(v[j].x, denominator, g.x), norm_value(v[j].y, denominator, g.y),
+                        norm_value(v[j].z, denominator, g.z), norm_value(v[j].w, denominator, g.w)};
     const size_t index = row * width + c;
     if (out != nullptr) {
       const f32x4v o = {y[0], y[1], y[2], y[3]};

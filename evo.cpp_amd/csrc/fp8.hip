@@ -25,6 +25,7 @@
 #include <type_traits>
 
 #include "common.hpp"
+#include "row_norm.hpp"
 #include "ops.hpp"
 
 namespace evo::hip {
@@ -324,11 +325,13 @@ __device__ inline void decode16(const uint4 codes, float (&out)[16]) {
 template <int kChunk, int kM, typename Out>
 __global__ __launch_bounds__(256) void fp8_gemv_kernel(
     const uint8_t *__restrict__ a, const uint8_t *__restrict__ w, Out *__restrict__ out,
-    int M, int N, int K, float output_scale) {
+    int M, int N, int K, float output_scale, const RowNorm norm, float code_scale) {
   constexpr int kLanesPerChunk = kChunk / 16;
   constexpr int kRowsPerWave = kGemv8Rows / 4;
-  // LDS: chunk sums [kGemv8Rows][M][K/kChunk].
+  // LDS: chunk sums [kGemv8Rows][M][K/kChunk], then (folded norm) the
+  // activation codes [M][K].
   extern __shared__ float chunk_s[];
+  __shared__ float norm_partial[4];
   const int chunks = K / kChunk;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int row0 = blockIdx.x * kGemv8Rows + wave * kRowsPerWave;
@@ -344,6 +347,31 @@ __global__ __launch_bounds__(256) void fp8_gemv_kernel(
   uint4 codes[kRowsPerWave];
   if (k < K)
     load_codes(k, codes);
+  // (The first weights are in flight while the block forms the activation
+  // codes of a folded norm.)
+  uint8_t *codes_s = reinterpret_cast<uint8_t *>(chunk_s + kGemv8Rows * M * chunks);
+  const bool folded = norm.x != nullptr;
+  if (folded) {
+    // The codes rms_norm would write, e4m3(bf16(norm(x)) * code_scale),
+    // formed by this block into LDS.
+#pragma unroll
+    for (int m = 0; m < kM; ++m) {
+      const float *row = norm.x + m * norm.ld;
+      const float denominator = row_norm_denominator(row, K, norm.eps, norm_partial);
+      for (int c = tid * 4; c < K; c += 1024) {
+        const float4 v = *reinterpret_cast<const float4 *>(row + c);
+        const float4 g = *reinterpret_cast<const float4 *>(norm.scale + c);
+        const float y[4] = {norm_value(v.x, denominator, g.x), norm_value(v.y, denominator, g.y),
+                            norm_value(v.z, denominator, g.z), norm_value(v.w, denominator, g.w)};
+        uint8_t code[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          code[e] = encode_e4m3(round_bf16(y[e]) * code_scale);
+        *reinterpret_cast<uint32_t *>(codes_s + m * K + c) = __builtin_bit_cast(uint32_t, code);
+      }
+      __syncthreads();
+    }
+  }
   for (; k < K; k += 1024) {
     uint4 next[kRowsPerWave];
     if (k + 1024 < K)
@@ -351,7 +379,9 @@ __global__ __launch_bounds__(256) void fp8_gemv_kernel(
     float av[kM][16];
 #pragma unroll
     for (int m = 0; m < kM; ++m)
-      decode16(*reinterpret_cast<const uint4 *>(a + static_cast<size_t>(m) * K + k), av[m]);
+      decode16(folded ? *reinterpret_cast<const uint4 *>(codes_s + m * K + k)
+                      : *reinterpret_cast<const uint4 *>(a + static_cast<size_t>(m) * K + k),
+               av[m]);
 #pragma unroll
     for (int r = 0; r < kRowsPerWave; ++r) {
       float wv[16];
@@ -418,7 +448,19 @@ Status e4m3_quantize_bf16(const uint16_t *x, size_t n, float scale,
 template <typename Out>
 Status fp8_linear_impl(const uint8_t *in_codes, const uint8_t *w_codes, Out *out,
                        size_t M, size_t N, size_t K, float output_scale,
-                       Fp8Mode mode, hipStream_t stream) {
+                       Fp8Mode mode, hipStream_t stream, const RowNorm *norm = nullptr,
+                       float code_scale = 0.0F) {
+  if (norm != nullptr) {
+    if (norm->x == nullptr || norm->scale == nullptr || M > static_cast<size_t>(kGemv8MaxM) ||
+        K > static_cast<size_t>(kGemv8MaxK) || mode == kFp8Exact || K % kBK != 0 ||
+        norm->ld < K || norm->ld % 4 != 0 || reinterpret_cast<uintptr_t>(norm->x) % 16 != 0 ||
+        reinterpret_cast<uintptr_t>(norm->scale) % 16 != 0 ||
+        !(code_scale > 0.0F && __builtin_isfinite(code_scale)))
+      return {ErrorCode::kInvalidArgument,
+              "fp8_linear_normed: needs an MFMA mode, M <= 4, K <= 8192 (a multiple of 128), "
+              "16-byte aligned F32 rows and scale, and a positive input scale"};
+    in_codes = w_codes;  // not read
+  }
   if (in_codes == nullptr || w_codes == nullptr || out == nullptr || M == 0 ||
       N == 0 || K == 0 || K % 32 != 0 || !(output_scale > 0.0F) ||
       !__builtin_isfinite(output_scale) || M > (1U << 30) || N > (1U << 30))
@@ -437,7 +479,8 @@ Status fp8_linear_impl(const uint8_t *in_codes, const uint8_t *w_codes, Out *out
   if (M <= static_cast<size_t>(kGemv8MaxM) && K <= static_cast<size_t>(kGemv8MaxK)) {
     const dim3 grid(static_cast<unsigned>(ceil_div(N, kGemv8Rows)));
     const int chunk = mode == kFp8MfmaK32 ? 32 : 128;
-    const size_t lds = kGemv8Rows * M * (K / chunk) * sizeof(float);
+    const size_t lds = kGemv8Rows * M * (K / chunk) * sizeof(float) +
+                       (norm != nullptr ? M * K : 0);
     auto pick = [&](auto rows_c) {
       constexpr int kM = decltype(rows_c)::value;
       return mode == kFp8MfmaK32 ? fp8_gemv_kernel<32, kM, Out> : fp8_gemv_kernel<128, kM, Out>;
@@ -451,8 +494,9 @@ Status fp8_linear_impl(const uint8_t *in_codes, const uint8_t *w_codes, Out *out
                                              hipFuncAttributeMaxDynamicSharedMemorySize,
                                              static_cast<int>(lds)),
                          "fp8_gemv_kernel LDS opt-in"));
+    const RowNorm folded = norm != nullptr ? *norm : RowNorm{nullptr, nullptr, 0.0F, 0};
     hipLaunchKernelGGL(kernel, grid, dim3(256), lds, stream, in_codes, w_codes, out, m, n, k,
-                       output_scale);
+                       output_scale, folded, code_scale);
     return launch_status("fp8_gemv_kernel");
   }
   const auto kernel = mode == kFp8MfmaK32 ? fp8_mfma_kernel<32, Out> : fp8_mfma_kernel<128, Out>;
@@ -477,6 +521,13 @@ Status fp8_linear(const uint8_t *in_codes, const uint8_t *w_codes, uint16_t *out
                   size_t M, size_t N, size_t K, float output_scale,
                   Fp8Mode mode, hipStream_t stream) {
   return fp8_linear_impl(in_codes, w_codes, out, M, N, K, output_scale, mode, stream);
+}
+
+Status fp8_linear_normed(const RowNorm &norm, float input_scale, const uint8_t *w_codes,
+                         uint16_t *out, size_t M, size_t N, size_t K, float output_scale,
+                         Fp8Mode mode, hipStream_t stream) {
+  return fp8_linear_impl(nullptr, w_codes, out, M, N, K, output_scale, mode, stream, &norm,
+                         input_scale);
 }
 
 }  // namespace evo::hip

@@ -28,6 +28,7 @@
 #include <type_traits>
 
 #include "common.hpp"
+#include "row_norm.hpp"
 #include "ops.hpp"
 
 namespace evo::hip {
@@ -489,8 +490,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(
     const uint16_t *__restrict__ a_hi, const uint16_t *__restrict__ a_lo, int lda,
     const uint16_t *__restrict__ W, int M, int N, int K, float *__restrict__ C,
     uint16_t *__restrict__ c_hi, uint16_t *__restrict__ c_lo, int ldc,
-    const Epilogue epi) {
+    const Epilogue epi, const RowNorm norm) {
   __shared__ float partial[4][kGemvRows][kGemvMaxM];
+  __shared__ float norm_partial[4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int unit = blockIdx.x;  // this block's 8 rows
   const bool gated = epi.mode == kGemmGated;
@@ -523,6 +525,16 @@ __global__ __launch_bounds__(256) void gemv_kernel(
   uint4 wv[kGemvRows];
   if (k < K)
     load_w(k, wv);
+  // Folded RMSNorm: the denominators of the block's activation rows, formed
+  // while the first weights are in flight.
+  float denominator[kM];
+  if (norm.x != nullptr) {
+#pragma unroll
+    for (int m = 0; m < kM; ++m) {
+      denominator[m] = row_norm_denominator(norm.x + m * norm.ld, K, norm.eps, norm_partial);
+      __syncthreads();
+    }
+  }
   for (; k < K; k += 2048) {
     uint4 wn[kGemvRows];
     if (k + 2048 < K)
@@ -530,6 +542,23 @@ __global__ __launch_bounds__(256) void gemv_kernel(
     float x[kM][8];
 #pragma unroll
     for (int m = 0; m < kM; ++m) {
+      if (norm.x != nullptr) {
+        // The planes rms_norm would write: hi = bf16(y), lo = bf16(y - hi).
+        const float *xs = norm.x + m * norm.ld + k;
+        const float4 v0 = *reinterpret_cast<const float4 *>(xs);
+        const float4 v1 = *reinterpret_cast<const float4 *>(xs + 4);
+        const float4 g0 = *reinterpret_cast<const float4 *>(norm.scale + k);
+        const float4 g1 = *reinterpret_cast<const float4 *>(norm.scale + k + 4);
+        const float xv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float y = norm_value(xv[e], denominator[m], gv[e]);
+          const float hi = bf16_to_f32(f32_to_bf16(y));
+          x[m][e] = hi + (kSplit ? bf16_to_f32(f32_to_bf16(y - hi)) : 0.0F);
+        }
+        continue;
+      }
       const uint4 h = *reinterpret_cast<const uint4 *>(a_hi + static_cast<size_t>(m) * lda + k);
       const uint16_t *hs = reinterpret_cast<const uint16_t *>(&h);
       uint4 l = make_uint4(0, 0, 0, 0);
@@ -656,16 +685,29 @@ Status split_planes(const float *x, size_t n, uint16_t *hi, uint16_t *lo,
   return launch_status("split_kernel");
 }
 
-Status gemm_bf16w(const Activation &a, const uint16_t *W, const GemmOutput &out,
-                  size_t M, size_t N, size_t K, GemmEpilogue mode,
-                  const uint16_t *bias, const float *residual, bool gelu,
-                  size_t gated_width, hipStream_t stream, float *split_workspace,
-                  size_t split_workspace_bytes) {
-  const bool split = a.lo != nullptr;
-  if (a.hi == nullptr || W == nullptr || M == 0 || N == 0 || K == 0 || K % 8 != 0 ||
-      a.ld < K || a.ld % 8 != 0 || M > (1U << 30) || N > (1U << 30) || K > (1U << 30))
+namespace {
+
+// Shared body of gemm_bf16w (norm == nullptr) and gemm_bf16w_normed.
+Status gemm_impl(const Activation &a, const RowNorm *norm, bool split, const uint16_t *W,
+                 const GemmOutput &out, size_t M, size_t N, size_t K, GemmEpilogue mode,
+                 const uint16_t *bias, const float *residual, bool gelu,
+                 size_t gated_width, hipStream_t stream, float *split_workspace,
+                 size_t split_workspace_bytes) {
+  if (norm != nullptr) {
+    if (norm->x == nullptr || norm->scale == nullptr || M > static_cast<size_t>(kGemvMaxM) ||
+        norm->ld < K || norm->ld % 4 != 0 ||
+        reinterpret_cast<uintptr_t>(norm->x) % 16 != 0 ||
+        reinterpret_cast<uintptr_t>(norm->scale) % 16 != 0)
+      return {ErrorCode::kInvalidArgument,
+              "gemm_bf16w_normed: needs M <= 4 and 16-byte aligned F32 rows and scale"};
+  } else if (a.hi == nullptr || a.ld < K || a.ld % 8 != 0) {
     return {ErrorCode::kInvalidArgument,
-            "gemm_bf16w: null operand or unsupported shape (K and lda multiples of 8)"};
+            "gemm_bf16w: null activation or unsupported stride (lda a multiple of 8)"};
+  }
+  if (W == nullptr || M == 0 || N == 0 || K == 0 || K % 8 != 0 ||
+      M > (1U << 30) || N > (1U << 30) || K > (1U << 30))
+    return {ErrorCode::kInvalidArgument,
+            "gemm_bf16w: null operand or unsupported shape (K a multiple of 8)"};
   if ((mode == kGemmBias || mode == kGemmBiasResidual) && bias == nullptr)
     return {ErrorCode::kInvalidArgument, "gemm_bf16w: bias epilogue needs a bias"};
   if ((mode == kGemmResidual || mode == kGemmBiasResidual) && residual == nullptr)
@@ -690,12 +732,13 @@ Status gemm_bf16w(const Activation &a, const uint16_t *W, const GemmOutput &out,
     const dim3 gemv_grid(static_cast<unsigned>(ceil_div(N, kGemvRows)));
     auto launch = [&](auto rows_c) {
       constexpr int kM = decltype(rows_c)::value;
+      const RowNorm folded = norm != nullptr ? *norm : RowNorm{nullptr, nullptr, 0.0F, 0};
       if (split)
         hipLaunchKernelGGL((gemv_kernel<true, kM>), gemv_grid, dim3(256), 0, stream, a.hi,
-                           a.lo, lda, W, m, n, k, out.f32, out.hi, out.lo, ldc, epi);
+                           a.lo, lda, W, m, n, k, out.f32, out.hi, out.lo, ldc, epi, folded);
       else
         hipLaunchKernelGGL((gemv_kernel<false, kM>), gemv_grid, dim3(256), 0, stream, a.hi,
-                           a.lo, lda, W, m, n, k, out.f32, out.hi, out.lo, ldc, epi);
+                           a.lo, lda, W, m, n, k, out.f32, out.hi, out.lo, ldc, epi, folded);
     };
     switch (M) {
       case 1: launch(std::integral_constant<int, 1>{}); break;
@@ -752,6 +795,25 @@ Status gemm_bf16w(const Activation &a, const uint16_t *W, const GemmOutput &out,
     hipLaunchKernelGGL(gemm_staged_kernel<false>, grid, dim3(kThreads), 0, stream, a.hi, a.lo,
                        lda, W, m, n, k, out.f32, out.hi, out.lo, ldc, epi);
   return launch_status("gemm_staged_kernel");
+}
+
+}  // namespace
+
+Status gemm_bf16w(const Activation &a, const uint16_t *W, const GemmOutput &out,
+                  size_t M, size_t N, size_t K, GemmEpilogue mode,
+                  const uint16_t *bias, const float *residual, bool gelu,
+                  size_t gated_width, hipStream_t stream, float *split_workspace,
+                  size_t split_workspace_bytes) {
+  return gemm_impl(a, nullptr, a.lo != nullptr, W, out, M, N, K, mode, bias, residual, gelu,
+                   gated_width, stream, split_workspace, split_workspace_bytes);
+}
+
+Status gemm_bf16w_normed(const RowNorm &norm, bool split, const uint16_t *W,
+                         const GemmOutput &out, size_t M, size_t N, size_t K,
+                         GemmEpilogue mode, const uint16_t *bias, const float *residual,
+                         bool gelu, size_t gated_width, hipStream_t stream) {
+  return gemm_impl(Activation{nullptr, nullptr, K}, &norm, split, W, out, M, N, K, mode, bias,
+                   residual, gelu, gated_width, stream, nullptr, 0);
 }
 
 }  // namespace evo::hip

@@ -2362,27 +2362,29 @@ __global__ void short_history_kernel(const T *__restrict__ P, size_t L,
 
 
 // ---- One-row continuation (the decode step) of the whole operator in one
-// launch. A block of 256 threads owns 64 channels; thread (g, lane) of
-// channel lane reads history rows g, g + 4, ... (each row once) into
-// registers, adds its share of the inner FIR (HCS / HCM), and after a
-// barrier writes them one row down (the new u goes to the last row); the
-// four partial sums meet in LDS and group 0 finishes the channel: short FIR
-// and gates from the short history and the projection row, the modal
-// recurrence instead for HCL (state updated in place), the outer gate, and
-// the projection row appended to the short history. Sums as in
-// hyena_fir_kernel except that the history part is added per row group
-// (groups 0..3 in order).
-constexpr int kDecodeRowsPerThread = 32;  // ceil(127 / 4)
+// launch. A block of 1024 threads (16 groups of 64) owns 64 channels:
+// thread (g, lane) of channel lane reads inner-history rows g, g + 16, ...
+// (each row once) into registers and adds its share of the inner FIR (HCS /
+// HCM), or, for HCL, loads the pole, residue and state of modes 4g .. 4g+3
+// (groups 0..3); group 0 forms the short FIR and gates of the projection
+// row. After a barrier the history rows move one row down (the new u goes
+// to the last row), group 1 shifts the short history, the HCL groups update
+// their modes; the partial sums meet in LDS and group 0 finishes the
+// channel (outer gate). Sums as in hyena_fir_kernel except that the history
+// part is added per row group (groups 0..15 in order); the modal sum adds
+// the four mode groups in order.
+constexpr int kDecodeGroups = 16;
+constexpr int kDecodeRowsPerThread = 8;  // ceil(127 / 16)
 
 template <typename T, typename O>
-__global__ __launch_bounds__(256) void hyena_decode_kernel(
+__global__ __launch_bounds__(64 * kDecodeGroups) void hyena_decode_kernel(
     int kind, const T *__restrict__ P, float *__restrict__ short_history,
     const uint16_t *__restrict__ short_filter, int short_len, float *__restrict__ inner_history,
     const float *__restrict__ filter, size_t groups, int k, int causal,
     const float *__restrict__ direct, const float *__restrict__ poles,
     const float *__restrict__ residues, float *__restrict__ modal_state, int S, size_t W,
     O out) {
-  __shared__ float partial_s[4][64];
+  __shared__ float partial_s[kDecodeGroups][64];
   __shared__ float u_s[64];
   const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
   const size_t c = blockIdx.x * 64ULL + lane;
@@ -2403,14 +2405,28 @@ __global__ __launch_bounds__(256) void hyena_decode_kernel(
     const float *h = filter + (c / (W / groups)) * k;
 #pragma unroll
     for (int i = 0; i < kDecodeRowsPerThread; ++i) {
-      const int old = g + 4 * i;
+      const int old = g + kDecodeGroups * i;
       v[i] = old < hist ? inner_history[old * W + c] : 0.0F;
     }
 #pragma unroll
     for (int i = 0; i < kDecodeRowsPerThread; ++i) {
-      const int old = g + 4 * i;
+      const int old = g + kDecodeGroups * i;
       if (old < hist)
         part += v[i] * h[causal ? k - 1 - old : old];
+    }
+  }
+  // HCL: modes 4g .. 4g+3 of the channel, loaded before the barrier.
+  const bool modal = !fir && valid && g < 4;
+  float pm[4] = {}, rm[4] = {}, st[4] = {};
+  if (modal) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int m = 4 * g + e;
+      if (m < S) {
+        pm[e] = poles[c * S + m];
+        rm[e] = residues[c * S + m];
+        st[e] = modal_state != nullptr ? modal_state[c * S + m] : 0.0F;
+      }
     }
   }
   partial_s[g][lane] = part;
@@ -2418,16 +2434,15 @@ __global__ __launch_bounds__(256) void hyena_decode_kernel(
   if (fir && valid && inner_history != nullptr) {
 #pragma unroll
     for (int i = 0; i < kDecodeRowsPerThread; ++i) {
-      const int old = g + 4 * i;
+      const int old = g + kDecodeGroups * i;
       if (old >= 1 && old < hist)
         inner_history[(old - 1) * W + c] = v[i];
     }
     if (g == 0 && hist > 0)
       inner_history[(hist - 1) * W + c] = u_s[lane];
   }
-  if (g != 0 || !valid)
-    return;
-  if (short_history != nullptr && short_len > 1) {
+  if (g == 1 && valid && short_history != nullptr && short_len > 1) {
+    // Group 0 read the short history before the barrier.
     const int rows = short_len - 1;
 #pragma unroll
     for (int s = 0; s < 3; ++s) {
@@ -2437,20 +2452,37 @@ __global__ __launch_bounds__(256) void hyena_decode_kernel(
       short_history[(rows - 1) * cols3 + col] = load_act(P, col);
     }
   }
+  if (!fir) {
+    if (modal) {
+      const float uc = u_s[lane];
+      float sum = 0.0F;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = 4 * g + e;
+        if (m < S) {
+          st[e] = pm[e] * st[e] + uc;
+          if (modal_state != nullptr)
+            modal_state[c * S + m] = st[e];
+          sum += rm[e] * st[e];
+        }
+      }
+      partial_s[g][lane] = sum;
+    }
+    __syncthreads();  // the mode groups' sums
+  }
+  if (g != 0 || !valid)
+    return;
   float total;
   if (!fir) {
-    float modal = 0.0F;
-    for (int m = 0; m < S; ++m) {
-      float st = modal_state != nullptr ? modal_state[c * S + m] : 0.0F;
-      st = poles[c * S + m] * st + u;
-      if (modal_state != nullptr)
-        modal_state[c * S + m] = st;
-      modal += residues[c * S + m] * st;
-    }
-    total = modal + direct[c] * u;
+    const float modal_sum =
+        ((partial_s[0][lane] + partial_s[1][lane]) + partial_s[2][lane]) + partial_s[3][lane];
+    total = modal_sum + direct[c] * u;
   } else {
     const float *h = filter + (c / (W / groups)) * k;
-    total = ((partial_s[0][lane] + partial_s[1][lane]) + partial_s[2][lane]) + partial_s[3][lane];
+    total = 0.0F;
+#pragma unroll
+    for (int q = 0; q < kDecodeGroups; ++q)
+      total += partial_s[q][lane];
     total += u * h[causal ? 0 : hist];
     if (direct != nullptr)
       total += direct[c] * u;
@@ -2595,7 +2627,8 @@ Status hyena_forward(int kind, const T *projection, size_t length,
         wt.groups != 0 && width % wt.groups == 0 && wt.inner_len >= 1 &&
         wt.inner_len <= 128 && (kind == kHyenaHcs || wt.direct != nullptr)))) {
     const bool hcm = kind == kHyenaHcm;
-    hipLaunchKernelGGL((hyena_decode_kernel<T, O>), dim3(ceil_div(width, 64)), dim3(256), 0,
+    hipLaunchKernelGGL((hyena_decode_kernel<T, O>), dim3(ceil_div(width, 64)),
+                       dim3(64 * kDecodeGroups), 0,
                        stream, kind, projection, short_history, wt.short_filter, short_len,
                        inner_history, wt.inner_filter, wt.groups,
                        static_cast<int>(wt.inner_len), hcm ? 1 : 0,

@@ -12,6 +12,10 @@ namespace evo::hip {
 namespace {
 
 constexpr size_t kArenaRows = 8192;  // activation rows per prefill chunk
+// Chunks of at most this many rows fold their RMSNorms into the few-row
+// products (the gemv kernels' row limit); FP8 folding also needs W <= 8192.
+constexpr size_t kFoldRows = 4;
+constexpr size_t kFoldMaxWidth = 8192;
 constexpr float kFp8InputAmax = 8.0F;  // activation amax of load-time FP8 conversion
 // Split-K partials of short-prompt GEMMs (splits x rows x N F32; the split
 // count is capped so that it fits).
@@ -427,26 +431,37 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
   const Activation mixed{mixed_hi, split ? mixed_lo : nullptr, w};
   const Activation gated{gated_hi, split ? gated_lo : nullptr, c.inner};
   const SplitOut mixed_out{mixed_hi, split ? mixed_lo : nullptr};
+  // Few-row chunks (decode) fold each RMSNorm into the product that reads
+  // it (same values, one launch and round trip less per norm).
+  const bool fold = rows <= kFoldRows;
   for (size_t i = 0; i < c.layers; ++i) {
     const Layer &L = model_->layer[i];
     Cache &k = cache_[i];
-    if (L.fp8) {
-      // The norm writes only the E4M3 codes of bf16(x) * input_scale: the
-      // projection is the sole consumer of this normed activation.
-      EVO_TRY(rms_norm(hidden, rows, w, L.pre_norm.as<float>(), c.eps, nullptr, nullptr,
-                       nullptr, stream_, codes_.as<uint8_t>(), L.fp8_input_scale));
-    } else {
-      EVO_TRY(rms_norm(hidden, rows, w, L.pre_norm.as<float>(), c.eps, nullptr, normed_hi,
-                       split ? normed_lo : nullptr, stream_));
-    }
+    const RowNorm pre{hidden, L.pre_norm.as<float>(), c.eps, w};
     if (L.fp8) {
       const Fp8Mode mode = (w % 128 != 0) ? kFp8Exact : options_.fp8_mode;
       // The product is BF16 by definition: store it as BF16 and halve the
       // projection's HBM traffic for the Hyena kernels that read it.
-      EVO_TRY(fp8_linear(codes_.as<uint8_t>(), L.projection.as<uint8_t>(),
-                         projected_.as<uint16_t>(), rows, 3 * w, w, L.fp8_output_scale,
-                         mode, stream_));
+      if (fold && mode != kFp8Exact && w <= kFoldMaxWidth) {
+        EVO_TRY(fp8_linear_normed(pre, L.fp8_input_scale, L.projection.as<uint8_t>(),
+                                  projected_.as<uint16_t>(), rows, 3 * w, w,
+                                  L.fp8_output_scale, mode, stream_));
+      } else {
+        // The norm writes only the E4M3 codes of bf16(x) * input_scale:
+        // the projection is the sole consumer of this normed activation.
+        EVO_TRY(rms_norm(hidden, rows, w, L.pre_norm.as<float>(), c.eps, nullptr, nullptr,
+                         nullptr, stream_, codes_.as<uint8_t>(), L.fp8_input_scale));
+        EVO_TRY(fp8_linear(codes_.as<uint8_t>(), L.projection.as<uint8_t>(),
+                           projected_.as<uint16_t>(), rows, 3 * w, w, L.fp8_output_scale,
+                           mode, stream_));
+      }
+    } else if (fold) {
+      EVO_TRY(gemm_bf16w_normed(pre, split, L.projection.as<uint16_t>(),
+                                GemmOutput{projected, nullptr, nullptr, 3 * w}, rows, 3 * w, w,
+                                kGemmStore, nullptr, nullptr, false, 0, stream_));
     } else {
+      EVO_TRY(rms_norm(hidden, rows, w, L.pre_norm.as<float>(), c.eps, nullptr, normed_hi,
+                       split ? normed_lo : nullptr, stream_));
       EVO_TRY(gemm_bf16w(normed, L.projection.as<uint16_t>(),
                          GemmOutput{projected, nullptr, nullptr, 3 * w}, rows, 3 * w, w,
                          kGemmStore, nullptr, nullptr, false, 0, stream_));
@@ -496,9 +511,12 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
                        GemmOutput{residual, nullptr, nullptr, w}, rows, w, w,
                        kGemmBiasResidual, L.out_bias.as<uint16_t>(), hidden, false, 0,
                        stream_, workspace_.as<float>(), workspace_.bytes()));
+    // gated = act(l1 x) * (l2 x), act = erf-GELU in block 0 only (`:650-667`).
+    // This norm stays a kernel of its own for few rows too: folded into the
+    // l1/l2 product, each of its N/8 blocks (2816 at 7B) normalises the row
+    // again (40 us against 6 + 32 at 7B).
     EVO_TRY(rms_norm(residual, rows, w, L.post_norm.as<float>(), c.eps, nullptr, normed_hi,
                      split ? normed_lo : nullptr, stream_));
-    // gated = act(l1 x) * (l2 x), act = erf-GELU in block 0 only (`:650-667`)
     EVO_TRY(gemm_bf16w(normed, L.mlp_in.as<uint16_t>(),
                        GemmOutput{nullptr, gated_hi, split ? gated_lo : nullptr, c.inner},
                        rows, 2 * c.inner_padded, w, kGemmGated, nullptr, nullptr, i == 0,
@@ -537,14 +555,21 @@ Status Context::enqueue(const uint32_t *device_tokens, size_t rows, bool initial
                        c.width, hidden_.as<float>(), flag_.as<int>(), stream_));
   EVO_TRY(run_layers(rows, capture_layer, capture));
   if (device_logits != nullptr) {
-    uint16_t *hi = normed_.as<uint16_t>();
-    uint16_t *lo = options_.split_activations ? hi + rows * c.width : nullptr;
-    EVO_TRY(rms_norm(hidden_.as<float>(), rows, c.width, model_->final_norm.as<float>(),
-                     c.eps, nullptr, hi, lo, stream_));
-    EVO_TRY(gemm_bf16w(Activation{hi, lo, c.width}, model_->embedding.as<uint16_t>(),
-                       GemmOutput{device_logits, nullptr, nullptr, c.vocab}, rows, c.vocab,
-                       c.width, kGemmStore, nullptr, nullptr, false, 0, stream_,
-                       workspace_.as<float>(), workspace_.bytes()));
+    const GemmOutput logits{device_logits, nullptr, nullptr, c.vocab};
+    if (rows <= kFoldRows) {
+      EVO_TRY(gemm_bf16w_normed(
+          RowNorm{hidden_.as<float>(), model_->final_norm.as<float>(), c.eps, c.width},
+          options_.split_activations, model_->embedding.as<uint16_t>(), logits, rows,
+          c.vocab, c.width, kGemmStore, nullptr, nullptr, false, 0, stream_));
+    } else {
+      uint16_t *hi = normed_.as<uint16_t>();
+      uint16_t *lo = options_.split_activations ? hi + rows * c.width : nullptr;
+      EVO_TRY(rms_norm(hidden_.as<float>(), rows, c.width, model_->final_norm.as<float>(),
+                       c.eps, nullptr, hi, lo, stream_));
+      EVO_TRY(gemm_bf16w(Activation{hi, lo, c.width}, model_->embedding.as<uint16_t>(), logits,
+                         rows, c.vocab, c.width, kGemmStore, nullptr, nullptr, false, 0,
+                         stream_, workspace_.as<float>(), workspace_.bytes()));
+    }
   }
   position_ = initial ? rows : position_ + rows;
   return Status::Ok();

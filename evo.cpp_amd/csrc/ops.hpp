@@ -43,6 +43,17 @@ struct GemmOutput {
   uint16_t *lo;
   size_t ld;
 };
+// RMSNorm of F32 rows x [M][ld] (scale [K], eps after the square root)
+// folded into a few-row product (M <= 4) as its input: the product's blocks
+// each normalise the rows in the order rms_norm uses, so the result equals
+// rms_norm followed by the unfused product, bit for bit, without the norm's
+// launch and round trip (decode).
+struct RowNorm {
+  const float *x;
+  const float *scale;
+  float eps;
+  size_t ld;
+};
 // C = A . W^T with W BF16 [N,K]; see gemm.hip.
 // With a split workspace (F32), launches with few output tiles (non-gated
 // modes) split K across blocks and sum the partials in split order.
@@ -51,6 +62,12 @@ Status gemm_bf16w(const Activation &a, const uint16_t *W, const GemmOutput &out,
                   const uint16_t *bias, const float *residual, bool gelu,
                   size_t gated_width, hipStream_t stream, float *split_workspace = nullptr,
                   size_t split_workspace_bytes = 0);
+// The same product of norm(x) (M <= 4; `split`: the activation as hi + lo
+// planes, as the hip-f32 profile's rms_norm writes it, else hi only).
+Status gemm_bf16w_normed(const RowNorm &norm, bool split, const uint16_t *W,
+                         const GemmOutput &out, size_t M, size_t N, size_t K,
+                         GemmEpilogue mode, const uint16_t *bias, const float *residual,
+                         bool gelu, size_t gated_width, hipStream_t stream);
 // hi[i] = bf16(x[i]), lo[i] = bf16(x[i] - hi[i]) (lo may be null).
 Status split_planes(const float *x, size_t n, uint16_t *hi, uint16_t *lo,
                     hipStream_t stream);
@@ -76,6 +93,11 @@ Status fp8_linear(const uint8_t *in_codes, const uint8_t *w_codes, float *out,
 Status fp8_linear(const uint8_t *in_codes, const uint8_t *w_codes, uint16_t *out,
                   size_t M, size_t N, size_t K, float output_scale,
                   Fp8Mode mode, hipStream_t stream);
+// The MFMA-mode product (M <= 4) of the codes e4m3(bf16(norm(x)) *
+// input_scale), which the blocks form themselves (the codes rms_norm writes).
+Status fp8_linear_normed(const RowNorm &norm, float input_scale, const uint8_t *w_codes,
+                         uint16_t *out, size_t M, size_t N, size_t K, float output_scale,
+                         Fp8Mode mode, hipStream_t stream);
 
 // ---- Elementwise / normalisation (elementwise.hip).
 Status embed_tokens(const uint32_t *tokens, size_t rows, const uint16_t *table,

@@ -41,6 +41,10 @@ _OPS = {
     "evo_hip_split_f32": (c_int, [c_void, c_size, c_void, c_void, c_void]),
     "evo_hip_linear": (c_int, [c_void, c_void, c_void, c_void, c_void, c_size, c_size,
                                c_size, c_void, c_void]),
+    "evo_hip_linear_normed": (c_int, [c_void, c_size, c_size, c_void, c_float, c_int, c_void,
+                                      c_size, c_void, c_void]),
+    "evo_hip_fp8_linear_normed": (c_int, [c_void, c_size, c_size, c_void, c_float, c_float,
+                                          c_void, c_size, c_float, c_int, c_void, c_void]),
     "evo_hip_linear_split": (c_int, [c_void, c_void, c_void, c_void, c_void, c_size, c_size,
                                      c_size, c_void, c_void, c_size, c_void]),
     "evo_hip_pack_mlp": (c_int, [c_void, c_void, c_size, c_size, c_void, c_void]),

@@ -195,6 +195,24 @@ EVO_API evo_status evo_hip_rms_norm_e4m3(const float *x, size_t rows, size_t wid
                                          const float *scale, float eps, float code_scale,
                                          uint8_t *codes, void *stream);
 
+/* Few-row products (m <= 4, the decode step) of RMSNorm'd rows without the
+ * norm's own launch: each block normalises x [m, k] (F32, 16-byte aligned,
+ * scale [k]) itself in the order evo_hip_rms_norm uses, so the results equal
+ * evo_hip_rms_norm (split planes when split != 0, else hi only) followed by
+ * evo_hip_linear, and evo_hip_rms_norm_e4m3 followed by
+ * evo_hip_fp8_linear_bf16 (modes 0 and 1), bit for bit. They fuse the
+ * reference's `bf16_rms_norm` with `bf16_linear` / the FP8 projection
+ * (`include/evo/cuda/ops.hpp:61-70, 104-120`) for the decode path. */
+EVO_API evo_status evo_hip_linear_normed(const float *x, size_t m, size_t k,
+                                         const float *scale, float eps, int split,
+                                         const uint16_t *w, size_t n, float *out,
+                                         void *stream);
+EVO_API evo_status evo_hip_fp8_linear_normed(const float *x, size_t m, size_t k,
+                                             const float *scale, float eps,
+                                             float input_scale, const uint8_t *w_codes,
+                                             size_t n, float output_scale, int mode,
+                                             uint16_t *out, void *stream);
+
 /* Attention block body: split the Wqkv output [rows, 3W], apply RoPE at
  * positions prefix.., append K/V at `prefix` of the caches, causal softmax
  * attention into out [rows, W] F32. query is workspace of 2*rows*W uint16;

@@ -288,6 +288,64 @@ def test_rms_norm_e4m3_codes(rows, width, code_scale):
     assert np.array_equal(host(codes), expected)
 
 
+@pytest.mark.parametrize("m,k,n", [(1, 4096, 12288), (3, 1920, 520), (4, 4096, 1000)])
+@pytest.mark.parametrize("split", [1, 0])
+def test_linear_normed_equals_norm_then_linear(m, k, n, split):
+    """Decode's folded norm: the product of norm(x) formed inside the
+    product's blocks is bit-identical to rms_norm's planes fed to the
+    few-row product (and so within the linear tests' oracle bounds)."""
+    r = rng(m * 7 + k + n + split)
+    x = r.standard_normal((m, k)).astype(np.float32) * 3
+    scale = (1 + 0.1 * r.standard_normal(k)).astype(np.float32)
+    w = bf16_bits(r.standard_normal((n, k)).astype(np.float32) * 0.02)
+    x_d, s_d, w_d = dev(x), dev(scale), dev(w)
+    hi, lo = empty((m, k), np.uint16), empty((m, k), np.uint16)
+    N.call("evo_hip_rms_norm", p(x_d), m, k, p(s_d), 1e-6, None, p(hi), p(lo), stream())
+    two_step = empty((m, n))
+    N.call("evo_hip_linear", p(hi), p(lo) if split else None, p(w_d), None, None, m, n, k,
+           p(two_step), stream())
+    folded = empty((m, n))
+    N.call("evo_hip_linear_normed", p(x_d), m, k, p(s_d), 1e-6, split, p(w_d), n, p(folded),
+           stream())
+    assert np.array_equal(host(folded).view(np.uint32), host(two_step).view(np.uint32))
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 4096, 12288), (2, 1920, 1000), (4, 4096, 520)])
+@pytest.mark.parametrize("mode", [0, 1])
+def test_fp8_linear_normed_equals_norm_codes_then_linear(m, k, n, mode):
+    """The folded FP8 projection forms the codes rms_norm_e4m3 writes, so
+    its output equals the two-step path bit for bit."""
+    r = rng(m * 11 + k + n + mode)
+    x = r.standard_normal((m, k)).astype(np.float32) * 2
+    scale = (1 + 0.1 * r.standard_normal(k)).astype(np.float32)
+    w_codes = r.integers(0, 0x7e, (n, k), dtype=np.uint8)
+    w_codes |= (r.integers(0, 2, (n, k), dtype=np.uint8) << 7)
+    code_scale, out_scale = 448.0 / 8.0, 1.0 / 448.0
+    x_d, s_d, w_d = dev(x), dev(scale), dev(w_codes)
+    codes = empty((m * k,), np.uint8)
+    N.call("evo_hip_rms_norm_e4m3", p(x_d), m, k, p(s_d), 1e-6, code_scale, p(codes),
+           stream())
+    two_step = empty((m, n), np.uint16)
+    N.call("evo_hip_fp8_linear_bf16", p(codes), p(w_d), p(two_step), m, n, k, out_scale,
+           mode, stream())
+    folded = empty((m, n), np.uint16)
+    N.call("evo_hip_fp8_linear_normed", p(x_d), m, k, p(s_d), 1e-6, code_scale, p(w_d), n,
+           out_scale, mode, p(folded), stream())
+    assert np.array_equal(host(folded), host(two_step))
+
+
+def test_normed_products_reject_unsupported_shapes():
+    x, scale = dev(np.ones((5, 256), np.float32)), dev(np.ones(256, np.float32))
+    w = dev(np.zeros((8, 256), np.uint16))
+    out = empty((5, 8))
+    with pytest.raises(N.OpError):
+        N.call("evo_hip_linear_normed", p(x), 5, 256, p(scale), 1e-6, 1, p(w), 8, p(out),
+               stream())
+    with pytest.raises(N.OpError):
+        N.call("evo_hip_fp8_linear_normed", p(x), 1, 256, p(scale), 1e-6, 1.0, p(w), 8, 1.0,
+               2, p(empty((1, 8), np.uint16)), stream())
+
+
 # --------------------------------------------------------------- Hyena
 def hyena_case(seed, kind, length, width, groups=16, inner_len=7, state=16):
     r = rng(seed)
