@@ -1198,7 +1198,9 @@ __global__ __launch_bounds__(256) void hcl_output_pair_kernel(
 
 // ---- Grouped FIR with k <= 128 (HCM) as a row stream on MFMA.
 // A block owns 64 channels (four 16-channel slices, one per wave; each slice
-// lies in one filter group) and a segment of kMsSegment output rows, walked
+// lies in one filter group) and a segment of kMsSegment output rows (fewer,
+// down to kMsMinSegment, while the grid would have under kMsMinBlocks
+// blocks: a 1024-token prompt at W = 4096 gets 256 blocks, not 64), walked
 // in steps of 32 rows:
 //  1. production (all lanes, two adjacent channels x 4 rows each): short FIR
 //     and gates from the projection rows, u as split BF16 planes into LDS
@@ -1218,6 +1220,8 @@ constexpr int kMsStep = 32;
 constexpr int kMsK = 5;             // K steps in the window
 constexpr int kMsChannels = 64;
 constexpr int kMsSegment = 1024;
+constexpr int kMsMinSegment = 256;
+constexpr unsigned kMsMinBlocks = 256;
 constexpr int kMsLead = 4;
 constexpr int kMsUStride = 40;      // BF16 per channel in the u stage (80 B)
 
@@ -1301,7 +1305,7 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void hyena_fir_mfma_st
     const uint16_t *__restrict__ short_filter, int short_len,
     const float *__restrict__ inner_history, const float *__restrict__ filter,
     size_t group_size, int k, int causal, const float *__restrict__ direct,
-    size_t L, size_t W, unsigned channel_blocks, unsigned segments, O out) {
+    size_t L, size_t W, unsigned channel_blocks, unsigned segments, unsigned seg_len, O out) {
   constexpr int kWin = 3;          // short FIR length
   constexpr int kRows = kWin + 3;  // projection rows per production lane
   // Projection stage of one step: rows R0 - 2 .. R0 + 31 of the block's 64
@@ -1327,8 +1331,8 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void hyena_fir_mfma_st
   const size_t c0 = static_cast<size_t>(linear % channel_blocks) * kMsChannels;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const size_t t0 = static_cast<size_t>(segment) * kMsSegment;
-  const uint32_t seg_rows = static_cast<uint32_t>(min(L - t0, static_cast<size_t>(kMsSegment)));
+  const size_t t0 = static_cast<size_t>(segment) * seg_len;
+  const uint32_t seg_rows = static_cast<uint32_t>(min(L - t0, static_cast<size_t>(seg_len)));
   const int lead = t0 == 0 ? 0 : kMsLead;
   const size_t t_start = t0 - static_cast<size_t>(lead) * kMsStep;  // first produced row
   const int steps = lead + static_cast<int>((seg_rows + kMsStep - 1) / kMsStep);
@@ -2699,11 +2703,14 @@ Status hyena_forward(int kind, const T *projection, size_t length,
     } else if (wt.taps_bf16 && short_len == 3 && planar == 0 && width % kMsChannels == 0 &&
                group_size % 16 == 0 && direct != nullptr) {
       const unsigned cblocks = static_cast<unsigned>(width / kMsChannels);
-      const unsigned segments = ceil_div(length, kMsSegment);
+      unsigned seg_len = kMsSegment;
+      while (seg_len > kMsMinSegment && cblocks * ceil_div(length, seg_len) < kMsMinBlocks)
+        seg_len /= 2;
+      const unsigned segments = ceil_div(length, seg_len);
       hipLaunchKernelGGL((hyena_fir_mfma_stream_kernel<T, O>), dim3(cblocks * segments),
                          dim3(256), 0, stream, projection, short_history, wt.short_filter,
                          short_len, inner_history, wt.inner_filter, group_size, k, causal, direct,
-                         length, width, cblocks, segments, out);
+                         length, width, cblocks, segments, seg_len, out);
       EVO_TRY(launch_status("hyena_fir_mfma_stream_kernel"));
     } else if (width % kChannels == 0 && group_size % 16 == 0) {
       const size_t steps = k <= 8 ? FirMfmaShape<8>::kSteps : FirMfmaShape<128>::kSteps;
