@@ -161,7 +161,8 @@ __global__ __launch_bounds__(kWaves * 64) void fp8_mfma_kernel(
     const uint8_t *__restrict__ a, const uint8_t *__restrict__ w,
     Out *__restrict__ out, int M, int N, int K, float output_scale) {
   extern __shared__ __attribute__((aligned(16))) uint8_t fp8_lds[];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5, col = lane & 31;
   const int wave_m = wave >> 1, wave_n = wave & 1;  // 4 x 2
   const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
@@ -170,9 +171,14 @@ __global__ __launch_bounds__(kWaves * 64) void fp8_mfma_kernel(
   const int block_m = tm * kBM, block_n = tn * kBN;
 
   // DMA op g = wave*7 + i: 1 KB chunk g of the stage (chunks 0..31 = A rows
-  // 8g.., 32..55 = W rows 8(g-32)..); lane l fills unit 64 g' + l.
-  const uint8_t *src[kDmaPerWave];
+  // 8g.., 32..55 = W rows 8(g-32)..); lane l fills unit 64 g' + l. Each op
+  // reads from a wave-uniform base (the block's first A or W row, advanced
+  // by the step's K offset) plus a fixed 32-bit per-lane offset.
+  const uint8_t *a_base = a + static_cast<size_t>(block_m) * K;
+  const uint8_t *w_base = w + static_cast<size_t>(block_n) * K;
+  uint32_t src[kDmaPerWave];
   int dst[kDmaPerWave];
+  bool from_a[kDmaPerWave];
 #pragma unroll
   for (int i = 0; i < kDmaPerWave; ++i) {
     const int g = wave * kDmaPerWave + i;
@@ -180,18 +186,18 @@ __global__ __launch_bounds__(kWaves * 64) void fp8_mfma_kernel(
     const int chunk = is_a ? g : g - kBM / 8;
     const int flat = chunk * 64 + lane;
     const int row = flat >> 3, unit = (flat & 7) ^ ((row >> 1) & 7);
-    if (is_a)
-      src[i] = a + static_cast<size_t>(min(block_m + row, M - 1)) * K + unit * 16;
-    else
-      src[i] = w + static_cast<size_t>(min(block_n + row, N - 1)) * K + unit * 16;
+    const int clamped = is_a ? min(block_m + row, M - 1) - block_m
+                             : min(block_n + row, N - 1) - block_n;
+    src[i] = static_cast<uint32_t>(clamped) * static_cast<uint32_t>(K) + unit * 16;
     dst[i] = (is_a ? 0 : kBM * kBK) + chunk * 1024;
+    from_a[i] = is_a;
   }
   auto issue = [&](int step) {
     uint8_t *stage = fp8_lds + (step % kStages) * kStageBytes;
     const int k0 = step * kBK;
 #pragma unroll
     for (int i = 0; i < kDmaPerWave; ++i)
-      dma16(src[i] + k0, stage + dst[i]);
+      dma16((from_a[i] ? a_base : w_base) + k0, src[i], stage + dst[i]);
   };
 
   f32x16 acc[2][3];
@@ -242,14 +248,28 @@ __global__ __launch_bounds__(kWaves * 64) void fp8_mfma_kernel(
           av[ks][i] = frag32(a_s, wave_m * 64 + i * 32 + col, ks * 4 + half * 2);
       }
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
+      for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int j = 0; j < 3; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+              av[0][i], bv[0][j], acc[i][j], 0, 0, 0, 127, 0, 127);
+      // Second K half: each tile's promotion runs while the next tile's
+      // MFMA executes (only the last tile's truncation is left at the end).
 #pragma unroll
-          for (int j = 0; j < 3; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                av[ks][i], bv[ks][j], acc[i][j], 0, 0, 0, 127, 0, 127);
-      truncate_all();
+      for (int t = 0; t < 6; ++t) {
+        const int i = t / 3, j = t % 3;
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+            av[1][i], bv[1][j], acc[i][j], 0, 0, 0, 127, 0, 127);
+        if (t > 0) {
+          const int pi = (t - 1) / 3, pj = (t - 1) % 3;
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            acc[pi][pj][e] = truncate_e8m13(acc[pi][pj][e]);
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        acc[1][2][e] = truncate_e8m13(acc[1][2][e]);
     } else {
       // Four 32-K chunks, each two K=16 MFMAs then a promotion.
 #pragma unroll
