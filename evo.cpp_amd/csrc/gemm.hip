@@ -231,6 +231,12 @@ __device__ inline int swizzled_unit(int row, int seg) {
 // product favours short, wide wave tiles: 64 x 128 reads 16 fragments per 64
 // MFMAs, 128 x 64 reads 20.
 constexpr int kGemmWavesM = EVO_GEMM_WAVES_M;
+// Tile order: each XCD walks bands of 4 M tiles (tile_of), so its 32
+// concurrent tiles form a 4 x 8 patch: 4 A panels (4 B per element, both
+// planes) and 8 W panels in flight instead of 8 and 4 with bands of 8 --
+// 20 % fewer L2 misses (FETCH_SIZE 1.81 -> 1.44 GB per MLP launch) at the
+// same speed.
+constexpr int kGemmGroupRows = 4;
 
 // Split K: block row blockIdx.y multiplies K range [y K, (y + 1) K) (K is
 // the per-split length, ldw the weight row stride) into C + y c_split.
@@ -262,7 +268,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(
   const int wave_n = wave % kWavesN;
   const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
   int tm, tn;
-  tile_of(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
+  tile_of<kGemmGroupRows>(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
   const int block_m = tm * kBM, block_n = tn * kBN;
 
   // This lane's DMA rows (instructions t = wave*2 + i) and segments.
