@@ -455,24 +455,45 @@ __global__ __launch_bounds__(512) void gemm_kernel(
         }
       }
     } else {
+      // Bias and residual for the whole row of tiles first, then the
+      // stores: C may alias the residual, so a load placed after a store
+      // would wait for it, one memory latency per value.
+      if (bias_mode || res_mode) {
+        float addend[kNJ][4];
+#pragma unroll
+        for (int j = 0; j < kNJ; ++j) {
+          const int col = min(wave_col + j * 16 + r16, N - 1);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int row = min(wave_row + i * 16 + e, M - 1);
+            addend[j][e] = res_mode ? epi.residual[static_cast<size_t>(row) * ldc + col] : 0.0F;
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < kNJ; ++j) {
+          const int col = min(wave_col + j * 16 + r16, N - 1);
+          const float bias = bias_mode ? bf16_to_f32(epi.bias[col]) : 0.0F;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float value = acc[i][j][e];
+            if (bias_mode)
+              value = value + bias;
+            if (res_mode)
+              value = value + addend[j][e];
+            acc[i][j][e] = value;
+          }
+        }
+      }
 #pragma unroll
       for (int j = 0; j < kNJ; ++j) {
         const int col = wave_col + j * 16 + r16;
         if (col >= N)
           continue;
-        const float bias = bias_mode ? bf16_to_f32(epi.bias[col]) : 0.0F;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int row = wave_row + i * 16 + e;
-          if (row < M) {
-            const size_t index = static_cast<size_t>(row) * ldc + col;
-            float value = acc[i][j][e];
-            if (bias_mode)
-              value = value + bias;
-            if (res_mode)
-              value = value + epi.residual[index];
-            C[index] = value;
-          }
+          if (row < M)
+            C[static_cast<size_t>(row) * ldc + col] = acc[i][j][e];
         }
       }
     }
@@ -668,13 +689,19 @@ __global__ void split_k_reduce_kernel(const float *__restrict__ part, int splits
         acc[e] = acc[e] + v[e];
     }
     const size_t index = m * ldc + n;
+    const bool res_mode = epi.mode == kGemmResidual || epi.mode == kGemmBiasResidual;
+    // The four residual loads ahead of the stores (C may alias the residual).
+    float residual[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      residual[e] = res_mode ? epi.residual[index + e] : 0.0F;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       float value = acc[e];
       if (epi.mode == kGemmBias || epi.mode == kGemmBiasResidual)
         value = value + bf16_to_f32(epi.bias[n + e]);
-      if (epi.mode == kGemmResidual || epi.mode == kGemmBiasResidual)
-        value = value + epi.residual[index + e];
+      if (res_mode)
+        value = value + residual[e];
       C[index + e] = value;
     }
   }
