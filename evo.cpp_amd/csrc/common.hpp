@@ -68,16 +68,20 @@ __device__ inline void wait_dma() {
 }
 
 // ---- GEMM tile order.
-// Maps the hardware block id to a (tile_m, tile_n) pair: consecutive ids go
-// to different XCDs, so id -> (xcd, slot) -> contiguous band per XCD.
+// Linear tile of hardware block `id` among `total` blocks: consecutive ids
+// go to different XCDs, so id -> (xcd, slot) -> contiguous band per XCD.
 // XCD x receives total/8 tiles (+1 for the first total%8 XCDs), so the map
 // from hardware id to linear tile is a bijection for every grid size.
-template <int kGroupRows = 8>
-__device__ inline void tile_of(int id, int tiles_m, int tiles_n, int *tm, int *tn) {
-  const int total = tiles_m * tiles_n;
+__device__ inline int xcd_linear(int id, int total) {
   const int q = total / 8, r = total % 8;
   const int xcd = id % 8;
-  const int linear = xcd * q + min(xcd, r) + id / 8;
+  return xcd * q + min(xcd, r) + id / 8;
+}
+
+// Linear tile -> (tile_m, tile_n): groups of kGroupRows tile rows, walked
+// column by column.
+template <int kGroupRows = 8>
+__device__ inline void tile_of_linear(int linear, int tiles_m, int tiles_n, int *tm, int *tn) {
   const int group_size = kGroupRows * tiles_n;
   const int group = linear / group_size;
   const int first_m = group * kGroupRows;
@@ -85,6 +89,12 @@ __device__ inline void tile_of(int id, int tiles_m, int tiles_n, int *tm, int *t
   const int in_group = linear % group_size;
   *tm = first_m + in_group % rows;
   *tn = in_group / rows;
+}
+
+// Hardware block id -> (tile_m, tile_n) over the whole tile grid.
+template <int kGroupRows = 8>
+__device__ inline void tile_of(int id, int tiles_m, int tiles_n, int *tm, int *tn) {
+  tile_of_linear<kGroupRows>(xcd_linear(id, tiles_m * tiles_n), tiles_m, tiles_n, tm, tn);
 }
 
 // ---- E4M3FN encoder: round to nearest even, saturating finite overflow and

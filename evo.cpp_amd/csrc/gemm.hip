@@ -237,26 +237,134 @@ constexpr int kGemmWavesM = EVO_GEMM_WAVES_M;
 // 20 % fewer L2 misses (FETCH_SIZE 1.81 -> 1.44 GB per MLP launch) at the
 // same speed.
 constexpr int kGemmGroupRows = 4;
+constexpr int kGemmWavesN = 8 / kGemmWavesM;
+constexpr int kGemmTM = kBM / kGemmWavesM, kGemmTN = kBN / kGemmWavesN;  // wave tile
+constexpr int kGemmMI = kGemmTM / 16, kGemmNJ = kGemmTN / 16;            // 16 x 16 MFMA tiles
+// CUs of the MI355X: one 256 x 256 tile per CU at a time (144 KB of LDS).
+constexpr int kGemmCUs = 256;
+
+// Epilogue of MFMA tile row i of a block tile (thread layout of
+// gemm_kernel: 8 waves, wave (wave_m, wave_n) owns a kGemmTM x kGemmTN
+// sub-tile). Accumulator e of tile (i, j): row i*16 + 4*(lane/16) + e,
+// column j*16 + lane%16 of the sub-tile. Gated mode: columns [64q, 64q+32)
+// hold l1 rows and [64q+32, 64q+64) the matching l2 rows, so tiles j and
+// j+2 of each 64-column group pair up in-lane.
+__device__ __attribute__((always_inline)) inline void gemm_epilogue_row(
+    f32x4 (&acc)[kGemmNJ], int i, int block_m, int block_n, int wave_m, int wave_n, int lane,
+    int M, int N, float *__restrict__ C, uint16_t *__restrict__ c_hi,
+    uint16_t *__restrict__ c_lo, int ldc, const Epilogue &epi) {
+  constexpr int kNJ = kGemmNJ;
+  const int r16 = lane & 15;
+  const int wave_col = block_n + wave_n * kGemmTN;
+  const int wave_row = block_m + wave_m * kGemmTM + (lane >> 4) * 4;
+  const bool bias_mode = epi.mode == kGemmBias || epi.mode == kGemmBiasResidual;
+  const bool res_mode = epi.mode == kGemmResidual || epi.mode == kGemmBiasResidual;
+  {
+    if (epi.mode == kGemmGated) {
+#pragma unroll
+      for (int j = 0; j < kNJ; ++j) {
+        if ((j & 3) >= 2)
+          continue;  // l2 tiles: consumed with their l1 partner
+        const int col = wave_col / 2 + (j >> 2) * 32 + (j & 3) * 16 + r16;
+        if (col >= epi.gated_width)
+          continue;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int row = wave_row + i * 16 + e;
+          if (row < M) {
+            const float first = acc[j][e];
+            const float value = (epi.gelu ? gelu_erf(first) : first) * acc[j + 2][e];
+            const size_t index = static_cast<size_t>(row) * ldc + col;
+            const uint16_t hi = f32_to_bf16(value);
+            c_hi[index] = hi;
+            if (c_lo != nullptr)
+              c_lo[index] = f32_to_bf16(value - bf16_to_f32(hi));
+          }
+        }
+      }
+    } else {
+      // Bias and residual for the whole row of tiles first, then the
+      // stores: C may alias the residual, so a load placed after a store
+      // would wait for it, one memory latency per value.
+      if (bias_mode || res_mode) {
+        float addend[kNJ][4];
+#pragma unroll
+        for (int j = 0; j < kNJ; ++j) {
+          const int col = min(wave_col + j * 16 + r16, N - 1);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int row = min(wave_row + i * 16 + e, M - 1);
+            addend[j][e] = res_mode ? epi.residual[static_cast<size_t>(row) * ldc + col] : 0.0F;
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < kNJ; ++j) {
+          const int col = min(wave_col + j * 16 + r16, N - 1);
+          const float bias = bias_mode ? bf16_to_f32(epi.bias[col]) : 0.0F;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float value = acc[j][e];
+            if (bias_mode)
+              value = value + bias;
+            if (res_mode)
+              value = value + addend[j][e];
+            acc[j][e] = value;
+          }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kNJ; ++j) {
+        const int col = wave_col + j * 16 + r16;
+        if (col >= N)
+          continue;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int row = wave_row + i * 16 + e;
+          if (row < M)
+            C[static_cast<size_t>(row) * ldc + col] = acc[j][e];
+        }
+      }
+    }
+  }
+}
 
 // Split K: block row blockIdx.y multiplies K range [y K, (y + 1) K) (K is
 // the per-split length, ldw the weight row stride) into C + y c_split.
+// Tail split: blocks [0, full_tiles) own whole tiles (the first full_tiles
+// in tile order); each later pair of blocks takes one remaining tile, block
+// 2t + h the K half h, and stores its raw accumulators in tail_part for
+// gemm_tail_kernel. A launch whose last round would leave most CUs idle
+// (352 tiles on 256 CUs) thus ends in a round of half-length tiles.
 template <bool kSplit>
 __global__ __launch_bounds__(512) void gemm_kernel(
     const uint16_t *__restrict__ a_hi, const uint16_t *__restrict__ a_lo, int lda,
     const uint16_t *__restrict__ W, int ldw, int M, int N, int K, float *__restrict__ C,
     size_t c_split, uint16_t *__restrict__ c_hi, uint16_t *__restrict__ c_lo, int ldc,
-    const Epilogue epi) {
+    const Epilogue epi, int full_tiles, float *__restrict__ tail_part) {
+  const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
+  int linear, half = -1;
+  if (static_cast<int>(blockIdx.x) < full_tiles) {
+    linear = xcd_linear(blockIdx.x, full_tiles);
+  } else {
+    const int t = blockIdx.x - full_tiles;
+    linear = full_tiles + t / 2;
+    half = t % 2;
+  }
+  int tm, tn;
+  tile_of_linear<kGemmGroupRows>(linear, tiles_m, tiles_n, &tm, &tn);
+  const int block_m = tm * kBM, block_n = tn * kBN;
+  const int k_len = half < 0 ? K : K / 2;
   {
-    const size_t k_first = static_cast<size_t>(blockIdx.y) * K;
+    const size_t k_first = static_cast<size_t>(blockIdx.y) * K + (half > 0 ? k_len : 0);
     a_hi += k_first;
     if (kSplit)
       a_lo += k_first;
     W += k_first;
     C += blockIdx.y * c_split;
   }
-  constexpr int kWavesN = 8 / kGemmWavesM;
-  constexpr int kTM = kBM / kGemmWavesM, kTN = kBN / kWavesN;  // wave tile
-  constexpr int kMI = kTM / 16, kNJ = kTN / 16;                // 16 x 16 MFMA tiles
+  constexpr int kWavesN = kGemmWavesN;
+  constexpr int kTM = kGemmTM, kTN = kGemmTN;
+  constexpr int kMI = kGemmMI, kNJ = kGemmNJ;
   constexpr int kPlanes = kSplit ? 3 : 2;  // A hi, (A lo), W
   constexpr int kStage = kPlanes * kPlane;
   __shared__ __attribute__((aligned(16))) uint16_t lds[kStages * kStage];
@@ -266,10 +374,6 @@ __global__ __launch_bounds__(512) void gemm_kernel(
   const int wave = tid >> 6;
   const int wave_m = wave / kWavesN;
   const int wave_n = wave % kWavesN;
-  const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
-  int tm, tn;
-  tile_of<kGemmGroupRows>(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
-  const int block_m = tm * kBM, block_n = tn * kBN;
 
   // This lane's DMA rows (instructions t = wave*2 + i) and segments.
   const uint16_t *src_a_hi[2], *src_a_lo[2], *src_w[2];
@@ -305,7 +409,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(
       for (int e = 0; e < 4; ++e)
         acc[i][j][e] = 0.0F;
 
-  const int steps = K / kBK;
+  const int steps = k_len / kBK;
   issue(0);
   if (steps > 1)
     issue(1);
@@ -422,81 +526,54 @@ __global__ __launch_bounds__(512) void gemm_kernel(
     }
   }
 
-  // Accumulator e of tile (i, j): row i*16 + 4*(lane/16) + e, column
-  // j*16 + lane%16 of the wave's TM x TN sub-tile. Gated mode: columns
-  // [64q, 64q+32) hold l1 rows and [64q+32, 64q+64) the matching l2 rows,
-  // so tiles j and j+2 of each 64-column group pair up in-lane.
-  const int wave_col = block_n + wave_n * kTN;
-  const int wave_row = block_m + wave_m * kTM + (lane >> 4) * 4;
-  const bool bias_mode = epi.mode == kGemmBias || epi.mode == kGemmBiasResidual;
-  const bool res_mode = epi.mode == kGemmResidual || epi.mode == kGemmBiasResidual;
+  if (half >= 0) {
+    // Tail half: the raw accumulators, one coalesced 16-byte unit per lane
+    // and MFMA tile; gemm_tail_kernel adds the halves and runs the epilogue.
+    float *part = tail_part + static_cast<size_t>((linear - full_tiles) * 2 + half) * (kBM * kBN);
 #pragma unroll
-  for (int i = 0; i < kMI; ++i) {
-    if (epi.mode == kGemmGated) {
+    for (int i = 0; i < kMI; ++i)
 #pragma unroll
-      for (int j = 0; j < kNJ; ++j) {
-        if ((j & 3) >= 2)
-          continue;  // l2 tiles: consumed with their l1 partner
-        const int col = wave_col / 2 + (j >> 2) * 32 + (j & 3) * 16 + r16;
-        if (col >= epi.gated_width)
-          continue;
+      for (int j = 0; j < kNJ; ++j)
+        *reinterpret_cast<f32x4 *>(part + ((i * kNJ + j) * 512 + tid) * 4) = acc[i][j];
+    return;
+  }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int row = wave_row + i * 16 + e;
-          if (row < M) {
-            const float first = acc[i][j][e];
-            const float value = (epi.gelu ? gelu_erf(first) : first) * acc[i][j + 2][e];
-            const size_t index = static_cast<size_t>(row) * ldc + col;
-            const uint16_t hi = f32_to_bf16(value);
-            c_hi[index] = hi;
-            if (c_lo != nullptr)
-              c_lo[index] = f32_to_bf16(value - bf16_to_f32(hi));
-          }
-        }
-      }
-    } else {
-      // Bias and residual for the whole row of tiles first, then the
-      // stores: C may alias the residual, so a load placed after a store
-      // would wait for it, one memory latency per value.
-      if (bias_mode || res_mode) {
-        float addend[kNJ][4];
+  for (int i = 0; i < kMI; ++i)
+    gemm_epilogue_row(acc[i], i, block_m, block_n, wave_m, wave_n, lane, M, N, C, c_hi, c_lo,
+                      ldc, epi);
+}
+
+// Tail tiles of a gemm_kernel launch: the two K halves summed (first half
+// first), then the tile's epilogue, in gemm_kernel's thread layout.
+__global__ __launch_bounds__(512) void gemm_tail_kernel(const float *__restrict__ tail_part,
+                                                        int full_tiles, int M, int N,
+                                                        float *__restrict__ C,
+                                                        uint16_t *__restrict__ c_hi,
+                                                        uint16_t *__restrict__ c_lo, int ldc,
+                                                        const Epilogue epi) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
+  int tm, tn;
+  tile_of_linear<kGemmGroupRows>(full_tiles + static_cast<int>(blockIdx.x), tiles_m, tiles_n,
+                                 &tm, &tn);
+  const float *first = tail_part + static_cast<size_t>(blockIdx.x) * 2 * (kBM * kBN);
+  const float *second = first + kBM * kBN;
 #pragma unroll
-        for (int j = 0; j < kNJ; ++j) {
-          const int col = min(wave_col + j * 16 + r16, N - 1);
+  for (int i = 0; i < kGemmMI; ++i) {
+    f32x4 acc[kGemmNJ];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int row = min(wave_row + i * 16 + e, M - 1);
-            addend[j][e] = res_mode ? epi.residual[static_cast<size_t>(row) * ldc + col] : 0.0F;
-          }
-        }
+    for (int j = 0; j < kGemmNJ; ++j) {
+      const int at = ((i * kGemmNJ + j) * 512 + tid) * 4;
+      const f32x4 a = *reinterpret_cast<const f32x4 *>(first + at);
+      const f32x4 b = *reinterpret_cast<const f32x4 *>(second + at);
 #pragma unroll
-        for (int j = 0; j < kNJ; ++j) {
-          const int col = min(wave_col + j * 16 + r16, N - 1);
-          const float bias = bias_mode ? bf16_to_f32(epi.bias[col]) : 0.0F;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float value = acc[i][j][e];
-            if (bias_mode)
-              value = value + bias;
-            if (res_mode)
-              value = value + addend[j][e];
-            acc[i][j][e] = value;
-          }
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < kNJ; ++j) {
-        const int col = wave_col + j * 16 + r16;
-        if (col >= N)
-          continue;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int row = wave_row + i * 16 + e;
-          if (row < M)
-            C[static_cast<size_t>(row) * ldc + col] = acc[i][j][e];
-        }
-      }
+      for (int e = 0; e < 4; ++e)
+        acc[j][e] = a[e] + b[e];
     }
+    gemm_epilogue_row(acc, i, tm * kBM, tn * kBN, wave / kGemmWavesN, wave % kGemmWavesN, lane,
+                      M, N, C, c_hi, c_lo, ldc, epi);
   }
 }
 
@@ -798,14 +875,15 @@ Status gemm_impl(const Activation &a, const RowNorm *norm, bool split, const uin
       const dim3 split_grid(static_cast<unsigned>(tiles), static_cast<unsigned>(splits));
       const int ks = k / splits;
       const size_t plane = M * N;
+      const int all = static_cast<int>(tiles);
       if (split)
         hipLaunchKernelGGL(gemm_kernel<true>, split_grid, dim3(512), 0, stream, a.hi, a.lo,
                            lda, W, k, m, n, ks, split_workspace, plane, nullptr, nullptr, n,
-                           store);
+                           store, all, nullptr);
       else
         hipLaunchKernelGGL(gemm_kernel<false>, split_grid, dim3(512), 0, stream, a.hi, a.lo,
                            lda, W, k, m, n, ks, split_workspace, plane, nullptr, nullptr, n,
-                           store);
+                           store, all, nullptr);
       EVO_TRY(launch_status("gemm_kernel (split K)"));
       const size_t quads = plane / 4;
       const unsigned blocks = static_cast<unsigned>(std::min<size_t>((quads + 255) / 256, 8192));
@@ -813,13 +891,31 @@ Status gemm_impl(const Activation &a, const RowNorm *norm, bool split, const uin
                          split_workspace, splits, m, n, out.f32, ldc, epi);
       return launch_status("split_k_reduce_kernel");
     }
+    // Tail split: when the last round would hold at most half the CUs, its
+    // tiles run as two K halves each (raw partials in the workspace), and
+    // gemm_tail_kernel sums them in order and applies the epilogue.
+    size_t tail = tiles > static_cast<size_t>(kGemmCUs) ? tiles % kGemmCUs : 0;
+    if (tail == 0 || 2 * tail > static_cast<size_t>(kGemmCUs) || split_workspace == nullptr ||
+        reinterpret_cast<uintptr_t>(split_workspace) % 16 != 0 || K % (2 * kBK) != 0 ||
+        K / 2 < 8 * static_cast<size_t>(kBK) ||
+        2 * tail * kBM * kBN * sizeof(float) > split_workspace_bytes)
+      tail = 0;
+    const int full = static_cast<int>(tiles - tail);
+    const dim3 main_grid(static_cast<unsigned>(tiles + tail));
     if (split)
-      hipLaunchKernelGGL(gemm_kernel<true>, grid, dim3(512), 0, stream, a.hi, a.lo, lda,
-                         W, k, m, n, k, out.f32, size_t{0}, out.hi, out.lo, ldc, epi);
+      hipLaunchKernelGGL(gemm_kernel<true>, main_grid, dim3(512), 0, stream, a.hi, a.lo, lda,
+                         W, k, m, n, k, out.f32, size_t{0}, out.hi, out.lo, ldc, epi, full,
+                         split_workspace);
     else
-      hipLaunchKernelGGL(gemm_kernel<false>, grid, dim3(512), 0, stream, a.hi, a.lo, lda,
-                         W, k, m, n, k, out.f32, size_t{0}, out.hi, out.lo, ldc, epi);
-    return launch_status("gemm_kernel");
+      hipLaunchKernelGGL(gemm_kernel<false>, main_grid, dim3(512), 0, stream, a.hi, a.lo, lda,
+                         W, k, m, n, k, out.f32, size_t{0}, out.hi, out.lo, ldc, epi, full,
+                         split_workspace);
+    if (tail == 0)
+      return launch_status("gemm_kernel");
+    EVO_TRY(launch_status("gemm_kernel (tail split)"));
+    hipLaunchKernelGGL(gemm_tail_kernel, dim3(static_cast<unsigned>(tail)), dim3(512), 0, stream,
+                       split_workspace, full, m, n, out.f32, out.hi, out.lo, ldc, epi);
+    return launch_status("gemm_tail_kernel");
   }
   if (split)
     hipLaunchKernelGGL(gemm_staged_kernel<true>, grid, dim3(kThreads), 0, stream, a.hi, a.lo,

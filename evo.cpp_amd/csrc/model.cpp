@@ -520,7 +520,7 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
     EVO_TRY(gemm_bf16w(normed, L.mlp_in.as<uint16_t>(),
                        GemmOutput{nullptr, gated_hi, split ? gated_lo : nullptr, c.inner},
                        rows, 2 * c.inner_padded, w, kGemmGated, nullptr, nullptr, i == 0,
-                       c.inner, stream_));
+                       c.inner, stream_, workspace_.as<float>(), workspace_.bytes()));
     // hidden = gated . l3^T + residual
     EVO_TRY(gemm_bf16w(gated, L.mlp_out.as<uint16_t>(), GemmOutput{hidden, nullptr, nullptr, w},
                        rows, w, c.inner, kGemmResidual, nullptr, residual, false, 0, stream_,

@@ -194,6 +194,44 @@ def test_linear_split_k_matches_oracle(m, n, k, bias, residual):
     assert np.array_equal(host(parted), host(unsplit))
 
 
+@pytest.mark.parametrize("m,n,k,bias,residual", [(256, 76800, 512, True, True),
+                                                  (600, 25000, 1024, False, False),
+                                                  (600, 25000, 1024, False, True)])
+def test_linear_tail_split_matches_unsplit(m, n, k, bias, residual):
+    """A launch whose last round of 256 x 256 tiles would fill at most half
+    of the 256 CUs (here 300 = 256 + 44 and 294 = 256 + 38 tiles, the second
+    with ragged M and N) runs those last tiles as two K halves, summed in
+    order before the epilogue: the unsplit product up to the F32 summation
+    order, and the oracle's on the columns of the split tiles."""
+    r = rng(m + n + k + 11)
+    x = r.standard_normal((m, k)).astype(np.float32)
+    w = bf16_bits(r.standard_normal((n, k)).astype(np.float32) / np.sqrt(k))
+    b = bf16_bits(r.standard_normal(n).astype(np.float32) * 0.1) if bias else None
+    res = r.standard_normal((m, n)).astype(np.float32) if residual else None
+    hi, lo = split_gpu(x)
+    args = (p(hi), p(lo), p(dev(w)), p(dev(b) if bias else None),
+            p(dev(res) if residual else None), m, n, k)
+    unsplit, parted = empty((m, n)), empty((m, n))
+    N.call("evo_hip_linear", *args, p(unsplit), stream())
+    tiles = -(-m // 256) * -(-n // 256)
+    tail = tiles % 256
+    assert tiles > 256 and 0 < tail <= 128
+    workspace = empty((2 * tail * 256 * 256,))
+    N.call("evo_hip_linear_split", *args, p(parted), p(workspace), workspace.numel() * 4, stream())
+    got, plain = host(parted), host(unsplit)
+    assert rel_err(got, plain) < 1e-5
+    assert not np.array_equal(got, plain)  # the split path ran
+    cols = slice(n - 512, n)  # inside the split tiles (the last in tile order)
+    expected = O.linear_bf16w(x, w[cols], b[cols] if bias else None)
+    if residual:
+        expected = expected + res[:, cols]
+    assert rel_err(got[:, cols], expected) < 2e-5
+    # One byte short of the partials: the unsplit launch, bit for bit.
+    N.call("evo_hip_linear_split", *args, p(parted), p(workspace), workspace.numel() * 4 - 1,
+           stream())
+    assert np.array_equal(host(parted), plain)
+
+
 def split_gpu(x):
     hi, lo = empty(x.shape, np.uint16), empty(x.shape, np.uint16)
     N.call("evo_hip_split_f32", p(dev(x)), x.size, p(hi), p(lo), stream())
