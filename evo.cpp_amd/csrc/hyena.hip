@@ -1756,6 +1756,30 @@ template <int kD> __device__ inline float hm_shift(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
       0, __builtin_bit_cast(int, v), 0x110 + kD, 0xf, 0xf, true));
 }
+// One level of the block scan over eight chains: v += q * v[lane - kD]
+// (nothing for the first kD lanes of each row of 16), as v_fmac_f32 with a
+// DPP row shift on the multiplicand: one instruction per chain instead of a
+// DPP move and an FMA. Same single rounding as fmaf(q, shifted v, v). The
+// s_nop gives the two wait states a DPP read needs after the VALU write of
+// its source, which the compiler cannot see inside the asm; the sources must
+// be VALU results (not MFMA results, which need more).
+template <int kD> __device__ inline void hm_scan_level(float (&v)[2][4], const float (&qa)[4],
+                                                       const float (&qb)[4]) {
+  asm(
+      "s_nop 1\n\t"
+      "v_fmac_f32_dpp %0, %0, %8 row_shr:%c16 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "v_fmac_f32_dpp %1, %1, %9 row_shr:%c16 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "v_fmac_f32_dpp %2, %2, %10 row_shr:%c16 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "v_fmac_f32_dpp %3, %3, %11 row_shr:%c16 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "v_fmac_f32_dpp %4, %4, %12 row_shr:%c16 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "v_fmac_f32_dpp %5, %5, %13 row_shr:%c16 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "v_fmac_f32_dpp %6, %6, %14 row_shr:%c16 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "v_fmac_f32_dpp %7, %7, %15 row_shr:%c16 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+      : "+v"(v[0][0]), "+v"(v[0][1]), "+v"(v[0][2]), "+v"(v[0][3]), "+v"(v[1][0]),
+        "+v"(v[1][1]), "+v"(v[1][2]), "+v"(v[1][3])
+      : "v"(qa[0]), "v"(qa[1]), "v"(qa[2]), "v"(qa[3]), "v"(qb[0]), "v"(qb[1]), "v"(qb[2]),
+        "v"(qb[3]), "n"(kD));
+}
 __device__ inline f32x4 hm_mfma3(const hm_s4 &ah, const hm_s4 &al, const hm_s4 &bh,
                                  const hm_s4 &bl, f32x4 acc) {
   acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bh, acc, 0, 0, 0);
@@ -1988,55 +2012,82 @@ __global__ __launch_bounds__(kHmThreads<O>, 1) void hcl_mfma_kernel(
 
   // ---- Product lane: channels 2 wave + k (k = 0, 1); column (block) b,
   // fragment group g. The constant fragments are computed once per channel
-  // in double precision (powers by repeated squaring), and the filter
-  // h[n] = sum_m R_m p_m^n by four lanes per n (modes 4g .. 4g+3 each)
-  // reduced across the lane groups.
+  // in double precision, and the filter h[n] = sum_m R_m p_m^n by four lanes
+  // per n (modes 4g .. 4g+3 each) reduced across the lane groups. The loads
+  // are issued here; the arithmetic (`constants`) runs after the first
+  // barrier, beside the production of step 0.
   const int b = lane & 15, g = lane >> 4;
   const int cwave = !kRoles ? wave : producer ? 0 : wave - Roles::kProducerWaves;
   hm_s4 w_hi[2], w_lo[2], h_hi[2], h_lo[2], v_hi[2], v_lo[2];
   float q1[2][4], q2[2][4], q4[2][4], q8[2][4], qb[2][4], carry[2][4];
+  // p of mode b, p and R of modes 4g + v, and D of each channel.
+  float p_b[2], p_g[2][4], r_g[2][4], d_c[2];
 #pragma unroll
   for (int k = 0; k < 2 && consumer; ++k) {
     const size_t c = c0 + 2 * cwave + k;
-    // Loads first (one round trip): p of mode b, p and R of modes 4g + v.
-    const float p_b = b < S ? poles[c * S + b] : 0.0F;
-    float p_g[4], r_g[4];
+    p_b[k] = b < S ? poles[c * S + b] : 0.0F;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int m = 4 * g + v;
-      p_g[v] = m < S ? poles[c * S + m] : 0.0F;
-      r_g[v] = m < S ? residues[c * S + m] : 0.0F;
+      p_g[k][v] = m < S ? poles[c * S + m] : 0.0F;
+      r_g[k][v] = m < S ? residues[c * S + m] : 0.0F;
       carry[k][v] = (modal_state != nullptr && m < S) ? modal_state[c * S + m] : 0.0F;
     }
-    const double d = direct[c];
-    // h[b] over this lane's four modes, then summed over the four groups.
-    double h_part = 0.0;
-#pragma unroll
-    for (int v = 0; v < 4; ++v)
-      h_part += static_cast<double>(r_g[v]) * hm_pow(p_g[v], b);
-    float h_n = static_cast<float>(h_part);
-    h_n += __shfl_xor(h_n, 16);
-    h_n += __shfl_xor(h_n, 32);
-    float wv[4], hv[4], vv[4];
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int j = 4 * g + v;  // A-operand K index; the A row is b
-      wv[v] = static_cast<float>(hm_pow(p_b, 15 - j));
-      const float h = __shfl(h_n, (b - j) & 15);
-      hv[v] = j <= b ? (j == b ? static_cast<float>(static_cast<double>(h) + d) : h) : 0.0F;
-      vv[v] = static_cast<float>(static_cast<double>(r_g[v]) * hm_pow(p_g[v], b + 1));
-      const double q = hm_pow(p_g[v], 16);  // block multiplier of mode 4g + v
-      const double q2d = q * q, q4d = q2d * q2d;
-      q1[k][v] = static_cast<float>(q);
-      q2[k][v] = static_cast<float>(q2d);
-      q4[k][v] = static_cast<float>(q4d);
-      q8[k][v] = static_cast<float>(q4d * q4d);
-      qb[k][v] = static_cast<float>(hm_pow(q, b + 1));
-    }
-    hm_split4(wv, w_hi[k], w_lo[k]);
-    hm_split4(hv, h_hi[k], h_lo[k]);
-    hm_split4(vv, v_hi[k], v_lo[k]);
+    d_c[k] = direct[c];
   }
+  // Powers with shared factors: p_g^b serves h[b], V (R p^(b+1)) and the
+  // lane's block multiplier q^(b+1) = (p^b)^16 p^16; W's four powers of p_b
+  // are one power and three products.
+  auto constants = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      double pgb[4], term[4];
+      double h_part = 0.0;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        pgb[v] = hm_pow(p_g[k][v], b);
+        term[v] = static_cast<double>(r_g[k][v]) * pgb[v];
+        h_part += term[v];
+      }
+      float h_n = static_cast<float>(h_part);
+      h_n += __shfl_xor(h_n, 16);
+      h_n += __shfl_xor(h_n, 32);
+      const double pb = p_b[k];
+      double wd[4];
+      wd[3] = hm_pow(pb, 12 - 4 * g);  // K index j = 4g + v takes pb^(15 - j)
+      wd[2] = wd[3] * pb;
+      wd[1] = wd[2] * pb;
+      wd[0] = wd[1] * pb;
+      float wv[4], hv[4], vv[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int j = 4 * g + v;  // A-operand K index; the A row is b
+        wv[v] = static_cast<float>(wd[v]);
+        const float h = __shfl(h_n, (b - j) & 15);
+        hv[v] = j <= b ? (j == b ? static_cast<float>(static_cast<double>(h) + d_c[k]) : h)
+                       : 0.0F;
+        const double p = p_g[k][v];
+        vv[v] = static_cast<float>(term[v] * p);
+        double q = p * p;  // block multiplier p^16 of mode 4g + v
+        q *= q;
+        q *= q;
+        q *= q;
+        const double q2d = q * q, q4d = q2d * q2d;
+        q1[k][v] = static_cast<float>(q);
+        q2[k][v] = static_cast<float>(q2d);
+        q4[k][v] = static_cast<float>(q4d);
+        q8[k][v] = static_cast<float>(q4d * q4d);
+        double x = pgb[v] * pgb[v];
+        x *= x;
+        x *= x;
+        x *= x;
+        qb[k][v] = static_cast<float>(x * q);
+      }
+      hm_split4(wv, w_hi[k], w_lo[k]);
+      hm_split4(hv, h_hi[k], h_lo[k]);
+      hm_split4(vv, v_hi[k], v_lo[k]);
+    }
+  };
 
   float sp_last[2][4];
   // The products of step `step` in two parts, so the phase can run the
@@ -2083,26 +2134,34 @@ __global__ __launch_bounds__(kHmThreads<O>, 1) void hcl_mfma_kernel(
 #pragma unroll
       for (int e = 0; e < 4; ++e)
         v[k][e] = z_acc[k][e];
+    // The first level stays compiler-visible: it reads the MFMA results, whose
+    // wait states the compiler inserts.
 #pragma unroll
     for (int k = 0; k < 2; ++k)
 #pragma unroll
       for (int e = 0; e < 4; ++e)
         v[k][e] = fmaf(q1[k][e], hm_shift<1>(v[k][e]), v[k][e]);
+    if constexpr (kRoles) {
+      hm_scan_level<2>(v, q2[0], q2[1]);
+      hm_scan_level<4>(v, q4[0], q4[1]);
+      hm_scan_level<8>(v, q8[0], q8[1]);
+    } else {
 #pragma unroll
-    for (int k = 0; k < 2; ++k)
+      for (int k = 0; k < 2; ++k)
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        v[k][e] = fmaf(q2[k][e], hm_shift<2>(v[k][e]), v[k][e]);
+        for (int e = 0; e < 4; ++e)
+          v[k][e] = fmaf(q2[k][e], hm_shift<2>(v[k][e]), v[k][e]);
 #pragma unroll
-    for (int k = 0; k < 2; ++k)
+      for (int k = 0; k < 2; ++k)
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        v[k][e] = fmaf(q4[k][e], hm_shift<4>(v[k][e]), v[k][e]);
+        for (int e = 0; e < 4; ++e)
+          v[k][e] = fmaf(q4[k][e], hm_shift<4>(v[k][e]), v[k][e]);
 #pragma unroll
-    for (int k = 0; k < 2; ++k)
+      for (int k = 0; k < 2; ++k)
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        v[k][e] = fmaf(q8[k][e], hm_shift<8>(v[k][e]), v[k][e]);
+        for (int e = 0; e < 4; ++e)
+          v[k][e] = fmaf(q8[k][e], hm_shift<8>(v[k][e]), v[k][e]);
+    }
 #pragma unroll
     for (int k = 0; k < 2; ++k)
 #pragma unroll
@@ -2232,6 +2291,8 @@ __global__ __launch_bounds__(kHmThreads<O>, 1) void hcl_mfma_kernel(
       hm_wait((more ? kDmaMin : 0) + (step >= 1 ? stores : 0) + (step >= 2 ? stores : 0));
     __syncthreads();
   };
+  if (!kRoles)
+    constants();
   if (producer) {
     for (int step = 0; step < kHmStages && step < steps; ++step)
       issue(step, std::false_type{});
@@ -2242,6 +2303,8 @@ __global__ __launch_bounds__(kHmThreads<O>, 1) void hcl_mfma_kernel(
     produce(0, HmMode<kHmFirst>{});
     hm_wait(steps > 2 ? kDmaMin : 0);
   }
+  if (kRoles && consumer)
+    constants();  // beside the production of step 0
   __syncthreads();
   if constexpr (kRoles) {
     if (producer) {
