@@ -1427,21 +1427,15 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void hyena_fir_mfma_st
   const size_t cw = c0 + 16 * wave + col;
   const float *h = filter + ((c0 + 16 * wave) / group_size) * k;
   const int stores = MsOut<O>::stores(out);
-  // The taps are BF16 values, so T has no lo plane.
+  // The wave's filter (k <= 128 taps of its group) goes to LDS in one
+  // coalesced read; the Toeplitz fragments are gathered from there after the
+  // first barrier (80 taps per lane read from global memory one by one took
+  // ~12 us of L2 latency). The scratch is the third x2 / y buffer, which the
+  // production first writes in phase 1.
+  float *taps_s = &xy_s[2][0][0] + wave * 128;
+  for (int i = lane; i < k; i += 64)
+    taps_s[i] = h[i];
   u32x4 a[2][kMsK];
-#pragma unroll
-  for (int half = 0; half < 2; ++half)
-#pragma unroll
-    for (int q = 0; q < kMsK; ++q) {
-      uint16_t taps[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int i = 32 * q + 8 * g + e;
-        const int o = i - 16 * half - col - 128 + (k - 1);
-        taps[e] = f32_to_bf16((o >= 0 && o < k) ? h[causal ? k - 1 - o : o] : 0.0F);
-      }
-      a[half][q] = __builtin_bit_cast(u32x4, taps);
-    }
   float d = direct[cw];
   // Keep d in a register: a global load re-issued inside the step loop would
   // make the wait for it also wait for every DMA in flight.
@@ -1591,13 +1585,27 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void hyena_fir_mfma_st
     }
   };
 
-  // Prologue: stage 0 (younger: the DMA of stage 1), production of step 0,
-  // then stage 1 complete.
+  // Prologue: stage 0 (younger: the DMA of stage 1) and the filter in LDS,
+  // the fragments, production of step 0, then stage 1 complete.
   if (steps > 1)
     wait_dma<kDmaMin>();
   else
     wait_dma<0>();
   __syncthreads();
+  // The taps are BF16 values, so T has no lo plane.
+#pragma unroll
+  for (int half = 0; half < 2; ++half)
+#pragma unroll
+    for (int q = 0; q < kMsK; ++q) {
+      uint16_t taps[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int i = 32 * q + 8 * g + e;
+        const int o = i - 16 * half - col - 128 + (k - 1);
+        taps[e] = f32_to_bf16((o >= 0 && o < k) ? taps_s[causal ? k - 1 - o : o] : 0.0F);
+      }
+      a[half][q] = __builtin_bit_cast(u32x4, taps);
+    }
   produce(0);
   wait_dma<0>();
   __syncthreads();
