@@ -1419,27 +1419,46 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void hyena_fir_mfma_st
       }
     }
   };
-  for (int step = 0; step < kStages && step < steps; ++step)
-    issue(step);
 
   // ---- MFMA lane: channel slice `wave`, fragment group g.
   const int col = lane & 15, g = lane >> 4;
   const size_t cw = c0 + 16 * wave + col;
   const float *h = filter + ((c0 + 16 * wave) / group_size) * k;
   const int stores = MsOut<O>::stores(out);
-  // The wave's filter (k <= 128 taps of its group) goes to LDS in one
-  // coalesced read; the Toeplitz fragments are gathered from there after the
-  // first barrier (80 taps per lane read from global memory one by one took
-  // ~12 us of L2 latency). The scratch is the third x2 / y buffer, which the
-  // production first writes in phase 1.
-  float *taps_s = &xy_s[2][0][0] + wave * 128;
-  for (int i = lane; i < k; i += 64)
-    taps_s[i] = h[i];
+  // The wave's filter (k <= 128 taps of its group) goes to LDS between 160
+  // zeros on either side, so that the Toeplitz fragments gather from there
+  // after the first barrier with unconditional reads (80 taps per lane read
+  // from global memory one by one took ~12 us of L2 latency, and conditional
+  // LDS reads ~5 us). With 16-byte aligned taps and direct terms both arrive
+  // by DMA ahead of the projection stages, so that the first barrier's wait
+  // covers them; otherwise by plain loads before the stages are issued (a
+  // wait for a load issued behind the DMA would wait for the DMA too). The
+  // scratch is the third x2 / y buffer, which the production first writes in
+  // phase 1: 448 floats per wave, then the block's 64 direct terms.
+  constexpr int kTapPad = 160;
+  float *taps_s = &xy_s[2][0][0] + wave * (2 * kTapPad + 128);
+  float *direct_s = &xy_s[2][0][0] + 4 * (2 * kTapPad + 128);
+  const bool dma_consts = k % 4 == 0 && reinterpret_cast<uintptr_t>(filter) % 16 == 0 &&
+                          reinterpret_cast<uintptr_t>(direct) % 16 == 0;
+  for (int i = lane; i < kTapPad; i += 64)
+    taps_s[i] = 0.0F;
+  for (int i = kTapPad + k + lane; i < 2 * kTapPad + 128; i += 64)
+    taps_s[i] = 0.0F;
+  float d = 0.0F;
+  if (dma_consts) {
+    if (lane < k / 4)
+      dma16(h + 4 * lane, taps_s + kTapPad);
+    if (wave == 0 && lane < kMsChannels / 4)
+      dma16(direct + c0 + 4 * lane, direct_s);
+  } else {
+    for (int i = lane; i < k; i += 64)
+      taps_s[kTapPad + i] = h[i];
+    d = direct[cw];
+    asm volatile("" : "+v"(d));
+  }
+  for (int step = 0; step < kStages && step < steps; ++step)
+    issue(step);
   u32x4 a[2][kMsK];
-  float d = direct[cw];
-  // Keep d in a register: a global load re-issued inside the step loop would
-  // make the wait for it also wait for every DMA in flight.
-  asm volatile("" : "+v"(d));
   u32x4 ring_hi[kMsK], ring_lo[kMsK];  // BF16 x 8 fragments as raw words
 #pragma unroll
   for (int q = 0; q < kMsK; ++q) {
@@ -1592,6 +1611,11 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void hyena_fir_mfma_st
   else
     wait_dma<0>();
   __syncthreads();
+  if (dma_consts)
+    d = direct_s[16 * wave + col];
+  // Keep d in a register: a load re-issued inside the step loop would make
+  // the wait for it also wait for every DMA in flight.
+  asm volatile("" : "+v"(d));
   // The taps are BF16 values, so T has no lo plane.
 #pragma unroll
   for (int half = 0; half < 2; ++half)
@@ -1601,8 +1625,8 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void hyena_fir_mfma_st
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int i = 32 * q + 8 * g + e;
-        const int o = i - 16 * half - col - 128 + (k - 1);
-        taps[e] = f32_to_bf16((o >= 0 && o < k) ? taps_s[causal ? k - 1 - o : o] : 0.0F);
+        const int o = i - 16 * half - col - 128 + (k - 1);  // -160 <= o < k + 31
+        taps[e] = f32_to_bf16(taps_s[kTapPad + (causal ? k - 1 - o : o)]);
       }
       a[half][q] = __builtin_bit_cast(u32x4, taps);
     }
