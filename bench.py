@@ -60,11 +60,15 @@ def artifact_path(directory):
 
 
 def event_time(fn, repeats):
-    """Average launch duration of fn() on torch's current stream (ms)."""
+    """Average launch duration of fn() on torch's current stream (ms). A
+    bounded spin kernel queued first holds the stream while the host
+    enqueues the launches, so the timed launches run back to back and the
+    host's per-call cost (ctypes, argument checks) is not counted."""
     import torch
     fn()
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    torch.cuda._sleep(50_000_000)  # ~20 ms of GPU clock cycles
     start.record()
     for _ in range(repeats):
         fn()
