@@ -174,6 +174,15 @@ def kernel_rooflines(split):
         flops = 2.0 * m * n * k
         out[name] = dict(kernel=f"fp8_mfma_kernel<{32 if mode == 0 else 128}>", ms=ms,
                          flops=flops, tflops=flops / ms / 1e9)
+    # The same projection at the 8192-token prefill's M (the model's shape).
+    m = 8192
+    a8 = torch.randint(0, 0x7e, (m, k), dtype=torch.uint8, device="cuda", generator=g)
+    y8 = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+    ms = event_time(lambda: native.call("evo_hip_fp8_linear_bf16", a8.data_ptr(), w8.data_ptr(),
+                                        y8.data_ptr(), m, n, k, 1e-3, 1, stream), 10)
+    flops = 2.0 * m * n * k
+    out["fp8_k128_m8192"] = dict(kernel="fp8_mfma_kernel<128>", ms=ms, flops=flops,
+                                 tflops=flops / ms / 1e9)
     return out
 
 
@@ -477,7 +486,7 @@ def main():
         worst = min(hyena, key=lambda h: h["frac"])
         result["hyena_roofline"] = dict(worst, bound="hbm", per_launch=per_launch)
         result["hyena_kernels"] = hyena
-        for name in ("fp8_k32", "fp8_k128"):
+        for name in ("fp8_k32", "fp8_k128", "fp8_k128_m8192"):
             f = kernels[name]
             result[name + "_roofline"] = {"bound": "mfma", "kernel": f["kernel"],
                                           "achieved": round(f["tflops"], 1),

@@ -544,7 +544,9 @@ __global__ __launch_bounds__(512) void gemm_kernel(
 }
 
 // Tail tiles of a gemm_kernel launch: the two K halves summed (first half
-// first), then the tile's epilogue, in gemm_kernel's thread layout.
+// first), then the tile's epilogue, in gemm_kernel's thread layout; block
+// (t, i) takes MFMA tile row i of every wave of tail tile t, so that the
+// reduction runs on kGemmMI blocks per tile.
 __global__ __launch_bounds__(512) void gemm_tail_kernel(const float *__restrict__ tail_part,
                                                         int full_tiles, int M, int N,
                                                         float *__restrict__ C,
@@ -560,21 +562,19 @@ __global__ __launch_bounds__(512) void gemm_tail_kernel(const float *__restrict_
                                  &tm, &tn);
   const float *first = tail_part + static_cast<size_t>(blockIdx.x) * 2 * (kBM * kBN);
   const float *second = first + kBM * kBN;
+  const int i = blockIdx.y;
+  f32x4 acc[kGemmNJ];
 #pragma unroll
-  for (int i = 0; i < kGemmMI; ++i) {
-    f32x4 acc[kGemmNJ];
+  for (int j = 0; j < kGemmNJ; ++j) {
+    const int at = ((i * kGemmNJ + j) * 512 + tid) * 4;
+    const f32x4 a = *reinterpret_cast<const f32x4 *>(first + at);
+    const f32x4 b = *reinterpret_cast<const f32x4 *>(second + at);
 #pragma unroll
-    for (int j = 0; j < kGemmNJ; ++j) {
-      const int at = ((i * kGemmNJ + j) * 512 + tid) * 4;
-      const f32x4 a = *reinterpret_cast<const f32x4 *>(first + at);
-      const f32x4 b = *reinterpret_cast<const f32x4 *>(second + at);
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        acc[j][e] = a[e] + b[e];
-    }
-    gemm_epilogue_row(acc, i, tm * kBM, tn * kBN, wave / kGemmWavesN, wave % kGemmWavesN, lane,
-                      M, N, C, c_hi, c_lo, ldc, epi);
+    for (int e = 0; e < 4; ++e)
+      acc[j][e] = a[e] + b[e];
   }
+  gemm_epilogue_row(acc, i, tm * kBM, tn * kBN, wave / kGemmWavesN, wave % kGemmWavesN, lane, M,
+                    N, C, c_hi, c_lo, ldc, epi);
 }
 
 // ---- Few-row product (decode, M <= 4): each 256-thread block owns 8
@@ -749,9 +749,11 @@ __global__ void split_kernel(const float *__restrict__ x, size_t n,
 
 // Sum of the split-K partials in split order, then the epilogue:
 // C[m, n] = sum_s part[s][m, n] (+ bias[n]) (+ residual[m, n]). Four columns
-// per thread (N % 4 == 0).
+// per thread (N % 4 == 0); `vec`: C, the residual (16 bytes) and the bias
+// (8 bytes) are aligned for vector accesses of the four (ldc % 4 == 0).
 __global__ void split_k_reduce_kernel(const float *__restrict__ part, int splits, int M, int N,
-                                      float *__restrict__ C, int ldc, const Epilogue epi) {
+                                      float *__restrict__ C, int ldc, const Epilogue epi,
+                                      bool vec) {
   const size_t quads = static_cast<size_t>(M) * (N / 4);
   const size_t plane = static_cast<size_t>(M) * N;
   for (size_t q = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; q < quads;
@@ -767,19 +769,42 @@ __global__ void split_k_reduce_kernel(const float *__restrict__ part, int splits
     }
     const size_t index = m * ldc + n;
     const bool res_mode = epi.mode == kGemmResidual || epi.mode == kGemmBiasResidual;
-    // The four residual loads ahead of the stores (C may alias the residual).
-    float residual[4];
+    const bool bias_mode = epi.mode == kGemmBias || epi.mode == kGemmBiasResidual;
+    // The residual loads ahead of the stores (C may alias the residual).
+    float residual[4], bias[4];
+    if (vec) {
+      const f32x4 r = res_mode ? *reinterpret_cast<const f32x4 *>(epi.residual + index)
+                               : f32x4{0.0F, 0.0F, 0.0F, 0.0F};
+      const uint2 b = bias_mode ? *reinterpret_cast<const uint2 *>(epi.bias + n) : uint2{0, 0};
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      residual[e] = res_mode ? epi.residual[index + e] : 0.0F;
+      for (int e = 0; e < 4; ++e)
+        residual[e] = r[e];
+      bias[0] = __builtin_bit_cast(float, b.x << 16);
+      bias[1] = __builtin_bit_cast(float, b.x & 0xffff0000U);
+      bias[2] = __builtin_bit_cast(float, b.y << 16);
+      bias[3] = __builtin_bit_cast(float, b.y & 0xffff0000U);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        residual[e] = res_mode ? epi.residual[index + e] : 0.0F;
+        bias[e] = bias_mode ? bf16_to_f32(epi.bias[n + e]) : 0.0F;
+      }
+    }
+    f32x4 value;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      float value = acc[e];
-      if (epi.mode == kGemmBias || epi.mode == kGemmBiasResidual)
-        value = value + bf16_to_f32(epi.bias[n + e]);
+      value[e] = acc[e];
+      if (bias_mode)
+        value[e] = value[e] + bias[e];
       if (res_mode)
-        value = value + residual[e];
-      C[index + e] = value;
+        value[e] = value[e] + residual[e];
+    }
+    if (vec) {
+      *reinterpret_cast<f32x4 *>(C + index) = value;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        C[index + e] = value[e];
     }
   }
 }
@@ -887,8 +912,11 @@ Status gemm_impl(const Activation &a, const RowNorm *norm, bool split, const uin
       EVO_TRY(launch_status("gemm_kernel (split K)"));
       const size_t quads = plane / 4;
       const unsigned blocks = static_cast<unsigned>(std::min<size_t>((quads + 255) / 256, 8192));
+      const bool vec = ldc % 4 == 0 && reinterpret_cast<uintptr_t>(out.f32) % 16 == 0 &&
+                       reinterpret_cast<uintptr_t>(residual) % 16 == 0 &&
+                       reinterpret_cast<uintptr_t>(bias) % 8 == 0;
       hipLaunchKernelGGL(split_k_reduce_kernel, dim3(blocks), dim3(256), 0, stream,
-                         split_workspace, splits, m, n, out.f32, ldc, epi);
+                         split_workspace, splits, m, n, out.f32, ldc, epi, vec);
       return launch_status("split_k_reduce_kernel");
     }
     // Tail split: when the last round would hold at most half the CUs, its
@@ -913,7 +941,8 @@ Status gemm_impl(const Activation &a, const RowNorm *norm, bool split, const uin
     if (tail == 0)
       return launch_status("gemm_kernel");
     EVO_TRY(launch_status("gemm_kernel (tail split)"));
-    hipLaunchKernelGGL(gemm_tail_kernel, dim3(static_cast<unsigned>(tail)), dim3(512), 0, stream,
+    hipLaunchKernelGGL(gemm_tail_kernel, dim3(static_cast<unsigned>(tail), kGemmMI), dim3(512), 0,
+                       stream,
                        split_workspace, full, m, n, out.f32, out.hi, out.lo, ldc, epi);
     return launch_status("gemm_tail_kernel");
   }
