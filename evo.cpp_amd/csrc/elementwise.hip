@@ -97,11 +97,24 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2v __attribute__((ext_vector_type(2)));
 
-template <int kVec>
+// Row source of the fused form: x = sum_s part[s] (s in order) (+ bf16
+// bias) (+ residual), the split-K reduction's values, also written to
+// `sum`; part == nullptr: x is read from memory.
+struct NormPartials {
+  const float *part;
+  int splits;
+  size_t plane;
+  const uint16_t *bias;
+  const float *residual;
+  float *sum;
+};
+
+template <int kVec, bool kPartials = false>
 __global__ __launch_bounds__(256) void rms_norm_reg_kernel(
     const float *__restrict__ x, size_t width, const float *__restrict__ scale,
     float eps, float *__restrict__ out, uint16_t *__restrict__ out_hi,
-    uint16_t *__restrict__ out_lo, uint8_t *__restrict__ codes, float code_scale) {
+    uint16_t *__restrict__ out_lo, uint8_t *__restrict__ codes, float code_scale,
+    const NormPartials parts) {
   __shared__ float partial[4];
   const size_t row = blockIdx.x;
   const float *src = x + row * width;
@@ -110,7 +123,33 @@ __global__ __launch_bounds__(256) void rms_norm_reg_kernel(
 #pragma unroll
   for (int j = 0; j < kVec; ++j) {
     const size_t c = threadIdx.x * 4 + j * 1024;
-    v[j] = c < width ? *reinterpret_cast<const float4 *>(src + c) : make_float4(0, 0, 0, 0);
+    if constexpr (kPartials) {
+      if (c < width) {
+        const size_t index = row * width + c;
+        float4 acc = *reinterpret_cast<const float4 *>(parts.part + index);
+        for (int sp = 1; sp < parts.splits; ++sp) {
+          const float4 p = *reinterpret_cast<const float4 *>(parts.part + sp * parts.plane + index);
+          acc = make_float4(acc.x + p.x, acc.y + p.y, acc.z + p.z, acc.w + p.w);
+        }
+        if (parts.bias != nullptr) {
+          const uint2 b = *reinterpret_cast<const uint2 *>(parts.bias + c);
+          acc = make_float4(acc.x + __builtin_bit_cast(float, b.x << 16),
+                            acc.y + __builtin_bit_cast(float, b.x & 0xffff0000U),
+                            acc.z + __builtin_bit_cast(float, b.y << 16),
+                            acc.w + __builtin_bit_cast(float, b.y & 0xffff0000U));
+        }
+        if (parts.residual != nullptr) {
+          const float4 r = *reinterpret_cast<const float4 *>(parts.residual + index);
+          acc = make_float4(acc.x + r.x, acc.y + r.y, acc.z + r.z, acc.w + r.w);
+        }
+        *reinterpret_cast<float4 *>(parts.sum + index) = acc;
+        v[j] = acc;
+      } else {
+        v[j] = make_float4(0, 0, 0, 0);
+      }
+    } else {
+      v[j] = c < width ? *reinterpret_cast<const float4 *>(src + c) : make_float4(0, 0, 0, 0);
+    }
     if (c < width)
       sum = norm_square_sum(v[j], sum);
   }
@@ -189,19 +228,54 @@ Status rms_norm(const float *x, size_t rows, size_t width, const float *scale,
       (codes != nullptr && !(code_scale > 0.0F && __builtin_isfinite(code_scale))))
     return {ErrorCode::kInvalidArgument, "rms_norm: invalid arguments"};
   const dim3 grid(static_cast<unsigned>(rows)), block(256);
+  const NormPartials none{nullptr, 0, 0, nullptr, nullptr, nullptr};
   if (width % 4 == 0 && width <= 2048)
     hipLaunchKernelGGL(rms_norm_reg_kernel<2>, grid, block, 0, stream, x, width, scale, eps,
-                       out, out_hi, out_lo, codes, code_scale);
+                       out, out_hi, out_lo, codes, code_scale, none);
   else if (width % 4 == 0 && width <= 4096)
     hipLaunchKernelGGL(rms_norm_reg_kernel<4>, grid, block, 0, stream, x, width, scale, eps,
-                       out, out_hi, out_lo, codes, code_scale);
+                       out, out_hi, out_lo, codes, code_scale, none);
   else if (width % 4 == 0 && width <= 8192)
     hipLaunchKernelGGL(rms_norm_reg_kernel<8>, grid, block, 0, stream, x, width, scale, eps,
-                       out, out_hi, out_lo, codes, code_scale);
+                       out, out_hi, out_lo, codes, code_scale, none);
   else
     hipLaunchKernelGGL(rms_norm_kernel, grid, block, 0, stream, x, width, scale, eps, out,
                        out_hi, out_lo, codes, code_scale);
   return launch_status("rms_norm_kernel");
+}
+
+Status rms_norm_partials(const SplitPartials &src, float *sum, size_t rows, size_t width,
+                         const float *scale, float eps, uint16_t *out_hi, uint16_t *out_lo,
+                         hipStream_t stream, uint8_t *codes, float code_scale) {
+  if (src.splits == 0)
+    return rms_norm(sum, rows, width, scale, eps, nullptr, out_hi, out_lo, stream, codes,
+                    code_scale);
+  const bool aligned = width % 4 == 0 && reinterpret_cast<uintptr_t>(src.part) % 16 == 0 &&
+                       reinterpret_cast<uintptr_t>(sum) % 16 == 0 &&
+                       reinterpret_cast<uintptr_t>(src.residual) % 16 == 0 &&
+                       reinterpret_cast<uintptr_t>(src.bias) % 8 == 0;
+  if (!aligned || width > 8192 || src.plane != rows * width) {
+    // Unfused: the reduction, then the norm of what it wrote.
+    EVO_TRY(split_k_finish(src, sum, rows, width, stream));
+    return rms_norm(sum, rows, width, scale, eps, nullptr, out_hi, out_lo, stream, codes,
+                    code_scale);
+  }
+  if (scale == nullptr || sum == nullptr || (out_hi == nullptr && codes == nullptr) ||
+      rows == 0 || rows > (1U << 31) ||
+      (codes != nullptr && !(code_scale > 0.0F && __builtin_isfinite(code_scale))))
+    return {ErrorCode::kInvalidArgument, "rms_norm_partials: invalid arguments"};
+  const dim3 grid(static_cast<unsigned>(rows)), block(256);
+  const NormPartials parts{src.part, src.splits, src.plane, src.bias, src.residual, sum};
+  if (width <= 2048)
+    hipLaunchKernelGGL((rms_norm_reg_kernel<2, true>), grid, block, 0, stream, nullptr, width,
+                       scale, eps, nullptr, out_hi, out_lo, codes, code_scale, parts);
+  else if (width <= 4096)
+    hipLaunchKernelGGL((rms_norm_reg_kernel<4, true>), grid, block, 0, stream, nullptr, width,
+                       scale, eps, nullptr, out_hi, out_lo, codes, code_scale, parts);
+  else
+    hipLaunchKernelGGL((rms_norm_reg_kernel<8, true>), grid, block, 0, stream, nullptr, width,
+                       scale, eps, nullptr, out_hi, out_lo, codes, code_scale, parts);
+  return launch_status("rms_norm_reg_kernel (split-K partials)");
 }
 
 Status update_history(const float *x, size_t rows, size_t channels,

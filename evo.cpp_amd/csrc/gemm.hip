@@ -827,7 +827,9 @@ Status gemm_impl(const Activation &a, const RowNorm *norm, bool split, const uin
                  const GemmOutput &out, size_t M, size_t N, size_t K, GemmEpilogue mode,
                  const uint16_t *bias, const float *residual, bool gelu,
                  size_t gated_width, hipStream_t stream, float *split_workspace,
-                 size_t split_workspace_bytes) {
+                 size_t split_workspace_bytes, SplitPartials *deferred) {
+  if (deferred != nullptr)
+    *deferred = SplitPartials{};
   if (norm != nullptr) {
     if (norm->x == nullptr || norm->scale == nullptr || M > static_cast<size_t>(kGemvMaxM) ||
         norm->ld < K || norm->ld % 4 != 0 ||
@@ -910,6 +912,13 @@ Status gemm_impl(const Activation &a, const RowNorm *norm, bool split, const uin
                            lda, W, k, m, n, ks, split_workspace, plane, nullptr, nullptr, n,
                            store, all, nullptr);
       EVO_TRY(launch_status("gemm_kernel (split K)"));
+      if (deferred != nullptr && ldc == n) {
+        const bool bias_mode = mode == kGemmBias || mode == kGemmBiasResidual;
+        const bool res_mode = mode == kGemmResidual || mode == kGemmBiasResidual;
+        *deferred = SplitPartials{split_workspace, splits, plane, bias_mode ? bias : nullptr,
+                                  res_mode ? residual : nullptr};
+        return Status::Ok();
+      }
       const size_t quads = plane / 4;
       const unsigned blocks = static_cast<unsigned>(std::min<size_t>((quads + 255) / 256, 8192));
       const bool vec = ldc % 4 == 0 && reinterpret_cast<uintptr_t>(out.f32) % 16 == 0 &&
@@ -961,9 +970,30 @@ Status gemm_bf16w(const Activation &a, const uint16_t *W, const GemmOutput &out,
                   size_t M, size_t N, size_t K, GemmEpilogue mode,
                   const uint16_t *bias, const float *residual, bool gelu,
                   size_t gated_width, hipStream_t stream, float *split_workspace,
-                  size_t split_workspace_bytes) {
+                  size_t split_workspace_bytes, SplitPartials *deferred) {
   return gemm_impl(a, nullptr, a.lo != nullptr, W, out, M, N, K, mode, bias, residual, gelu,
-                   gated_width, stream, split_workspace, split_workspace_bytes);
+                   gated_width, stream, split_workspace, split_workspace_bytes, deferred);
+}
+
+Status split_k_finish(const SplitPartials &src, float *C, size_t rows, size_t width,
+                      hipStream_t stream) {
+  if (src.splits == 0)
+    return Status::Ok();
+  if (src.part == nullptr || C == nullptr || width % 4 != 0 || src.plane != rows * width)
+    return {ErrorCode::kInvalidArgument, "split_k_finish: invalid partials"};
+  const GemmEpilogue mode = src.bias != nullptr
+                                ? (src.residual != nullptr ? kGemmBiasResidual : kGemmBias)
+                                : (src.residual != nullptr ? kGemmResidual : kGemmStore);
+  const Epilogue epi{static_cast<int>(mode), src.bias, src.residual, 0, 0};
+  const size_t quads = src.plane / 4;
+  const unsigned blocks = static_cast<unsigned>(std::min<size_t>((quads + 255) / 256, 8192));
+  const bool vec = reinterpret_cast<uintptr_t>(C) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(src.residual) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(src.bias) % 8 == 0;
+  hipLaunchKernelGGL(split_k_reduce_kernel, dim3(blocks), dim3(256), 0, stream, src.part,
+                     src.splits, static_cast<int>(rows), static_cast<int>(width), C,
+                     static_cast<int>(width), epi, vec);
+  return launch_status("split_k_reduce_kernel");
 }
 
 Status gemm_bf16w_normed(const RowNorm &norm, bool split, const uint16_t *W,
@@ -971,7 +1001,7 @@ Status gemm_bf16w_normed(const RowNorm &norm, bool split, const uint16_t *W,
                          GemmEpilogue mode, const uint16_t *bias, const float *residual,
                          bool gelu, size_t gated_width, hipStream_t stream) {
   return gemm_impl(Activation{nullptr, nullptr, K}, &norm, split, W, out, M, N, K, mode, bias,
-                   residual, gelu, gated_width, stream, nullptr, 0);
+                   residual, gelu, gated_width, stream, nullptr, 0, nullptr);
 }
 
 }  // namespace evo::hip

@@ -434,10 +434,15 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
   // Few-row chunks (decode) fold each RMSNorm into the product that reads
   // it (same values, one launch and round trip less per norm).
   const bool fold = rows <= kFoldRows;
+  pending_ = SplitPartials{};
   for (size_t i = 0; i < c.layers; ++i) {
     const Layer &L = model_->layer[i];
     Cache &k = cache_[i];
     const RowNorm pre{hidden, L.pre_norm.as<float>(), c.eps, w};
+    if (fold && pending_.splits != 0) {
+      EVO_TRY(split_k_finish(pending_, hidden, rows, w, stream_));
+      pending_ = SplitPartials{};
+    }
     if (L.fp8) {
       const Fp8Mode mode = (w % 128 != 0) ? kFp8Exact : options_.fp8_mode;
       // The product is BF16 by definition: store it as BF16 and halve the
@@ -449,8 +454,12 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
       } else {
         // The norm writes only the E4M3 codes of bf16(x) * input_scale:
         // the projection is the sole consumer of this normed activation.
-        EVO_TRY(rms_norm(hidden, rows, w, L.pre_norm.as<float>(), c.eps, nullptr, nullptr,
-                         nullptr, stream_, codes_.as<uint8_t>(), L.fp8_input_scale));
+        // (With pending split-K partials of the previous l3 product, the norm
+        // sums them into hidden as it reads them.)
+        EVO_TRY(rms_norm_partials(pending_, hidden, rows, w, L.pre_norm.as<float>(), c.eps,
+                                  nullptr, nullptr, stream_, codes_.as<uint8_t>(),
+                                  L.fp8_input_scale));
+        pending_ = SplitPartials{};
         EVO_TRY(fp8_linear(codes_.as<uint8_t>(), L.projection.as<uint8_t>(),
                            projected_.as<uint16_t>(), rows, 3 * w, w, L.fp8_output_scale,
                            mode, stream_));
@@ -460,8 +469,9 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
                                 GemmOutput{projected, nullptr, nullptr, 3 * w}, rows, 3 * w, w,
                                 kGemmStore, nullptr, nullptr, false, 0, stream_));
     } else {
-      EVO_TRY(rms_norm(hidden, rows, w, L.pre_norm.as<float>(), c.eps, nullptr, normed_hi,
-                       split ? normed_lo : nullptr, stream_));
+      EVO_TRY(rms_norm_partials(pending_, hidden, rows, w, L.pre_norm.as<float>(), c.eps,
+                                normed_hi, split ? normed_lo : nullptr, stream_));
+      pending_ = SplitPartials{};
       EVO_TRY(gemm_bf16w(normed, L.projection.as<uint16_t>(),
                          GemmOutput{projected, nullptr, nullptr, 3 * w}, rows, 3 * w, w,
                          kGemmStore, nullptr, nullptr, false, 0, stream_));
@@ -507,25 +517,37 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
                                                 mixed_out, stream_)));
     }
     // residual = (mixed . Wout^T + bias) + hidden   (`src/cpu/model.cpp:641-645`)
+    // Short chunks split K here; the post-mixer norm then sums the partials
+    // (with bias and hidden) into residual as it reads them.
+    SplitPartials out_partials;
     EVO_TRY(gemm_bf16w(mixed, L.out_weight.as<uint16_t>(),
                        GemmOutput{residual, nullptr, nullptr, w}, rows, w, w,
                        kGemmBiasResidual, L.out_bias.as<uint16_t>(), hidden, false, 0,
-                       stream_, workspace_.as<float>(), workspace_.bytes()));
+                       stream_, workspace_.as<float>(), workspace_.bytes(),
+                       fold ? nullptr : &out_partials));
     // gated = act(l1 x) * (l2 x), act = erf-GELU in block 0 only (`:650-667`).
     // This norm stays a kernel of its own for few rows too: folded into the
     // l1/l2 product, each of its N/8 blocks (2816 at 7B) normalises the row
     // again (40 us against 6 + 32 at 7B).
-    EVO_TRY(rms_norm(residual, rows, w, L.post_norm.as<float>(), c.eps, nullptr, normed_hi,
-                     split ? normed_lo : nullptr, stream_));
+    if (fold)
+      EVO_TRY(rms_norm(residual, rows, w, L.post_norm.as<float>(), c.eps, nullptr, normed_hi,
+                       split ? normed_lo : nullptr, stream_));
+    else
+      EVO_TRY(rms_norm_partials(out_partials, residual, rows, w, L.post_norm.as<float>(),
+                                c.eps, normed_hi, split ? normed_lo : nullptr, stream_));
     EVO_TRY(gemm_bf16w(normed, L.mlp_in.as<uint16_t>(),
                        GemmOutput{nullptr, gated_hi, split ? gated_lo : nullptr, c.inner},
                        rows, 2 * c.inner_padded, w, kGemmGated, nullptr, nullptr, i == 0,
                        c.inner, stream_, workspace_.as<float>(), workspace_.bytes()));
     // hidden = gated . l3^T + residual
+    // Its split-K partials (short chunks) are summed by the next norm of
+    // hidden, unless this layer's output is captured.
+    const bool captured = capture != nullptr && capture_layer == i;
     EVO_TRY(gemm_bf16w(gated, L.mlp_out.as<uint16_t>(), GemmOutput{hidden, nullptr, nullptr, w},
                        rows, w, c.inner, kGemmResidual, nullptr, residual, false, 0, stream_,
-                       workspace_.as<float>(), workspace_.bytes()));
-    if (capture != nullptr && capture_layer == i)
+                       workspace_.as<float>(), workspace_.bytes(),
+                       fold || captured ? nullptr : &pending_));
+    if (captured)
       EVO_TRY(hip_check(hipMemcpyAsync(capture, hidden, rows * w * 4,
                                        hipMemcpyDeviceToHost, stream_),
                         "capture download"));
@@ -554,6 +576,10 @@ Status Context::enqueue(const uint32_t *device_tokens, size_t rows, bool initial
   EVO_TRY(embed_tokens(device_tokens, rows, model_->embedding.as<uint16_t>(), c.vocab,
                        c.width, hidden_.as<float>(), flag_.as<int>(), stream_));
   EVO_TRY(run_layers(rows, capture_layer, capture));
+  if (device_logits == nullptr || rows <= kFoldRows) {
+    EVO_TRY(split_k_finish(pending_, hidden_.as<float>(), rows, c.width, stream_));
+    pending_ = SplitPartials{};
+  }
   if (device_logits != nullptr) {
     const GemmOutput logits{device_logits, nullptr, nullptr, c.vocab};
     if (rows <= kFoldRows) {
@@ -564,8 +590,9 @@ Status Context::enqueue(const uint32_t *device_tokens, size_t rows, bool initial
     } else {
       uint16_t *hi = normed_.as<uint16_t>();
       uint16_t *lo = options_.split_activations ? hi + rows * c.width : nullptr;
-      EVO_TRY(rms_norm(hidden_.as<float>(), rows, c.width, model_->final_norm.as<float>(),
-                       c.eps, nullptr, hi, lo, stream_));
+      EVO_TRY(rms_norm_partials(pending_, hidden_.as<float>(), rows, c.width,
+                                model_->final_norm.as<float>(), c.eps, hi, lo, stream_));
+      pending_ = SplitPartials{};
       EVO_TRY(gemm_bf16w(Activation{hi, lo, c.width}, model_->embedding.as<uint16_t>(), logits,
                          rows, c.vocab, c.width, kGemmStore, nullptr, nullptr, false, 0,
                          stream_, workspace_.as<float>(), workspace_.bytes()));

@@ -139,6 +139,9 @@ private:
   void reset_caches();
 
   std::shared_ptr<const Model> model_;
+  // Split-K partials of the last MLP l3 product not yet summed into hidden_
+  // (short chunks): the next RMSNorm of hidden_ sums them as it reads them.
+  SplitPartials pending_{};
   ContextOptions options_;
   std::string profile_;
   hipStream_t stream_{nullptr};

@@ -54,14 +54,31 @@ struct RowNorm {
   float eps;
   size_t ld;
 };
+// Split-K partial products left for their consumer: C[m, n] =
+// sum_s part[s][m, n] (s in order) (+ bf16 bias[n]) (+ residual[m, n]),
+// C row stride N. splits == 0: nothing is pending.
+struct SplitPartials {
+  const float *part = nullptr;
+  int splits = 0;
+  size_t plane = 0;  // floats per partial (M * N)
+  const uint16_t *bias = nullptr;
+  const float *residual = nullptr;
+};
 // C = A . W^T with W BF16 [N,K]; see gemm.hip.
 // With a split workspace (F32), launches with few output tiles (non-gated
-// modes) split K across blocks and sum the partials in split order.
+// modes) split K across blocks and sum the partials in split order. With
+// `deferred` (and C rows of stride N), such a launch stores only the
+// partials and describes them there, for a consumer that sums them itself
+// (rms_norm_partials, or split_k_finish); otherwise deferred->splits = 0.
 Status gemm_bf16w(const Activation &a, const uint16_t *W, const GemmOutput &out,
                   size_t M, size_t N, size_t K, GemmEpilogue mode,
                   const uint16_t *bias, const float *residual, bool gelu,
                   size_t gated_width, hipStream_t stream, float *split_workspace = nullptr,
-                  size_t split_workspace_bytes = 0);
+                  size_t split_workspace_bytes = 0, SplitPartials *deferred = nullptr);
+// Forms C [rows, width] from pending partials (what the GEMM's own
+// reduction would have written).
+Status split_k_finish(const SplitPartials &src, float *C, size_t rows, size_t width,
+                      hipStream_t stream);
 // The same product of norm(x) (M <= 4; `split`: the activation as hi + lo
 // planes, as the hip-f32 profile's rms_norm writes it, else hi only).
 Status gemm_bf16w_normed(const RowNorm &norm, bool split, const uint16_t *W,
@@ -109,6 +126,13 @@ Status embed_tokens(const uint32_t *tokens, size_t rows, const uint16_t *table,
 Status rms_norm(const float *x, size_t rows, size_t width, const float *scale,
                 float eps, float *out_f32, uint16_t *out_hi, uint16_t *out_lo,
                 hipStream_t stream, uint8_t *codes = nullptr, float code_scale = 1.0F);
+// rms_norm of x = the sum of pending split-K partials, which it also
+// writes to `sum` (F32 [rows, width]): split_k_finish followed by rms_norm
+// of its output, in one pass, with the same values.
+Status rms_norm_partials(const SplitPartials &src, float *sum, size_t rows, size_t width,
+                         const float *scale, float eps, uint16_t *out_hi, uint16_t *out_lo,
+                         hipStream_t stream, uint8_t *codes = nullptr,
+                         float code_scale = 1.0F);
 // Copies the last `history` rows of the sequence [old_history ; x] into
 // history (F32 [history, channels]), keeping continuation caches.
 Status update_history(const float *x, size_t rows, size_t channels,
