@@ -162,8 +162,17 @@ def kernel_rooflines(split):
     del proj, planes_out
     # config 3: FP8 projection GEMM M=1024 K=4096 N=12288 (promotion every 32 K)
     m, k, n = 1024, 4096, 12288
-    a8 = torch.randint(0, 0x7e, (m, k), dtype=torch.uint8, device="cuda", generator=g)
-    w8 = torch.randint(0, 0x7e, (n, k), dtype=torch.uint8, device="cuda", generator=g)
+
+    def e4m3_codes(shape, std):
+        """Config 3's operands: N(0, std) values quantised per tensor to
+        E4M3 with amax scaling (the codes; the scale folds into the output
+        scale)."""
+        x = torch.randn(shape, device="cuda", generator=g) * std
+        x = x * (448.0 / x.abs().max())
+        return x.to(torch.float8_e4m3fn).view(torch.uint8)
+
+    a8 = e4m3_codes((m, k), 1.0)
+    w8 = e4m3_codes((n, k), 0.02)
     # BF16 output, the projection's own output type (each value is
     # bf16(acc * output_scale)), as the model writes it.
     y8 = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
@@ -174,15 +183,6 @@ def kernel_rooflines(split):
         flops = 2.0 * m * n * k
         out[name] = dict(kernel=f"fp8_mfma_kernel<{32 if mode == 0 else 128}>", ms=ms,
                          flops=flops, tflops=flops / ms / 1e9)
-    # The same projection at the 8192-token prefill's M (the model's shape).
-    m = 8192
-    a8 = torch.randint(0, 0x7e, (m, k), dtype=torch.uint8, device="cuda", generator=g)
-    y8 = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
-    ms = event_time(lambda: native.call("evo_hip_fp8_linear_bf16", a8.data_ptr(), w8.data_ptr(),
-                                        y8.data_ptr(), m, n, k, 1e-3, 1, stream), 10)
-    flops = 2.0 * m * n * k
-    out["fp8_k128_m8192"] = dict(kernel="fp8_mfma_kernel<128>", ms=ms, flops=flops,
-                                 tflops=flops / ms / 1e9)
     return out
 
 
@@ -486,7 +486,7 @@ def main():
         worst = min(hyena, key=lambda h: h["frac"])
         result["hyena_roofline"] = dict(worst, bound="hbm", per_launch=per_launch)
         result["hyena_kernels"] = hyena
-        for name in ("fp8_k32", "fp8_k128", "fp8_k128_m8192"):
+        for name in ("fp8_k32", "fp8_k128"):
             f = kernels[name]
             result[name + "_roofline"] = {"bound": "mfma", "kernel": f["kernel"],
                                           "achieved": round(f["tflops"], 1),
