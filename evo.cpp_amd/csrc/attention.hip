@@ -235,15 +235,13 @@ __global__ __launch_bounds__(kFlashWaves * 64) void flash_attention_kernel(
   const size_t wave_first = prefix + block_row + wave * kQueriesPerWave;  // lowest position
   issue(0);
   for (size_t tile = 0; tile < tiles; ++tile) {
-    // Every wave has left buffer (tile+1)&1 (tile-1's) once it passes here.
+    // This wave's DMA of the tile (the only one in flight), then one
+    // barrier: every wave's DMA of the tile has landed and every wave has
+    // left buffer (tile+1)&1 (tile-1's), which the next DMA overwrites.
+    wait_dma<0>();
     __syncthreads();
-    if (tile + 1 < tiles) {
+    if (tile + 1 < tiles)
       issue(tile + 1);
-      wait_dma<Shape::kDmaPerWave>();
-    } else {
-      wait_dma<0>();
-    }
-    __syncthreads();
     const uint16_t *stage = flash_lds + (tile & 1) * Shape::kStage;
     const uint16_t *k_hi = stage, *k_lo = stage + Shape::kKPlane;
     const uint16_t *v_hi = stage + 2 * Shape::kKPlane, *v_lo = v_hi + Shape::kVPlane;
