@@ -579,6 +579,23 @@ evo_status evo_hip_context_prefill_resident(evo_context *context, const uint32_t
   });
 }
 
+evo_status evo_hip_context_set_product_timing(evo_context *context, int enable) {
+  return protect([&]() -> evo_status {
+    if (context == nullptr || !context->hip)
+      return publish(EVO_STATUS_INVALID_ARGUMENT, "invalid_argument: context is null");
+    return publish(context->hip->set_product_timing(enable != 0));
+  });
+}
+
+evo_status evo_hip_context_product_time(const evo_context *context, float *ms,
+                                        size_t *launches) {
+  return protect([&]() -> evo_status {
+    if (context == nullptr || !context->hip)
+      return publish(EVO_STATUS_INVALID_ARGUMENT, "invalid_argument: context is null");
+    return publish(context->hip->product_time(ms, launches));
+  });
+}
+
 void *evo_hip_context_stream(const evo_context *context) {
   return context == nullptr || !context->hip ? nullptr : context->hip->stream();
 }

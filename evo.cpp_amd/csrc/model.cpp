@@ -321,12 +321,44 @@ Status Model::load(const Artifact &a, int device, bool allow_synthetic,
 
 // ------------------------------------------------------------------ Context
 Context::~Context() {
+  for (hipEvent_t event : timing_events_)
+    (void)hipEventDestroy(event);
   if (host_logits_ != nullptr)
     (void)hipHostFree(host_logits_);
   if (host_flag_ != nullptr)
     (void)hipHostFree(host_flag_);
   if (stream_ != nullptr)
     (void)hipStreamDestroy(stream_);
+}
+
+Status Context::set_product_timing(bool on) {
+  if (!on) {
+    for (hipEvent_t event : timing_events_)
+      EVO_TRY(hip_check(hipEventDestroy(event), "timing event"));
+    timing_events_.clear();
+    return Status::Ok();
+  }
+  if (!timing_events_.empty())
+    return Status::Ok();
+  timing_events_.resize(2 * model_->config().layers, nullptr);
+  for (hipEvent_t &event : timing_events_)
+    EVO_TRY(hip_check(hipEventCreate(&event), "timing event"));
+  return Status::Ok();
+}
+
+Status Context::product_time(float *ms, size_t *launches) const {
+  if (ms == nullptr || launches == nullptr)
+    return {ErrorCode::kInvalidArgument, "invalid_argument: null output"};
+  *ms = 0.0F;
+  *launches = 0;
+  for (size_t i = 0; i + 1 < timing_events_.size(); i += 2) {
+    float elapsed = 0.0F;
+    EVO_TRY(hip_check(hipEventElapsedTime(&elapsed, timing_events_[i], timing_events_[i + 1]),
+                      "timing event"));
+    *ms += elapsed;
+    ++*launches;
+  }
+  return Status::Ok();
 }
 
 Status Context::initialize(std::shared_ptr<const Model> model, size_t capacity,
@@ -535,10 +567,14 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
     else
       EVO_TRY(rms_norm_partials(out_partials, residual, rows, w, L.post_norm.as<float>(),
                                 c.eps, normed_hi, split ? normed_lo : nullptr, stream_));
+    if (!timing_events_.empty())
+      EVO_TRY(hip_check(hipEventRecord(timing_events_[2 * i], stream_), "timing event"));
     EVO_TRY(gemm_bf16w(normed, L.mlp_in.as<uint16_t>(),
                        GemmOutput{nullptr, gated_hi, split ? gated_lo : nullptr, c.inner},
                        rows, 2 * c.inner_padded, w, kGemmGated, nullptr, nullptr, i == 0,
                        c.inner, stream_, workspace_.as<float>(), workspace_.bytes()));
+    if (!timing_events_.empty())
+      EVO_TRY(hip_check(hipEventRecord(timing_events_[2 * i + 1], stream_), "timing event"));
     // hidden = gated . l3^T + residual
     // Its split-K partials (short chunks) are summed by the next norm of
     // hidden, unless this layer's output is captured.

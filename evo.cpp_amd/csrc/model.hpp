@@ -124,6 +124,11 @@ public:
   // one synchronisation at the end, no host transfer of activations.
   Status prefill_resident(const uint32_t *device_tokens, size_t count,
                           float *device_logits);
+  // HIP events around each layer's MLP l1/l2 product (off by default), for
+  // timing the dominant kernel inside real prefills; product_time reads the
+  // last chunk's launches (the caller has synchronised).
+  Status set_product_timing(bool on);
+  Status product_time(float *ms, size_t *launches) const;
   size_t position() const { return position_; }
   size_t activation_capacity() const { return arena_rows_; }
   size_t capacity() const { return capacity_; }
@@ -142,6 +147,7 @@ private:
   // Split-K partials of the last MLP l3 product not yet summed into hidden_
   // (short chunks): the next RMSNorm of hidden_ sums them as it reads them.
   SplitPartials pending_{};
+  std::vector<hipEvent_t> timing_events_;  // start / stop per layer, or empty
   ContextOptions options_;
   std::string profile_;
   hipStream_t stream_{nullptr};

@@ -55,6 +55,8 @@ _OPS = {
     "evo_hip_rms_norm": (c_int, [c_void, c_size, c_size, c_void, c_float, c_void, c_void,
                                  c_void, c_void]),
     "evo_hip_context_prefill_resident": (c_int, [c_void, c_void, c_size, c_void]),
+    "evo_hip_context_set_product_timing": (c_int, [c_void, c_int]),
+    "evo_hip_context_product_time": (c_int, [c_void, c_void, c_void]),
     "evo_hip_attention": (c_int, [c_void, c_size, c_size, c_size, c_int, c_void, c_float,
                                   c_size, c_void, c_void, c_void, c_size, c_void, c_void]),
     "evo_hip_attention_ws": (c_int, [c_void, c_size, c_size, c_size, c_int, c_void, c_float,

@@ -39,6 +39,15 @@ EVO_API evo_status evo_hip_context_prefill_resident(evo_context *context,
 /* The context's HIP stream (hipStream_t), for ordering caller work. */
 EVO_API void *evo_hip_context_stream(const evo_context *context);
 
+/* Measurement hooks (no counterpart in the reference): with timing on, each
+ * prefill records HIP events on the context stream around every layer's MLP
+ * l1/l2 product (the dominant kernel); evo_hip_context_product_time returns
+ * the summed duration (ms) and the number of launches of the last chunk
+ * prefilled, once the caller has seen that prefill complete. Off by default. */
+EVO_API evo_status evo_hip_context_set_product_timing(evo_context *context, int enable);
+EVO_API evo_status evo_hip_context_product_time(const evo_context *context, float *ms,
+                                                size_t *launches);
+
 /* Storage type of activation tensors passed to the Hyena operator. */
 /* EVO_HIP_SPLIT: F32 input, output as split BF16 planes [2][rows][cols]
  * (hi = bf16(y), lo = bf16(y - hi)), the GEMM activation layout.
