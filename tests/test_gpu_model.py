@@ -223,3 +223,31 @@ def test_decode_argument_errors(hip, tmp_path):
         ctx.decode(512)
     assert vocab.value.status == 2
     assert ctx.decode(71).shape == (512,)  # a rejected call leaves the context usable
+
+
+def test_product_timing_hooks(hip, tmp_path):
+    """The measurement hooks bench.py reads: no timed launches by default;
+    with timing on, one MLP l1/l2 launch per layer, each with a positive
+    duration, after a prefill; off again, none."""
+    import ctypes
+    shape = A.tiny_shape(width=64, layers=8, heads=2, inner=96, groups=4, attn=(3,))
+    path = make(tmp_path, shape, seed=44)
+    ctx = open_context(hip, path, capacity=64)
+    lib = hip.lib
+    lib.evo_hip_context_set_product_timing.argtypes = [ctypes.c_void_p, ctypes.c_int]
+    lib.evo_hip_context_product_time.argtypes = [
+        ctypes.c_void_p, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_size_t)]
+    ms, launches = ctypes.c_float(), ctypes.c_size_t()
+
+    def read():
+        hip.check(lib.evo_hip_context_product_time(ctx.handle, ctypes.byref(ms),
+                                                   ctypes.byref(launches)))
+        return ms.value, launches.value
+
+    assert read() == (0.0, 0)
+    hip.check(lib.evo_hip_context_set_product_timing(ctx.handle, 1))
+    ctx.prefill(bytes(A.acgt_tokens(64, seed=2).astype(np.uint8)))
+    total, count = read()
+    assert count == 8 and total > 0.0
+    hip.check(lib.evo_hip_context_set_product_timing(ctx.handle, 0))
+    assert read() == (0.0, 0)
