@@ -298,6 +298,34 @@ __global__ __launch_bounds__(kWaves * 64) void fp8_mfma_kernel(
       }
     }
   }
+  if constexpr (std::is_same<Out, uint16_t>::value) {
+    if (N % 2 == 0 && reinterpret_cast<uintptr_t>(out) % 4 == 0) {
+      // BF16 pairs: lanes col and col ^ 1 swap one value of each row pair
+      // (e, e + 1), so the even lane stores row r at columns (col, col + 1)
+      // and the odd lane row r + 1 at (col - 1, col): one 32-bit store per
+      // two values.
+      const bool even = (col & 1) == 0;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; e += 2) {
+          const int row = block_m + wave_m * 64 + i * 32 + (e >> 2) * 8 + half * 4 + (e & 3);
+#pragma unroll
+          for (int j = 0; j < 3; ++j) {
+            const uint32_t first = f32_to_bf16(round_bf16(acc[i][j][e] * output_scale));
+            const uint32_t second = f32_to_bf16(round_bf16(acc[i][j][e + 1] * output_scale));
+            const uint32_t other = static_cast<uint32_t>(__shfl_xor(
+                static_cast<int>(even ? second : first), 1, 64));
+            const int out_row = even ? row : row + 1;
+            const int column = block_n + wave_n * 96 + j * 32 + (col & ~1);
+            if (out_row < M && column < N)
+              *reinterpret_cast<uint32_t *>(out + static_cast<size_t>(out_row) * N + column) =
+                  even ? (first | (other << 16)) : (other | (second << 16));
+          }
+        }
+      return;
+    }
+  }
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
