@@ -128,7 +128,7 @@ __device__ inline int swizzle(int row, int unit) {
   return unit ^ ((row * kUnits / 16) & (kUnits - 1));
 }
 
-template <int kD>
+template <int kD, int kFlashWaves = kFlashWaves>
 struct FlashShape {
   static constexpr int kKUnits = kD / 8;             // 16-byte units per K row
   static constexpr int kKPlane = kKeys * kD;         // BF16 per K plane
@@ -139,12 +139,12 @@ struct FlashShape {
   static constexpr int kDmaPerWave = 4 * kChunksPerPlane / kFlashWaves;
 };
 
-template <int kD, typename O>
+template <int kD, typename O, int kFlashWaves = kFlashWaves>
 __global__ __launch_bounds__(kFlashWaves * 64) void flash_attention_kernel(
     const uint16_t *__restrict__ q, size_t q_plane, const uint16_t *__restrict__ k_cache,
     const uint16_t *__restrict__ vt_cache, size_t cache_plane, size_t capacity, size_t rows,
     size_t prefix, size_t heads, O out) {
-  using Shape = FlashShape<kD>;
+  using Shape = FlashShape<kD, kFlashWaves>;
   constexpr int kDSteps = kD / 16;  // K-steps of S^T over head_dim
   constexpr int kDTiles = kD / 32;  // 32-row tiles of O^T
   extern __shared__ __attribute__((aligned(16))) uint16_t flash_lds[];
@@ -418,15 +418,21 @@ Status launch_flash(const uint16_t *q, size_t q_plane, const uint16_t *k_cache,
                     size_t prefix, size_t heads, O out, hipStream_t stream) {
   constexpr size_t lds = FlashShape<kD>::kLdsBytes;
   static_assert(lds <= 160 * 1024, "LDS");
-  auto kernel = flash_attention_kernel<kD, O>;
+  // Blocks of 8 waves share each K/V tile among 256 queries; when that
+  // leaves CUs idle (short chunks: 1024 rows x 32 heads = 128 blocks), blocks
+  // of 4 waves (128 queries) fill twice as many.
+  const bool half = ceil_div(rows, kFlashWaves * kQueriesPerWave) * heads < 256;
+  const int waves = half ? kFlashWaves / 2 : kFlashWaves;
+  auto kernel = half ? flash_attention_kernel<kD, O, kFlashWaves / 2>
+                     : flash_attention_kernel<kD, O, kFlashWaves>;
   EVO_TRY(hip_status(hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
                                          hipFuncAttributeMaxDynamicSharedMemorySize,
                                          static_cast<int>(lds)),
                      "flash_attention_kernel LDS opt-in"));
-  const size_t blocks = ceil_div(rows, kFlashWaves * kQueriesPerWave) * heads;
-  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(kFlashWaves * 64), lds,
-                     stream, q,
-                     q_plane, k_cache, v_cache, cache_plane, capacity, rows, prefix, heads, out);
+  const size_t blocks = ceil_div(rows, static_cast<size_t>(waves) * kQueriesPerWave) * heads;
+  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(waves * 64), lds, stream,
+                     q, q_plane, k_cache, v_cache, cache_plane, capacity, rows, prefix, heads,
+                     out);
   return launch_status("flash_attention_kernel");
 }
 
