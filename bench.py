@@ -1,4 +1,4 @@
-"""Prefill benchmark of the MI355X StripedHyena2 library.
+"""Prefill benchmark of the MI355X StripedHyena2 library (the 7B-shaped prefill).
 
 Workload: Evo-2-7B-shaped model (32 blocks, width 4096, 32 heads, FFN 11264,
 byte vocab 512; hyena short/medium-128/long striping with attention at blocks
@@ -316,7 +316,8 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build runs on one "
-              "MI355X; the multi-GPU layout is described in DESIGN.md", file=sys.stderr)
+              "MI355X (one process per GPU would each run this prefill on its own "
+              "share; no collective is implemented)", file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -453,7 +454,7 @@ def main():
                  else "fp8-e4m3 projections + bf16 MFMA",
         "data": "synthetic (seeded random-init weights, uniform ACGT tokens)",
         "config": {"workload": f"evo2-7b-shape prefill L={args.tokens}, batch 1, "
-                               "fp8 hyena projections (BASELINE config 4)",
+                               "fp8 hyena projections (config 4)",
                    "tokens": args.tokens, "layers": shape.layers, "width": shape.width,
                    "heads": shape.heads, "ffn": shape.inner,
                    "profile": context.profile, "tok_s_1k": round(rate_1k, 1),
