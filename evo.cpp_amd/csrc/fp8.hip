@@ -136,8 +136,10 @@ __global__ __launch_bounds__(256) void qgmma_exact_kernel(
     put(out, static_cast<size_t>(row) * N + col, round_bf16(acc * output_scale));
 }
 
-// MFMA path. Block 256 (M) x 192 (N) outputs, 8 waves as 4 (M) x 2 (N) of
-// 64 x 96 (2 x 3 MFMA 32x32 tiles), two waves per SIMD; the 96 accumulators
+// MFMA path. Block 128 (M) x 192 (N) outputs, 4 waves as 2 (M) x 2 (N) of
+// 64 x 96 (2 x 3 MFMA 32x32 tiles); two blocks share a CU (80 KB of LDS
+// each), so two waves per SIMD and one block's barrier wait runs under the
+// other block's MFMAs; the 96 accumulators
 // per lane stay in VGPRs, so the E8M13 truncation after each promotion is
 // one VALU op per value. The accumulator is the MFMA's C operand: a chunk's
 // products are summed onto it inside the matrix core and the sum is
@@ -146,32 +148,32 @@ __global__ __launch_bounds__(256) void qgmma_exact_kernel(
 // per step by DMA into LDS rows of eight 16-byte units, unit u of row r at
 // r*8 + (u ^ ((r >> 1) & 7)) so that the fragment reads of 8 consecutive rows
 // hit 8 distinct bank groups; two stages alternate. A 1024-row projection
-// is 4 x 64 = 256 tiles: one per CU. Rows beyond M or N load a clamped
+// is 8 x 64 = 512 tiles: two per CU. Rows beyond M or N load a clamped
 // valid row and are never stored.
-constexpr int kBM = 256, kBN = 192, kBK = 128, kStages = 2;
-constexpr int kWaves = 8;
-constexpr int kStageBytes = (kBM + kBN) * kBK;            // 56 KB
-constexpr int kDmaPerWave = kStageBytes / 1024 / kWaves;  // 7
+constexpr int kBM = 128, kBN = 192, kBK = 128, kStages = 2;
+constexpr int kWaves = 4;
+constexpr int kStageBytes = (kBM + kBN) * kBK;            // 40 KB
+constexpr int kDmaPerWave = kStageBytes / 1024 / kWaves;  // 10
 constexpr size_t kMfmaLds = static_cast<size_t>(kStages) * kStageBytes;
 
 __device__ inline int fp8_unit(int row, int unit) { return row * 8 + (unit ^ ((row >> 1) & 7)); }
 
 template <int kChunk, typename Out>
-__global__ __launch_bounds__(kWaves * 64) void fp8_mfma_kernel(
+__global__ __launch_bounds__(kWaves * 64, 2) void fp8_mfma_kernel(
     const uint8_t *__restrict__ a, const uint8_t *__restrict__ w,
     Out *__restrict__ out, int M, int N, int K, float output_scale) {
   extern __shared__ __attribute__((aligned(16))) uint8_t fp8_lds[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5, col = lane & 31;
-  const int wave_m = wave >> 1, wave_n = wave & 1;  // 4 x 2
+  const int wave_m = wave >> 1, wave_n = wave & 1;  // 2 x 2
   const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
   int tm, tn;
   tile_of(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
   const int block_m = tm * kBM, block_n = tn * kBN;
 
-  // DMA op g = wave*7 + i: 1 KB chunk g of the stage (chunks 0..31 = A rows
-  // 8g.., 32..55 = W rows 8(g-32)..); lane l fills unit 64 g' + l. Each op
+  // DMA op g = wave*10 + i: 1 KB chunk g of the stage (chunks 0..15 = A rows
+  // 8g.., 16..39 = W rows 8(g-16)..); lane l fills unit 64 g' + l. Each op
   // reads from a wave-uniform base (the block's first A or W row, advanced
   // by the step's K offset) plus a fixed 32-bit per-lane offset.
   const uint8_t *a_base = a + static_cast<size_t>(block_m) * K;
@@ -548,7 +550,8 @@ Status fp8_linear_impl(const uint8_t *in_codes, const uint8_t *w_codes, Out *out
     return launch_status("fp8_gemv_kernel");
   }
   const auto kernel = mode == kFp8MfmaK32 ? fp8_mfma_kernel<32, Out> : fp8_mfma_kernel<128, Out>;
-  // 112 KB of the CU's 160 KB LDS: opt in above the 64 KB default.
+  // 80 KB of the CU's 160 KB LDS (two blocks per CU): opt in above the
+  // 64 KB default.
   EVO_TRY(hip_status(hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
                                          hipFuncAttributeMaxDynamicSharedMemorySize,
                                          static_cast<int>(kMfmaLds)),
