@@ -387,6 +387,8 @@ __global__ __launch_bounds__(512) void gemm_kernel(
     src_a_lo[i] = kSplit ? a_lo + static_cast<size_t>(ar) * lda + seg * 8 : nullptr;
     src_w[i] = W + static_cast<size_t>(wr) * ldw + seg * 8;
   }
+  // The A planes' DMAs go out before the weight's (issuing them
+  // interleaved per row group measured 4 % slower on the MLP shape).
   auto issue = [&](int step) {
     uint16_t *stage = lds + (step % kStages) * kStage;
     const int k0 = step * kBK;
@@ -396,8 +398,10 @@ __global__ __launch_bounds__(512) void gemm_kernel(
       dma16(src_a_hi[i] + k0, stage + unit0 * 8);
       if (kSplit)
         dma16(src_a_lo[i] + k0, stage + kPlane + unit0 * 8);
-      dma16(src_w[i] + k0, stage + (kPlanes - 1) * kPlane + unit0 * 8);
     }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      dma16(src_w[i] + k0, stage + (kPlanes - 1) * kPlane + (wave * 2 + i) * 64 * 8);
   };
 
   f32x4 acc[kMI][kNJ];
