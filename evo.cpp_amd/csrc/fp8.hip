@@ -233,8 +233,6 @@ __global__ __launch_bounds__(kWaves * 64, 2) void fp8_mfma_kernel(
     // Every wave's DMA of step s has landed and every wave has left the
     // buffer of step s-1, which the next issue overwrites.
     __syncthreads();
-    if (s + 1 < steps)
-      issue(s + 1);
     const uint8_t *a_s = fp8_lds + (s % kStages) * kStageBytes;
     const uint8_t *w_s = a_s + kBM * kBK;
     if constexpr (kChunk == 128) {
@@ -255,6 +253,14 @@ __global__ __launch_bounds__(kWaves * 64, 2) void fp8_mfma_kernel(
         for (int j = 0; j < 3; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
               av[0][i], bv[0][j], acc[i][j], 0, 0, 0, 127, 0, 127);
+      // The next step's DMA (into the buffer of step s-1, which every wave
+      // has left) goes out here, under the first K half's MFMAs, rather
+      // than right after the barrier, where its VMEM issue delayed the
+      // fragment reads (config 3: 53.5 -> 50.3 us, bit-identical).
+      __builtin_amdgcn_sched_barrier(0);
+      if (s + 1 < steps)
+        issue(s + 1);
+      __builtin_amdgcn_sched_barrier(0);
       // Second K half: each tile's promotion runs while the next tile's
       // MFMA executes (only the last tile's truncation is left at the end).
 #pragma unroll
@@ -273,6 +279,8 @@ __global__ __launch_bounds__(kWaves * 64, 2) void fp8_mfma_kernel(
       for (int e = 0; e < 16; ++e)
         acc[1][2][e] = truncate_e8m13(acc[1][2][e]);
     } else {
+      if (s + 1 < steps)
+        issue(s + 1);
       // Four 32-K chunks, each two K=16 MFMAs then a promotion.
 #pragma unroll
       for (int c = 0; c < kBK / 32; ++c) {
