@@ -1261,14 +1261,12 @@ __device__ inline void store16_words(void *dst, const uint32_t (&w)[4]) {
   __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(dst));
 }
 template <> struct MsOut<float *> {
-  __device__ static int stores(float *) { return 2; }
   __device__ static void flush(const float *src, float *out, size_t index) {
     store16_nt(out + index, src);
     store16_nt(out + index + 4, src + 4);
   }
 };
 template <> struct MsOut<uint16_t *> {
-  __device__ static int stores(uint16_t *) { return 1; }
   __device__ static void flush(const float *src, uint16_t *out, size_t index) {
     float v[8];
     load8(src, v);
@@ -1280,7 +1278,6 @@ template <> struct MsOut<uint16_t *> {
   }
 };
 template <> struct MsOut<SplitOut> {
-  __device__ static int stores(const SplitOut &out) { return out.lo != nullptr ? 2 : 1; }
   __device__ static void flush(const float *src, const SplitOut &out, size_t index) {
     float v[8];
     load8(src, v);
@@ -1424,7 +1421,6 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void hyena_fir_mfma_st
   const int col = lane & 15, g = lane >> 4;
   const size_t cw = c0 + 16 * wave + col;
   const float *h = filter + ((c0 + 16 * wave) / group_size) * k;
-  const int stores = MsOut<O>::stores(out);
   // The wave's filter (k <= 128 taps of its group) goes to LDS between 160
   // zeros on either side, so that the Toeplitz fragments gather from there
   // after the first barrier with unconditional reads (80 taps per lane read
@@ -1634,25 +1630,21 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void hyena_fir_mfma_st
   wait_dma<0>();
   __syncthreads();
 
-  // Phase s: DMA of step s + 2 into the stage step s used; flush s - 1;
+  // Phase s: flush s - 1; DMA of step s + 2 into the stage step s used;
   // produce s + 1; multiply s. Before the barrier, the DMA of step s + 2 must
-  // be complete (younger: only the flush stores of step s - 1).
+  // be complete (nothing younger is in flight). The flush goes out ahead of
+  // the DMA: the other order, with the wait leaving the younger flush
+  // stores in flight, measured 1 % slower.
   auto phase = [&](auto rot, int step) __attribute__((always_inline)) {
-    if (step + 2 < steps)
-      issue(step + 2);
     if (step >= 1)
       flush(step - 1);
+    if (step + 2 < steps)
+      issue(step + 2);
     if (step + 1 < steps)
       produce(step + 1);
     multiply(rot, step);
-    if (step + 2 < steps) {
-      if (step - 1 >= lead && stores == 2)
-        wait_dma<2>();
-      else if (step - 1 >= lead)
-        wait_dma<1>();
-      else
-        wait_dma<0>();
-    }
+    if (step + 2 < steps)
+      wait_dma<0>();
     __syncthreads();
   };
   // Unrolled by the ring length so that the rotation is static.
