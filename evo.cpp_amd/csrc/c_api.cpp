@@ -669,14 +669,6 @@ evo_status evo_hip_hyena_forward_static(evo_hip_hyena_kind kind, evo_hip_dtype d
                                         float *inner_history, float *modal_state, void *output,
                                         void *stream) {
   return protect([&]() -> evo_status {
-    const size_t needed = evo::hip::hyena_workspace_bytes(static_cast<int>(kind), length,
-                                                          width, state_size);
-    if (needed > evo::hip::kHyenaStaticScratchBytes)
-      return publish(EVO_STATUS_INVALID_ARGUMENT,
-                     "invalid_argument: operator needs " + std::to_string(needed) +
-                         " bytes of workspace, more than the static scratch's " +
-                         std::to_string(evo::hip::kHyenaStaticScratchBytes) +
-                         "; use evo_hip_hyena_forward with a workspace");
     void *scratch = nullptr;
     const auto found = evo::hip::hyena_static_scratch(&scratch);
     if (!found.ok())
@@ -684,10 +676,22 @@ evo_status evo_hip_hyena_forward_static(evo_hip_hyena_kind kind, evo_hip_dtype d
     const bool taps_bf16 = (static_cast<int>(dtype) & EVO_HIP_BF16_TAPS) != 0;
     const evo::hip::HyenaWeights w{short_filter, short_len, inner_filter, groups, inner_len,
                                    direct, poles, residues, state_size, taps_bf16};
-    return publish(hyena_dispatch(kind, dtype, projection, length, width, w, short_history,
-                                  inner_history, modal_state, scratch,
-                                  evo::hip::kHyenaStaticScratchBytes, output,
-                                  static_cast<hipStream_t>(stream)));
+    // Only the paths that keep data in a workspace (the three-pass HCL
+    // fallback's chunk states, the F32-tap Toeplitz table) use the scratch;
+    // each checks its need against the scratch's size before any launch.
+    const evo::Status status =
+        hyena_dispatch(kind, dtype, projection, length, width, w, short_history, inner_history,
+                       modal_state, scratch, evo::hip::kHyenaStaticScratchBytes, output,
+                       static_cast<hipStream_t>(stream));
+    if (!status.ok() && status.message().find("workspace too small") != std::string::npos)
+      return publish(EVO_STATUS_INVALID_ARGUMENT,
+                     "invalid_argument: this shape's path needs " +
+                         std::to_string(evo::hip::hyena_workspace_bytes(
+                             static_cast<int>(kind), length, width, state_size)) +
+                         " bytes of workspace, more than the static scratch's " +
+                         std::to_string(evo::hip::kHyenaStaticScratchBytes) +
+                         "; use evo_hip_hyena_forward with a workspace");
+    return publish(status);
   });
 }
 

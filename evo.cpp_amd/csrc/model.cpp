@@ -336,13 +336,22 @@ Status Context::set_product_timing(bool on) {
     for (hipEvent_t event : timing_events_)
       EVO_TRY(hip_check(hipEventDestroy(event), "timing event"));
     timing_events_.clear();
+    timed_pairs_ = 0;
     return Status::Ok();
   }
   if (!timing_events_.empty())
     return Status::Ok();
+  timed_pairs_ = 0;
   timing_events_.resize(2 * model_->config().layers, nullptr);
   for (hipEvent_t &event : timing_events_)
     EVO_TRY(hip_check(hipEventCreate(&event), "timing event"));
+  return Status::Ok();
+}
+
+Status Context::workspace_free(const char *user) const {
+  if (pending_.splits != 0)
+    return {ErrorCode::kInternal, std::string("internal: ") + user +
+                                      " would overwrite deferred split-K partials"};
   return Status::Ok();
 }
 
@@ -351,7 +360,7 @@ Status Context::product_time(float *ms, size_t *launches) const {
     return {ErrorCode::kInvalidArgument, "invalid_argument: null output"};
   *ms = 0.0F;
   *launches = 0;
-  for (size_t i = 0; i + 1 < timing_events_.size(); i += 2) {
+  for (size_t i = 0; i + 1 < timing_events_.size() && i / 2 < timed_pairs_; i += 2) {
     float elapsed = 0.0F;
     EVO_TRY(hip_check(hipEventElapsedTime(&elapsed, timing_events_[i], timing_events_[i + 1]),
                       "timing event"));
@@ -467,6 +476,7 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
   // it (same values, one launch and round trip less per norm).
   const bool fold = rows <= kFoldRows;
   pending_ = SplitPartials{};
+  timed_pairs_ = 0;
   for (size_t i = 0; i < c.layers; ++i) {
     const Layer &L = model_->layer[i];
     Cache &k = cache_[i];
@@ -508,6 +518,7 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
                          GemmOutput{projected, nullptr, nullptr, 3 * w}, rows, 3 * w, w,
                          kGemmStore, nullptr, nullptr, false, 0, stream_));
     }
+    EVO_TRY(workspace_free("the mixer"));
     if (L.type == Mixer::kAttention) {
       uint16_t *query = query_.as<uint16_t>();
       const size_t cache_plane = cache_capacity_ * w;
@@ -573,8 +584,10 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
                        GemmOutput{nullptr, gated_hi, split ? gated_lo : nullptr, c.inner},
                        rows, 2 * c.inner_padded, w, kGemmGated, nullptr, nullptr, i == 0,
                        c.inner, stream_, workspace_.as<float>(), workspace_.bytes()));
-    if (!timing_events_.empty())
+    if (!timing_events_.empty()) {
       EVO_TRY(hip_check(hipEventRecord(timing_events_[2 * i + 1], stream_), "timing event"));
+      timed_pairs_ = i + 1;
+    }
     // hidden = gated . l3^T + residual
     // Its split-K partials (short chunks) are summed by the next norm of
     // hidden, unless this layer's output is captured.
@@ -629,6 +642,7 @@ Status Context::enqueue(const uint32_t *device_tokens, size_t rows, bool initial
       EVO_TRY(rms_norm_partials(pending_, hidden_.as<float>(), rows, c.width,
                                 model_->final_norm.as<float>(), c.eps, hi, lo, stream_));
       pending_ = SplitPartials{};
+      EVO_TRY(workspace_free("the unembedding"));
       EVO_TRY(gemm_bf16w(Activation{hi, lo, c.width}, model_->embedding.as<uint16_t>(), logits,
                          rows, c.vocab, c.width, kGemmStore, nullptr, nullptr, false, 0,
                          stream_, workspace_.as<float>(), workspace_.bytes()));

@@ -126,7 +126,9 @@ public:
                           float *device_logits);
   // HIP events around each layer's MLP l1/l2 product (off by default), for
   // timing the dominant kernel inside real prefills; product_time reads the
-  // last chunk's launches (the caller has synchronised).
+  // launches of the last enqueued chunk (the caller has synchronised). A
+  // decode step is a chunk too and replaces them; (0, 0) before any chunk
+  // and after a chunk that failed before its first product.
   Status set_product_timing(bool on);
   Status product_time(float *ms, size_t *launches) const;
   size_t position() const { return position_; }
@@ -142,12 +144,16 @@ private:
   Status finish();
   Status run_layers(size_t rows, size_t capture_layer, float *capture);
   void reset_caches();
+  // workspace_ holds pending_'s partials until the next norm of hidden_
+  // consumes them: every other user of workspace_ checks this first.
+  Status workspace_free(const char *user) const;
 
   std::shared_ptr<const Model> model_;
   // Split-K partials of the last MLP l3 product not yet summed into hidden_
   // (short chunks): the next RMSNorm of hidden_ sums them as it reads them.
   SplitPartials pending_{};
   std::vector<hipEvent_t> timing_events_;  // start / stop per layer, or empty
+  size_t timed_pairs_{0};  // event pairs the last enqueued chunk recorded
   ContextOptions options_;
   std::string profile_;
   hipStream_t stream_{nullptr};

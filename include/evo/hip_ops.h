@@ -107,8 +107,13 @@ EVO_API evo_status evo_hip_hyena_forward(
  * the workspace, same kernels and results. The workspace comes from a fixed
  * device array of evo_hip_hyena_static_scratch_bytes() (32 MiB) in the
  * library, one per device, held until the process ends; the call fails with
- * EVO_STATUS_INVALID_ARGUMENT when evo_hip_hyena_workspace_bytes() of the
- * shape exceeds it (HCL at W = 4096, 16 states: up to 16384 rows per call).
+ * EVO_STATUS_INVALID_ARGUMENT, before any launch, when the path the shape
+ * takes keeps more than that in its workspace. Only two paths use one: the
+ * three-pass HCL fallback (planar projections, short filters other than 3
+ * taps, W % 16 != 0; chunk states of evo_hip_hyena_workspace_bytes()) and
+ * the F32-tap HCS/HCM MFMA FIR (its Toeplitz table, 2.6 MB at W = 4096).
+ * The model's shapes (one-pass HCL, streaming HCS/HCM) need none and are
+ * accepted at any length.
  * The call makes no device allocation (no hipMalloc/hipFree), so callers that
  * cannot allocate (code under HIP graph capture, tight serving loops) can
  * use it. Every call on a device shares that device's array: calls that

@@ -521,38 +521,176 @@ qgmma_group(const int32_t *sa, const int32_t *ea, const int32_t *ba,
                                   0xfffffc00U);
 }
 
+__attribute__((target("avx2"), always_inline)) inline __m256i
+load_i8x8(const int8_t *p) {
+  return _mm256_cvtepi8_epi32(_mm_loadl_epi64(reinterpret_cast<const __m128i *>(p)));
+}
+
+// Eight outputs of one row at once (one per lane) over weight tables laid
+// out [k][lane] (significand, exponent, binade planes). Per
+// group and lane the same integer arithmetic as qgmma_group; lanes whose
+// rescale would leave the normal range finish through qgmma_group_avx2's
+// scalar tail instead.
+__attribute__((target("avx2"))) void
+qgmma_row_lanes(const int8_t *sa, const int8_t *ea, const int8_t *ba, const int8_t *tsig,
+                const int8_t *texp, const int8_t *tbin, size_t inner, size_t group_k,
+                float *result) {
+  const __m256i zero = _mm256_setzero_si256();
+  __m256 acc = _mm256_setzero_ps();
+  for (size_t start = 0; start < inner; start += group_k) {
+    const __m256i acc_bits = _mm256_castps_si256(acc);
+    const __m256i acc_zero = _mm256_cmpeq_epi32(
+        _mm256_and_si256(acc_bits, _mm256_set1_epi32(0x7fffffff)), zero);
+    const __m256i acc_exp = _mm256_sub_epi32(
+        _mm256_and_si256(_mm256_srli_epi32(acc_bits, 23), _mm256_set1_epi32(0xff)),
+        _mm256_set1_epi32(127));
+    __m256i top = _mm256_blendv_epi8(acc_exp, _mm256_set1_epi32(-1024), acc_zero);
+    for (size_t k = 0; k < group_k; ++k) {
+      const __m256i bv = load_i8x8(tbin + (start + k) * 8);
+      top = _mm256_max_epi32(top, _mm256_add_epi32(bv, _mm256_set1_epi32(ba[start + k])));
+    }
+    const __m256i bias = _mm256_sub_epi32(_mm256_set1_epi32(13), top);
+    __m256i sum = zero;
+    for (size_t k = 0; k < group_k; ++k) {
+      const __m256i sig_b = load_i8x8(tsig + (start + k) * 8);
+      const __m256i exp_b = load_i8x8(texp + (start + k) * 8);
+      const __m256i product = _mm256_mullo_epi32(sig_b, _mm256_set1_epi32(sa[start + k]));
+      const __m256i shift = _mm256_add_epi32(_mm256_add_epi32(exp_b, _mm256_set1_epi32(ea[start + k])), bias);
+      const __m256i left = _mm256_max_epi32(shift, zero);
+      const __m256i right = _mm256_max_epi32(_mm256_sub_epi32(zero, shift), zero);
+      const __m256i aligned =
+          _mm256_srlv_epi32(_mm256_sllv_epi32(_mm256_abs_epi32(product), left), right);
+      sum = _mm256_add_epi32(sum, _mm256_sign_epi32(aligned, product));
+    }
+    // The accumulator aligned to top (align_to with product = false).
+    const __m256i acc_sig = _mm256_srli_epi32(
+        _mm256_or_si256(_mm256_and_si256(acc_bits, _mm256_set1_epi32(0x7fffff)),
+                        _mm256_set1_epi32(0x800000)), 10);
+    __m256i acc_aligned = _mm256_srlv_epi32(acc_sig, _mm256_sub_epi32(top, acc_exp));
+    acc_aligned = _mm256_sign_epi32(acc_aligned,
+                                    _mm256_or_si256(acc_bits, _mm256_set1_epi32(1)));
+    acc_aligned = _mm256_andnot_si256(acc_zero, acc_aligned);
+    sum = _mm256_add_epi32(sum, acc_aligned);
+    // ldexp(float(sum), top - 13) as a product by 2^(top - 13), exact while
+    // normal; other lanes take std::ldexp.
+    const __m256i e = _mm256_sub_epi32(top, _mm256_set1_epi32(13));
+    const __m256i e_ok = _mm256_and_si256(_mm256_cmpgt_epi32(e, _mm256_set1_epi32(-127)),
+                                          _mm256_cmpgt_epi32(_mm256_set1_epi32(128), e));
+    const __m256 pow2 = _mm256_castsi256_ps(
+        _mm256_slli_epi32(_mm256_add_epi32(e, _mm256_set1_epi32(127)), 23));
+    const __m256 fsum = _mm256_cvtepi32_ps(sum);
+    __m256 scaled = _mm256_mul_ps(fsum, pow2);
+    const __m256 mag = _mm256_andnot_ps(_mm256_set1_ps(-0.0F), scaled);
+    const __m256 normal = _mm256_and_ps(_mm256_cmp_ps(mag, _mm256_set1_ps(0x1p-126F), _CMP_GE_OQ),
+                                        _mm256_cmp_ps(mag, _mm256_set1_ps(INFINITY), _CMP_LT_OQ));
+    const __m256i sum_zero = _mm256_cmpeq_epi32(sum, zero);
+    const int good = _mm256_movemask_ps(_mm256_or_ps(
+        _mm256_castsi256_ps(sum_zero),
+        _mm256_and_ps(normal, _mm256_castsi256_ps(e_ok))));
+    scaled = _mm256_andnot_ps(_mm256_castsi256_ps(sum_zero), scaled);
+    if (good != 0xff) {
+      alignas(32) float lanes[8];
+      alignas(32) int32_t sums[8], exps[8];
+      _mm256_store_ps(lanes, scaled);
+      _mm256_store_si256(reinterpret_cast<__m256i *>(sums), sum);
+      _mm256_store_si256(reinterpret_cast<__m256i *>(exps), e);
+      for (int lane = 0; lane < 8; ++lane)
+        if ((good >> lane & 1) == 0)
+          lanes[lane] = std::ldexp(static_cast<float>(sums[lane]), exps[lane]);
+      scaled = _mm256_load_ps(lanes);
+    }
+    acc = _mm256_castsi256_ps(
+        _mm256_and_si256(_mm256_castps_si256(scaled), _mm256_set1_epi32(static_cast<int>(0xfffffc00U))));
+  }
+  _mm256_storeu_ps(result, acc);
+}
+
+
 void qgmma_core(const uint8_t *input_codes, const uint8_t *weight_codes,
                 size_t rows, size_t inner, size_t cols, float output_scale,
                 size_t group_k, float *out, int threads) {
   static const E4m3Table table;
-  // Decoded input rows, tabulated once: significand, exponent, binade.
-  std::vector<int32_t> sa(rows * inner), ea(rows * inner), ba(rows * inner);
-  for (size_t i = 0; i < rows * inner; ++i) {
-    sa[i] = table.signed_significand[input_codes[i]];
-    ea[i] = table.exponent[input_codes[i]];
-    ba[i] = table.binade[input_codes[i]];
+  if (group_k % 8 != 0) {
+    // Scalar walk for groups the vector form does not cover.
+    std::vector<int32_t> sa(rows * inner), ea(rows * inner), ba(rows * inner);
+    for (size_t i = 0; i < rows * inner; ++i) {
+      sa[i] = table.signed_significand[input_codes[i]];
+      ea[i] = table.exponent[input_codes[i]];
+      ba[i] = table.binade[input_codes[i]];
+    }
+#pragma omp parallel num_threads(threads > 0 ? threads : 1)
+    {
+      std::vector<int32_t> sb(inner), eb(inner), bb(inner);
+#pragma omp for schedule(dynamic, 4)
+      for (long long c = 0; c < static_cast<long long>(cols); ++c) {
+        const size_t col = static_cast<size_t>(c);
+        for (size_t k = 0; k < inner; ++k) {
+          const uint8_t code = weight_codes[col * inner + k];
+          sb[k] = table.signed_significand[code];
+          eb[k] = table.exponent[code];
+          bb[k] = table.binade[code];
+        }
+        for (size_t row = 0; row < rows; ++row) {
+          float acc = 0.0F;
+          for (size_t start = 0; start < inner; start += group_k) {
+            const size_t at = row * inner + start;
+            qgmma_group(&sa[at], &ea[at], &ba[at], &sb[start], &eb[start], &bb[start],
+                        group_k, &acc);
+          }
+          out[row * cols + col] =
+              bf16_bits_to_float(float_to_bf16_rne(acc * output_scale));
+        }
+      }
+    }
+    return;
   }
+  // int8 tables of both operands (zero and NaN codes get binade -64, below
+  // every real product binade, so they never set a group's top).
+  auto decode = [&](const uint8_t *codes, size_t n, std::vector<int8_t> &s,
+                    std::vector<int8_t> &e, std::vector<int8_t> &b) {
+    s.resize(n), e.resize(n), b.resize(n);
+#pragma omp parallel for schedule(static) num_threads(threads > 0 ? threads : 1)
+    for (long long i = 0; i < static_cast<long long>(n); ++i) {
+      const uint8_t code = codes[i];
+      s[i] = static_cast<int8_t>(table.signed_significand[code]);
+      e[i] = static_cast<int8_t>(table.exponent[code]);
+      b[i] = static_cast<int8_t>(std::max(table.binade[code], -64));
+    }
+  };
+  std::vector<int8_t> sa, ea, ba, sb, eb, bb;
+  decode(input_codes, rows * inner, sa, ea, ba);
+  decode(weight_codes, cols * inner, sb, eb, bb);
+  // Eight columns at a time, one per vector lane: the weight tables of the
+  // eight columns are laid out [k][lane], the row's terms broadcast.
+  // Each lane is one output's sequential group walk.
+  constexpr size_t kLanes = 8, kRows = 64;
+  const size_t col_tiles = (cols + kLanes - 1) / kLanes, row_tiles = (rows + kRows - 1) / kRows;
 #pragma omp parallel num_threads(threads > 0 ? threads : 1)
   {
-    std::vector<int32_t> sb(inner), eb(inner), bb(inner);
-#pragma omp for schedule(dynamic, 4)
-    for (long long c = 0; c < static_cast<long long>(cols); ++c) {
-      const size_t col = static_cast<size_t>(c);
-      for (size_t k = 0; k < inner; ++k) {
-        const uint8_t code = weight_codes[col * inner + k];
-        sb[k] = table.signed_significand[code];
-        eb[k] = table.exponent[code];
-        bb[k] = table.binade[code];
+    std::vector<int8_t> tb(inner * kLanes * 3);
+    long long current = -1;
+#pragma omp for schedule(dynamic, 1)
+    for (long long tile = 0; tile < static_cast<long long>(col_tiles * row_tiles); ++tile) {
+      const size_t c0 = static_cast<size_t>(tile) / row_tiles * kLanes;
+      const size_t r0 = static_cast<size_t>(tile) % row_tiles * kRows;
+      if (current != static_cast<long long>(c0)) {
+        current = static_cast<long long>(c0);
+        for (size_t k = 0; k < inner; ++k)
+          for (size_t lane = 0; lane < kLanes; ++lane) {
+            const size_t col = std::min(c0 + lane, cols - 1);
+            tb[k * kLanes + lane] = sb[col * inner + k];
+            tb[(inner + k) * kLanes + lane] = eb[col * inner + k];
+            tb[(2 * inner + k) * kLanes + lane] = bb[col * inner + k];
+          }
       }
-      for (size_t row = 0; row < rows; ++row) {
-        float acc = 0.0F;
-        for (size_t start = 0; start < inner; start += group_k) {
-          const size_t at = row * inner + start;
-          qgmma_group(&sa[at], &ea[at], &ba[at], &sb[start], &eb[start], &bb[start],
-                      group_k, &acc);
-        }
-        out[row * cols + col] =
-            bf16_bits_to_float(float_to_bf16_rne(acc * output_scale));
+      float results[kLanes];
+      for (size_t row = r0; row < std::min(r0 + kRows, rows); ++row) {
+        qgmma_row_lanes(&sa[row * inner], &ea[row * inner], &ba[row * inner], tb.data(),
+                        tb.data() + inner * kLanes, tb.data() + 2 * inner * kLanes, inner,
+                        group_k, results);
+        for (size_t lane = 0; lane < kLanes && c0 + lane < cols; ++lane)
+          out[row * cols + c0 + lane] =
+              bf16_bits_to_float(float_to_bf16_rne(results[lane] * output_scale));
       }
     }
   }
@@ -993,8 +1131,20 @@ void oracle_e4m3_quantize_f32(const float *x, size_t n, float scale,
 
 void oracle_e4m3_quantize_bf16(const uint16_t *x, size_t n, float scale,
                                uint8_t *codes) {
-  for (size_t i = 0; i < n; ++i)
-    codes[i] = oracle_e4m3_encode(bf16_bits_to_float(x[i]) * scale);
+  // The code depends only on the 16-bit input pattern: large inputs encode
+  // each of the 65536 patterns once and look them up.
+  if (n < (1U << 18)) {
+    for (size_t i = 0; i < n; ++i)
+      codes[i] = oracle_e4m3_encode(bf16_bits_to_float(x[i]) * scale);
+    return;
+  }
+  std::vector<uint8_t> table(1U << 16);
+#pragma omp parallel for schedule(static)
+  for (int bits = 0; bits < (1 << 16); ++bits)
+    table[bits] = oracle_e4m3_encode(bf16_bits_to_float(static_cast<uint16_t>(bits)) * scale);
+#pragma omp parallel for schedule(static)
+  for (long long i = 0; i < static_cast<long long>(n); ++i)
+    codes[i] = table[x[i]];
 }
 
 int oracle_qgmma_linear(const uint8_t *input_codes, const uint8_t *weight_codes,

@@ -335,3 +335,66 @@ def test_fp8_projection_modes_at_7b_width(hip, evo2_7b):
         assert logit_error <= 2e-4
         assert block_error <= 2e-4
         assert agreement >= 0.993
+
+
+# ------------------------- the benchmarked configuration against the oracle
+def fp8_block_errors(model, sequence, blocks, layers, capacity):
+    """Max error of every block output (relative to that block's oracle
+    output scale) with the benchmarked context (flags 0: FP8 MFMA K128)."""
+    errors = []
+    for layer in range(layers):
+        hidden = context_of(model, capacity).embed(sequence, layer)
+        errors.append(relmax(hidden, blocks[layer]))
+    return errors
+
+
+@pytest.mark.timeout(1200)
+def test_benchmarked_fp8_k128_full_7b_at_1024_tokens(hip, evo2_7b):
+    """The benchmarked configuration exactly as bench.py runs it: the 32-block
+    7B shape, every Hyena projection converted to E4M3 at load, context flags
+    0 (MFMA K128), 1024 tokens, against the oracle with the same conversion
+    (the reference CPU path's ops, with the CUDA reference's FP8 semantics:
+    codes of bf16(x) * input_scale, QGMMA K=32). Every block output and the
+    logits within 1e-3 of their scale, top-1 100 %."""
+    tokens = A.acgt_tokens(1024, seed=1024)
+    sequence = tokens.astype(np.uint8).tobytes()
+    t0 = time.time()
+    expected, blocks = O.OracleModel(evo2_7b).convert_fp8(8.0).prefill(
+        tokens, chunk=1024, threads=THREADS, capture_layer="all")
+    say(f"FP8 7B oracle (1024 tokens): {time.time() - t0:.1f} s")
+    model = loaded(hip, evo2_7b, 1 << 8)
+    ids = dev(tokens.astype(np.uint32))
+    logits_dev = empty((1024, 512))
+    N.call("evo_hip_context_prefill_resident", context_of(model, 1024).handle, p(ids), 1024,
+           p(logits_dev))
+    logits = host(logits_dev)
+    errors = fp8_block_errors(model, sequence, blocks, A.evo2_7b_shape().layers, 1024)
+    top1 = float(np.mean(logits.argmax(1) == expected.argmax(1)))
+    say(f"  logits max err {relmax(logits, expected):.3g}, worst block {max(errors):.3g} "
+        f"(block {int(np.argmax(errors))}), top-1 {top1}")
+    assert max(errors) <= 1e-3
+    assert relmax(logits, expected) <= 1e-3
+    assert top1 == 1.0
+
+
+@pytest.mark.timeout(1200)
+def test_fp8_k128_one_block_of_each_mixer_at_8192_tokens(hip, one_of_each_7b):
+    """Config 4's one-of-each 7B-width model (HCS, HCM, HCL, attention) with
+    FP8 Hyena projections converted at load, MFMA K128, 8192 tokens, against
+    the oracle with the same conversion: every block output and the logits
+    within 1e-3 of their scale, top-1 100 %."""
+    tokens = A.acgt_tokens(8192, seed=48)
+    sequence = tokens.astype(np.uint8).tobytes()
+    t0 = time.time()
+    expected, blocks = O.OracleModel(one_of_each_7b).convert_fp8(8.0).prefill(
+        tokens, chunk=8192, threads=THREADS, capture_layer="all")
+    say(f"FP8 one-of-each oracle (8192 tokens): {time.time() - t0:.1f} s")
+    model = hip.load(one_of_each_7b, capi.BACKEND_HIP, flags=1 << 8)
+    logits = context_of(model, 8192).prefill(sequence)
+    errors = fp8_block_errors(model, sequence, blocks, 4, 8192)
+    top1 = float(np.mean(logits.argmax(1) == expected.argmax(1)))
+    say(f"  logits max err {relmax(logits, expected):.3g}, block errors "
+        f"{', '.join(f'{e:.3g}' for e in errors)}, top-1 {top1}")
+    assert max(errors) <= 1e-3
+    assert relmax(logits, expected) <= 1e-3
+    assert top1 == 1.0
