@@ -363,11 +363,7 @@ def test_benchmarked_fp8_k128_full_7b_at_1024_tokens(hip, evo2_7b):
         tokens, chunk=1024, threads=THREADS, capture_layer="all")
     say(f"FP8 7B oracle (1024 tokens): {time.time() - t0:.1f} s")
     model = loaded(hip, evo2_7b, 1 << 8)
-    ids = dev(tokens.astype(np.uint32))
-    logits_dev = empty((1024, 512))
-    N.call("evo_hip_context_prefill_resident", context_of(model, 1024).handle, p(ids), 1024,
-           p(logits_dev))
-    logits = host(logits_dev)
+    logits = resident_prefill(hip, evo2_7b, tokens, model_flags=1 << 8)
     errors = fp8_block_errors(model, sequence, blocks, A.evo2_7b_shape().layers, 1024)
     top1 = float(np.mean(logits.argmax(1) == expected.argmax(1)))
     say(f"  logits max err {relmax(logits, expected):.3g}, worst block {max(errors):.3g} "
