@@ -112,9 +112,12 @@ def test_fp8_projection_model_mfma(hip, tmp_path):
     by about one BF16 ulp and downstream E4M3 codes flip; with the "unit"
     init each flip moves the logits visibly. Measured: relmax 0.0345, cosine
     0.99966, top-1 98.7 % (2 of 150 rows, near ties). Bounds: that envelope
-    with margin (relmax 0.06, cosine 0.9993, top-1 97 %). At 7B width with the
-    benchmark init this mode is within 4e-5 and top-1 100 %
-    (test_gpu_configs.py::test_fp8_projection_modes_at_7b_width)."""
+    with margin (relmax 0.06, cosine 0.9993, top-1 97 %). This tiny model is
+    built to amplify code flips (the "unit" init) and bounds how far they can
+    carry, not the benchmarked configuration's accuracy: with the benchmark
+    init the same mode is within 1e-3 of the oracle with top-1 100 % at 7B
+    width (measured 4.3e-5 for the full 32 blocks at 1024 tokens, 1.5e-5 for
+    the one-of-each model at 8192 tokens: test_gpu_configs.py)."""
     path, tokens, expected = fp8_model(tmp_path)
     actual, profile = run_hip(hip, path, tokens)
     cosine = float((actual.ravel() @ expected.ravel()) /
