@@ -382,6 +382,12 @@ Status Context::initialize(std::shared_ptr<const Model> model, size_t capacity,
   cache_capacity_ = (capacity + 63) / 64 * 64;
   arena_rows_ = std::min(capacity, kArenaRows);
   // Test hook: a smaller activation arena forces multi-chunk prefill.
+  // Diagnostic: GEMM classes that read only the hi plane of their split
+  // activation (bit 0 BF16 projections, 1 out-projection, 2 MLP l1/l2,
+  // 3 MLP l3), to measure how each class's activation rounding reaches the
+  // logits. Unset (0) in every supported profile.
+  if (const char *mask = std::getenv("EVO_HIP_HI_ONLY_GEMMS"))
+    hi_only_ = static_cast<unsigned>(std::strtoul(mask, nullptr, 0));
   if (const char *rows = std::getenv("EVO_HIP_ARENA_ROWS")) {
     const long value = std::atol(rows);
     if (value > 0)
@@ -514,7 +520,8 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
       EVO_TRY(rms_norm_partials(pending_, hidden, rows, w, L.pre_norm.as<float>(), c.eps,
                                 normed_hi, split ? normed_lo : nullptr, stream_));
       pending_ = SplitPartials{};
-      EVO_TRY(gemm_bf16w(normed, L.projection.as<uint16_t>(),
+      EVO_TRY(gemm_bf16w(hi_only_ & 1U ? Activation{normed_hi, nullptr, w} : normed,
+                         L.projection.as<uint16_t>(),
                          GemmOutput{projected, nullptr, nullptr, 3 * w}, rows, 3 * w, w,
                          kGemmStore, nullptr, nullptr, false, 0, stream_));
     }
@@ -563,7 +570,8 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
     // Short chunks split K here; the post-mixer norm then sums the partials
     // (with bias and hidden) into residual as it reads them.
     SplitPartials out_partials;
-    EVO_TRY(gemm_bf16w(mixed, L.out_weight.as<uint16_t>(),
+    EVO_TRY(gemm_bf16w(hi_only_ & 2U ? Activation{mixed_hi, nullptr, w} : mixed,
+                       L.out_weight.as<uint16_t>(),
                        GemmOutput{residual, nullptr, nullptr, w}, rows, w, w,
                        kGemmBiasResidual, L.out_bias.as<uint16_t>(), hidden, false, 0,
                        stream_, workspace_.as<float>(), workspace_.bytes(),
@@ -580,7 +588,8 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
                                 c.eps, normed_hi, split ? normed_lo : nullptr, stream_));
     if (!timing_events_.empty())
       EVO_TRY(hip_check(hipEventRecord(timing_events_[2 * i], stream_), "timing event"));
-    EVO_TRY(gemm_bf16w(normed, L.mlp_in.as<uint16_t>(),
+    EVO_TRY(gemm_bf16w(hi_only_ & 4U ? Activation{normed_hi, nullptr, w} : normed,
+                       L.mlp_in.as<uint16_t>(),
                        GemmOutput{nullptr, gated_hi, split ? gated_lo : nullptr, c.inner},
                        rows, 2 * c.inner_padded, w, kGemmGated, nullptr, nullptr, i == 0,
                        c.inner, stream_, workspace_.as<float>(), workspace_.bytes()));
@@ -592,7 +601,8 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
     // Its split-K partials (short chunks) are summed by the next norm of
     // hidden, unless this layer's output is captured.
     const bool captured = capture != nullptr && capture_layer == i;
-    EVO_TRY(gemm_bf16w(gated, L.mlp_out.as<uint16_t>(), GemmOutput{hidden, nullptr, nullptr, w},
+    EVO_TRY(gemm_bf16w(hi_only_ & 8U ? Activation{gated_hi, nullptr, c.inner} : gated,
+                       L.mlp_out.as<uint16_t>(), GemmOutput{hidden, nullptr, nullptr, w},
                        rows, w, c.inner, kGemmResidual, nullptr, residual, false, 0, stream_,
                        workspace_.as<float>(), workspace_.bytes(),
                        fold || captured ? nullptr : &pending_));

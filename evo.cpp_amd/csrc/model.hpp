@@ -153,7 +153,8 @@ private:
   // (short chunks): the next RMSNorm of hidden_ sums them as it reads them.
   SplitPartials pending_{};
   std::vector<hipEvent_t> timing_events_;  // start / stop per layer, or empty
-  size_t timed_pairs_{0};  // event pairs the last enqueued chunk recorded
+  size_t timed_pairs_{0};
+  unsigned hi_only_{0};  // diagnostic: GEMM classes run on the hi plane only  // event pairs the last enqueued chunk recorded
   ContextOptions options_;
   std::string profile_;
   hipStream_t stream_{nullptr};

@@ -729,6 +729,83 @@ void linear_model(const std::vector<float> &input, size_t rows, size_t in,
   }
 }
 
+// ---- Design experiment, not a reference function (off unless
+// oracle_set_lo_emulation sets a class mask): a BF16-weight linear as a
+// proposed two-pass GEMM would compute it, y = hi . W + q(lo) . q(W), with
+// hi = bf16(x), lo = x - hi, and q() E4M3 (RNE, satfinite) under an
+// E8M0 scale per row and 32-K block (2^ceil(log2(amax / 448)), so no block
+// saturates). q(W) is exact in BF16, so both products run as BF16-weight
+// dots. Used only to measure how such a GEMM's rounding reaches the logits.
+unsigned g_lo_emulation = 0;  // bit 0 projections, 1 out, 2 l1/l2, 3 l3
+
+float e4m3_block_scale(const float *v, size_t n) {
+  float amax = 0.0F;
+  for (size_t i = 0; i < n; ++i)
+    amax = std::max(amax, std::fabs(v[i]));
+  if (!(amax > 0.0F))
+    return 1.0F;
+  return std::ldexp(1.0F, static_cast<int>(std::ceil(std::log2(amax / 448.0F))));
+}
+
+float e4m3_round(const float value, const float scale) {
+  return oracle_e4m3_decode(oracle_e4m3_encode(value / scale)) * scale;
+}
+
+const Tensor &quantized_weight(const Tensor &weight, size_t out_width, size_t in) {
+  static std::map<const uint8_t *, std::pair<std::vector<uint16_t>, Tensor>> cache;
+  auto found = cache.find(weight.data);
+  if (found != cache.end())
+    return found->second.second;
+  auto &entry = cache[weight.data];
+  entry.first.resize(out_width * in);
+#pragma omp parallel for schedule(static)
+  for (long long r = 0; r < static_cast<long long>(out_width); ++r) {
+    std::vector<float> block(32);
+    for (size_t k0 = 0; k0 < in; k0 += 32) {
+      const size_t n = std::min<size_t>(32, in - k0);
+      for (size_t k = 0; k < n; ++k)
+        block[k] = weight.at(static_cast<size_t>(r) * in + k0 + k);
+      const float scale = e4m3_block_scale(block.data(), n);
+      for (size_t k = 0; k < n; ++k)
+        entry.first[static_cast<size_t>(r) * in + k0 + k] =
+            float_to_bf16_rne(e4m3_round(block[k], scale));
+    }
+  }
+  entry.second = weight;
+  entry.second.data = reinterpret_cast<const uint8_t *>(entry.first.data());
+  return entry.second;
+}
+
+void linear_class(unsigned cls, const std::vector<float> &input, size_t rows, size_t in,
+                  const Tensor &weight, size_t out_width, const Tensor *bias,
+                  std::vector<float> *output, int threads) {
+  if ((g_lo_emulation >> cls & 1U) == 0 || weight.dtype != "BF16") {
+    linear_model(input, rows, in, weight, out_width, bias, output, threads);
+    return;
+  }
+  std::vector<float> hi(input.size()), lo(input.size());
+#pragma omp parallel for schedule(static)
+  for (long long r = 0; r < static_cast<long long>(rows); ++r) {
+    const size_t base = static_cast<size_t>(r) * in;
+    for (size_t k = 0; k < in; ++k) {
+      hi[base + k] = bf16_bits_to_float(float_to_bf16_rne(input[base + k]));
+      lo[base + k] = input[base + k] - hi[base + k];
+    }
+    for (size_t k0 = 0; k0 < in; k0 += 32) {
+      const size_t n = std::min<size_t>(32, in - k0);
+      const float scale = e4m3_block_scale(&lo[base + k0], n);
+      for (size_t k = 0; k < n; ++k)
+        lo[base + k0 + k] = e4m3_round(lo[base + k0 + k], scale);
+    }
+  }
+  std::vector<float> second;
+  linear_model(hi, rows, in, weight, out_width, bias, output, threads);
+  linear_model(lo, rows, in, quantized_weight(weight, out_width, in), out_width, nullptr,
+               &second, threads);
+  for (size_t i = 0; i < output->size(); ++i)
+    (*output)[i] += second[i];
+}
+
 // FP8 projection with CUDA-reference semantics: codes of bf16(x)*input_scale,
 // QGMMA K=32 accumulation, bf16(acc*output_scale).
 void linear_fp8(const std::vector<float> &input, size_t rows, size_t in,
@@ -1088,6 +1165,8 @@ extern "C" {
 
 const char *oracle_last_error(void) { return g_error.c_str(); }
 
+void oracle_set_lo_emulation(unsigned mask) { g_lo_emulation = mask; }
+
 uint8_t oracle_e4m3_encode(const float value) {
   const bool negative = std::signbit(value);
   const auto sign = static_cast<uint8_t>(negative ? 0x80U : 0x00U);
@@ -1444,7 +1523,7 @@ int oracle_model_prefill(void *model_handle, const uint32_t *tokens, size_t n,
                    layer.fp8_input_scale, layer.fp8_output_scale, &projected,
                    threads);
       else
-        linear_model(normalized, rows, w, *layer.projection, 3 * w, nullptr,
+        linear_class(0, normalized, rows, w, *layer.projection, 3 * w, nullptr,
                      &projected, threads);
       if (layer.type == Mixer::kAttention) {
         attention_model(m, projected, rows, layer, &state[index], &mixed);
@@ -1463,21 +1542,21 @@ int oracle_model_prefill(void *model_handle, const uint32_t *tokens, size_t n,
             [res](size_t i) { return res->at(i); }, m.state, &state[index],
             &mixed);
       }
-      linear_model(mixed, rows, w, *layer.out_weight, w, layer.out_bias,
+      linear_class(1, mixed, rows, w, *layer.out_weight, w, layer.out_bias,
                    &residual, threads);
       for (size_t i = 0; i < residual.size(); ++i)
         residual[i] += hidden[i];
       rms_norm_model(residual, rows, w, *layer.post_norm, m.eps, &normalized);
-      linear_model(normalized, rows, w, *layer.l1, m.inner, nullptr, &first,
+      linear_class(2, normalized, rows, w, *layer.l1, m.inner, nullptr, &first,
                    threads);
-      linear_model(normalized, rows, w, *layer.l2, m.inner, nullptr, &second,
+      linear_class(2, normalized, rows, w, *layer.l2, m.inner, nullptr, &second,
                    threads);
       gated.resize(first.size());
       for (size_t i = 0; i < gated.size(); ++i) {
         const float activated = index == 0 ? gelu_erf(first[i]) : first[i];
         gated[i] = activated * second[i];
       }
-      linear_model(gated, rows, m.inner, *layer.l3, w, nullptr, &hidden,
+      linear_class(3, gated, rows, m.inner, *layer.l3, w, nullptr, &hidden,
                    threads);
       for (size_t i = 0; i < hidden.size(); ++i)
         hidden[i] += residual[i];
