@@ -184,6 +184,32 @@ def kernel_rooflines(split):
         flops = 2.0 * m * n * k
         out[name] = dict(kernel=f"fp8_mfma_kernel<{32 if mode == 0 else 128}>", ms=ms,
                          flops=flops, tflops=flops / ms / 1e9)
+    # The bit-exact mode (the reference's per-term QGMMA semantics on the
+    # VALU): one launch, for the cost of exact reference semantics.
+    ms = event_time(lambda: native.call("evo_hip_fp8_linear_bf16", a8.data_ptr(),
+                                        w8.data_ptr(), y8.data_ptr(), m, n, k, 1e-3, 2,
+                                        stream), 1)
+    out["fp8_exact"] = dict(kernel="qgmma_exact_kernel", ms=ms, flops=2.0 * m * n * k,
+                            tflops=2.0 * m * n * k / ms / 1e9)
+    del a8, w8, y8
+    # Attention block body at the benchmarked shape (8192 rows from position
+    # 0, 32 heads of 128): causal 2 * L^2 * W flop (Q.K^T and P.V over the
+    # lower triangle); the timed op includes the Q/K/V split and RoPE.
+    length, width, heads = 8192, 4096, 32
+    cap = length
+    projected = torch.randn(length, 3 * width, device="cuda", generator=g)
+    inv_freq = (1.0 / (10000.0 ** (torch.arange(0, 128, 2, device="cuda").float() / 128)))
+    query = torch.empty(2 * length * width, dtype=torch.int16, device="cuda")
+    keys = torch.zeros(2 * cap * width, dtype=torch.int16, device="cuda")
+    values = torch.zeros(2 * cap * width, dtype=torch.int16, device="cuda")
+    att_out = torch.empty(length, width, device="cuda")
+    ms = event_time(lambda: native.call("evo_hip_attention", projected.data_ptr(), length,
+                                        width, heads, 1, inv_freq.data_ptr(), 1.0, 0,
+                                        query.data_ptr(), keys.data_ptr(), values.data_ptr(),
+                                        cap, att_out.data_ptr(), stream), 5)
+    flops = 2.0 * length * length * width
+    out["attention"] = dict(kernel="qkv_rope_kernel + flash_attention_kernel", ms=ms,
+                            flops=flops, tflops=flops / ms / 1e9)
     return out
 
 
@@ -545,6 +571,19 @@ def main():
                                           "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
                                           "frac": round(f["tflops"] / FP8_PEAK_TFLOPS, 4),
                                           "ms": round(f["ms"], 4)}
+        f = kernels["fp8_exact"]
+        result["fp8_exact"] = {"kernel": f["kernel"], "ms": round(f["ms"], 3),
+                               "achieved": round(f["tflops"], 2), "unit": "TFLOP/s",
+                               "frac": round(f["tflops"] / FP8_PEAK_TFLOPS, 5),
+                               "note": "bit-exact reference QGMMA semantics (integer "
+                                       "emulation on the VALU), config 3"}
+        f = kernels["attention"]
+        result["attention_roofline"] = {
+            "bound": "mfma", "kernel": f["kernel"], "achieved": round(f["tflops"], 1),
+            "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(f["tflops"] / BF16_PEAK_TFLOPS, 4), "ms": round(f["ms"], 4),
+            "per_launch": "2*8192^2*4096 flop (causal Q.K^T and P.V, 32 heads of 128; "
+                          "three BF16 MFMA passes per product)"}
     context.close()
     model.close()
     torch.cuda.empty_cache()
