@@ -736,7 +736,7 @@ void linear_model(const std::vector<float> &input, size_t rows, size_t in,
 // E8M0 scale per row and 32-K block (2^ceil(log2(amax / 448)), so no block
 // saturates). q(W) is exact in BF16, so both products run as BF16-weight
 // dots. Used only to measure how such a GEMM's rounding reaches the logits.
-unsigned g_lo_emulation = 0;  // bit 0 projections, 1 out, 2 l1/l2, 3 l3
+unsigned g_lo_emulation = 0;  // bit 0 projections, 1 out, 2 l1/l2, 3 l3; 4, 5 attention
 
 float e4m3_block_scale(const float *v, size_t n) {
   float amax = 0.0F;
@@ -965,6 +965,15 @@ void attention_model(const Model &m, const std::vector<float> &projected,
       }
     }
   }
+  // Design experiment (oracle_set_lo_emulation bits 4 and 5): keys or
+  // values rounded to BF16, i.e. two-pass split products K.Q^T or P.V
+  // (hi.hi + hi.lo with the key's / value's lo pass dropped).
+  if (g_lo_emulation >> 4 & 1U)
+    for (float &v : key)
+      v = bf16_bits_to_float(float_to_bf16_rne(v));
+  if (g_lo_emulation >> 5 & 1U)
+    for (float &v : value)
+      v = bf16_bits_to_float(float_to_bf16_rne(v));
   cache->key.insert(cache->key.end(), key.begin(), key.end());
   cache->value.insert(cache->value.end(), value.begin(), value.end());
   output->assign(rows * width, 0.0F);

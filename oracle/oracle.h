@@ -118,8 +118,9 @@ int oracle_model_convert_fp8(void *model, float input_amax);
 const char *oracle_last_error(void);
 /* Design experiment (off by default): BF16-weight linears of the classes in
  * `mask` (bit 0 projections, 1 out-projection, 2 MLP l1/l2, 3 MLP l3) run as
- * hi . W + E4M3(lo) . E4M3(W) with E8M0 scales per 32 K. Not a reference
- * function. */
+ * hi . W + E4M3(lo) . E4M3(W) with E8M0 scales per 32 K; bit 4 rounds the
+ * attention keys and bit 5 the values to BF16 (two-pass split products).
+ * Not a reference function. */
 void oracle_set_lo_emulation(unsigned mask);
 
 #ifdef __cplusplus
