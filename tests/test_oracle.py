@@ -381,3 +381,39 @@ def test_oracle_fp8_conversion_matches_artifact_codes(tmp_path):
     written = O.OracleModel(fp8_path).prefill(tokens)
     assert np.array_equal(converted.view(np.uint32), written.view(np.uint32))
     assert not np.array_equal(converted, O.OracleModel(bf16_path).prefill(tokens))
+
+
+@pytest.mark.parametrize("group", [8, 16, 24, 12])
+def test_qgmma_group_sizes_and_ragged_columns(group):
+    """The vector walk (groups a multiple of 8: eight output columns per
+    vector, ragged last column tile) and the scalar walk (other groups)
+    against the rational restatement."""
+    r = np.random.Generator(np.random.PCG64(100 + group))
+    k = 4 * group * (2 if group < 16 else 1)
+    a = r.integers(0, 256, size=(3, k)).astype(np.uint8)
+    w = r.integers(0, 256, size=(11, k)).astype(np.uint8)
+    a[(a & 0x7f) == 0x7f] = 0x41
+    w[(w & 0x7f) == 0x7f] = 0x39
+    out = O.qgmma(a, w, 0.0625, group_k=group)
+    da, dw = _decode(a), _decode(w)
+    for i in range(3):
+        for j in range(11):
+            assert out[i, j] == _qgmma_bruteforce(da[i], dw[j], 0.0625, group=group)
+
+
+def test_e4m3_quantize_bf16_table_path_equals_direct_encode():
+    """Large inputs encode through a 65536-entry table: every BF16 pattern,
+    repeated past the table threshold, gets the code of the direct encoder."""
+    L = O.lib()
+    L.oracle_e4m3_quantize_bf16.argtypes = [O.P, O.S, O.F, O.P]
+    patterns = np.arange(1 << 16, dtype=np.uint16)
+    for scale in (1.0, 448.0 / 3.1, 2.0 ** -7):
+        direct = np.zeros(patterns.size, np.uint8)
+        L.oracle_e4m3_quantize_bf16(O.ptr(patterns), patterns.size, scale, O.ptr(direct))
+        big = np.tile(patterns, 5)
+        table = np.zeros(big.size, np.uint8)
+        L.oracle_e4m3_quantize_bf16(O.ptr(big), big.size, scale, O.ptr(table))
+        assert np.array_equal(table, np.tile(direct, 5))
+        spot = [int(L.oracle_e4m3_encode(float(A.bf16_to_f32(np.array([p], np.uint16))[0])
+                                          * np.float32(scale))) for p in patterns[::4099]]
+        assert spot == list(direct[::4099])
