@@ -736,7 +736,7 @@ void linear_model(const std::vector<float> &input, size_t rows, size_t in,
 // E8M0 scale per row and 32-K block (2^ceil(log2(amax / 448)), so no block
 // saturates). q(W) is exact in BF16, so both products run as BF16-weight
 // dots. Used only to measure how such a GEMM's rounding reaches the logits.
-unsigned g_lo_emulation = 0;  // bit 0 projections, 1 out, 2 l1/l2, 3 l3; 4, 5 attention
+unsigned g_lo_emulation = 0;  // bit 0 projections, 1 out, 2 l1/l2, 3 l3; 4, 5 attention; 6 FP16 hi; 7 no lo; 8 row scales
 
 float e4m3_block_scale(const float *v, size_t n) {
   float amax = 0.0F;
@@ -751,18 +751,34 @@ float e4m3_round(const float value, const float scale) {
   return oracle_e4m3_decode(oracle_e4m3_encode(value / scale)) * scale;
 }
 
+// Bit 6: hi = FP16 of x (round to nearest even, subnormals below 2^-14,
+// saturating at 65504) instead of BF16; bit 7: no lo pass (hi only).
+float fp16_round(const float x) {
+  const float magnitude = std::fabs(x);
+  if (!(magnitude > 0.0F))
+    return x;
+  if (magnitude >= 65504.0F)
+    return std::copysign(65504.0F, x);
+  const int e = magnitude < 0x1p-14F ? -14 : static_cast<int>(std::floor(std::log2(magnitude)));
+  const float quantum = std::ldexp(1.0F, e - 10);
+  return std::nearbyint(x / quantum) * quantum;
+}
+
 const Tensor &quantized_weight(const Tensor &weight, size_t out_width, size_t in) {
-  static std::map<const uint8_t *, std::pair<std::vector<uint16_t>, Tensor>> cache;
-  auto found = cache.find(weight.data);
+  static std::map<std::pair<const uint8_t *, size_t>, std::pair<std::vector<uint16_t>, Tensor>>
+      cache;
+  const size_t width = (g_lo_emulation >> 8 & 1U) ? in : 32;
+  const auto key = std::make_pair(weight.data, width);
+  auto found = cache.find(key);
   if (found != cache.end())
     return found->second.second;
-  auto &entry = cache[weight.data];
+  auto &entry = cache[key];
   entry.first.resize(out_width * in);
 #pragma omp parallel for schedule(static)
   for (long long r = 0; r < static_cast<long long>(out_width); ++r) {
-    std::vector<float> block(32);
-    for (size_t k0 = 0; k0 < in; k0 += 32) {
-      const size_t n = std::min<size_t>(32, in - k0);
+    std::vector<float> block(width);
+    for (size_t k0 = 0; k0 < in; k0 += width) {
+      const size_t n = std::min<size_t>(width, in - k0);
       for (size_t k = 0; k < n; ++k)
         block[k] = weight.at(static_cast<size_t>(r) * in + k0 + k);
       const float scale = e4m3_block_scale(block.data(), n);
@@ -788,11 +804,14 @@ void linear_class(unsigned cls, const std::vector<float> &input, size_t rows, si
   for (long long r = 0; r < static_cast<long long>(rows); ++r) {
     const size_t base = static_cast<size_t>(r) * in;
     for (size_t k = 0; k < in; ++k) {
-      hi[base + k] = bf16_bits_to_float(float_to_bf16_rne(input[base + k]));
-      lo[base + k] = input[base + k] - hi[base + k];
+      hi[base + k] = (g_lo_emulation >> 6 & 1U) ? fp16_round(input[base + k])
+                                                 : bf16_bits_to_float(float_to_bf16_rne(input[base + k]));
+      lo[base + k] = (g_lo_emulation >> 7 & 1U) ? 0.0F : input[base + k] - hi[base + k];
     }
-    for (size_t k0 = 0; k0 < in; k0 += 32) {
-      const size_t n = std::min<size_t>(32, in - k0);
+    // Bit 8: one scale per row instead of per 32-K block.
+    const size_t block = (g_lo_emulation >> 8 & 1U) ? in : 32;
+    for (size_t k0 = 0; k0 < in; k0 += block) {
+      const size_t n = std::min<size_t>(block, in - k0);
       const float scale = e4m3_block_scale(&lo[base + k0], n);
       for (size_t k = 0; k < n; ++k)
         lo[base + k0 + k] = e4m3_round(lo[base + k0 + k], scale);

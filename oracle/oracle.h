@@ -119,8 +119,10 @@ const char *oracle_last_error(void);
 /* Design experiment (off by default): BF16-weight linears of the classes in
  * `mask` (bit 0 projections, 1 out-projection, 2 MLP l1/l2, 3 MLP l3) run as
  * hi . W + E4M3(lo) . E4M3(W) with E8M0 scales per 32 K; bit 4 rounds the
- * attention keys and bit 5 the values to BF16 (two-pass split products).
- * Not a reference function. */
+ * attention keys and bit 5 the values to BF16 (two-pass split products);
+ * bit 6 makes hi FP16 instead of BF16, bit 7 drops the lo pass, bit 8 uses
+ * one E4M3 scale per row instead of per 32-K block. Not a reference
+ * function. */
 void oracle_set_lo_emulation(unsigned mask);
 
 #ifdef __cplusplus
