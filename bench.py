@@ -36,6 +36,7 @@ from evo_hip import capi, native  # noqa: E402
 METRIC = "prefill tok/s at 1 GPU, 7B-shape @1k/8k tok; % HBM BW and % FP8 MFMA peak"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+F16_PROJ_FLAG = 1 << 11  # EVO_CONTEXT_FLAG_HIP_F16_PROJ
 FP8_PEAK_TFLOPS = 5000.0
 LIB = os.path.join(ROOT, "evo.cpp_amd", "lib", "libevo_hip.so")
 REF_LIB = os.path.join(ROOT, "oracle", "_ref", "libevo_ref.so")
@@ -346,6 +347,9 @@ def main():
     parser.add_argument("--warmup", type=int, default=2)
     parser.add_argument("--tokens", type=int, default=8192)
     parser.add_argument("--profile", choices=["f32", "bf16"], default="f32")
+    parser.add_argument("--f16-projections", action="store_true",
+                        help="out- and attention projections on one FP16 pass (the "
+                             "+f16-proj context flag) instead of split BF16")
     parser.add_argument("--artifact-dir", default="/tmp/evo_bench")
     parser.add_argument("--cpu-sample", type=int, default=16)
     parser.add_argument("--no-cpu-baseline", action="store_true")
@@ -384,7 +388,10 @@ def main():
     model = hip.load(path, capi.BACKEND_HIP, flags=1 << 8)
     params = hip.lib.evo_context_default_params()
     params.context_size = max(args.tokens, 1024)
-    params.flags = 0 if args.profile == "f32" else (1 << 8)
+    # The benchmarked context: FP8 K128 projections, every other product on
+    # split BF16 (flags 0); --f16-projections adds EVO_CONTEXT_FLAG_HIP_F16_PROJ.
+    params.flags = (0 if args.profile == "f32" else (1 << 8)) | \
+        (F16_PROJ_FLAG if args.f16_projections else 0)
     handle = ctypes.c_void_p()
     hip.check(hip.lib.evo_context_create(model.handle, ctypes.byref(params),
                                          ctypes.byref(handle)))
@@ -502,7 +509,9 @@ def main():
         "metric": METRIC, "value": round(value, 1), "unit": "tok/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 3),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "fp8-e4m3 projections + f32 (split-bf16 MFMA)" if args.profile == "f32"
+        "dtype": ("fp8-e4m3 projections + f32 (split-bf16 MFMA"
+                  + ("; fp16 out/attention projections" if args.f16_projections else "") + ")")
+                 if args.profile == "f32"
                  else "fp8-e4m3 projections + bf16 MFMA",
         "data": "synthetic (seeded random-init weights, uniform ACGT tokens)",
         "config": {"workload": f"evo2-7b-shape prefill L={args.tokens}, batch 1, "

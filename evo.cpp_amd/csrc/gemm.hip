@@ -335,7 +335,7 @@ __device__ __attribute__((always_inline)) inline void gemm_epilogue_row(
 // 2t + h the K half h, and stores its raw accumulators in tail_part for
 // gemm_tail_kernel. A launch whose last round would leave most CUs idle
 // (352 tiles on 256 CUs) thus ends in a round of half-length tiles.
-template <bool kSplit>
+template <bool kSplit, bool kF16 = false>
 __global__ __launch_bounds__(512) void gemm_kernel(
     const uint16_t *__restrict__ a_hi, const uint16_t *__restrict__ a_lo, int lda,
     const uint16_t *__restrict__ W, int ldw, int M, int N, int K, float *__restrict__ C,
@@ -444,22 +444,28 @@ __global__ __launch_bounds__(512) void gemm_kernel(
     // the longer dimension are read first; the reads of the second half
     // interleave with the MFMAs of the first (one LDS read, then a group of
     // MFMAs).
-    bf16x8 b[kNJ], ah[kMI], al[kMI];
+    // kF16: FP16 activation and weight (one pass, v_mfma_f32_16x16x32_f16).
+    using Frag = std::conditional_t<kF16, f16x8, bf16x8>;
+    Frag b[kNJ], ah[kMI], al[kMI];
     auto read_a = [&](int i) {
-      ah[i] = *reinterpret_cast<const bf16x8 *>(
+      ah[i] = *reinterpret_cast<const Frag *>(
           sa_hi + swizzled_unit(wave_m * kTM + i * 16 + r16, seg) * 8);
       if (kSplit)
-        al[i] = *reinterpret_cast<const bf16x8 *>(
+        al[i] = *reinterpret_cast<const Frag *>(
             sa_lo + swizzled_unit(wave_m * kTM + i * 16 + r16, seg) * 8);
     };
     auto read_b = [&](int j) {
-      b[j] = *reinterpret_cast<const bf16x8 *>(
+      b[j] = *reinterpret_cast<const Frag *>(
           sw + swizzled_unit(wave_n * kTN + j * 16 + r16, seg) * 8);
     };
     auto mfma = [&](int i, int j) {
-      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], b[j], acc[i][j], 0, 0, 0);
-      if (kSplit)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], b[j], acc[i][j], 0, 0, 0);
+      if constexpr (kF16) {
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], b[j], acc[i][j], 0, 0, 0);
+      } else {
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], b[j], acc[i][j], 0, 0, 0);
+        if (kSplit)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], b[j], acc[i][j], 0, 0, 0);
+      }
     };
     if constexpr (kMI >= kNJ) {
       // tall wave tile: B whole, A in two halves
@@ -740,6 +746,37 @@ __global__ __launch_bounds__(256) void gemv_kernel(
   }
 }
 
+// Split BF16 planes (hi + lo) -> one FP16 plane of their sum (RNE,
+// saturating), 8 elements per thread and step.
+__global__ void planes_to_f16_kernel(const uint16_t *__restrict__ hi,
+                                     const uint16_t *__restrict__ lo, size_t n8,
+                                     _Float16 *__restrict__ out) {
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n8;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    const uint4 h = reinterpret_cast<const uint4 *>(hi)[i];
+    const uint4 l = reinterpret_cast<const uint4 *>(lo)[i];
+    const uint32_t hw[4] = {h.x, h.y, h.z, h.w}, lw[4] = {l.x, l.y, l.z, l.w};
+    f16x8 v;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float a = __builtin_bit_cast(float, hw[q] << 16) + __builtin_bit_cast(float, lw[q] << 16);
+      const float b = __builtin_bit_cast(float, hw[q] & 0xffff0000U) +
+                      __builtin_bit_cast(float, lw[q] & 0xffff0000U);
+      v[2 * q] = static_cast<_Float16>(fminf(fmaxf(a, -65504.0F), 65504.0F));
+      v[2 * q + 1] = static_cast<_Float16>(fminf(fmaxf(b, -65504.0F), 65504.0F));
+    }
+    reinterpret_cast<f16x8 *>(out)[i] = v;
+  }
+}
+
+// BF16 -> FP16 (RNE, saturating), e.g. a weight for the FP16 product.
+__global__ void bf16_to_f16_kernel(const uint16_t *__restrict__ x, size_t n,
+                                   _Float16 *__restrict__ out) {
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x)
+    out[i] = static_cast<_Float16>(fminf(fmaxf(bf16_to_f32(x[i]), -65504.0F), 65504.0F));
+}
+
 __global__ void split_kernel(const float *__restrict__ x, size_t n,
                              uint16_t *__restrict__ hi, uint16_t *__restrict__ lo) {
   for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
@@ -815,6 +852,29 @@ __global__ void split_k_reduce_kernel(const float *__restrict__ part, int splits
 
 }  // namespace
 
+Status planes_to_f16(const uint16_t *hi, const uint16_t *lo, size_t n, uint16_t *out,
+                     hipStream_t stream) {
+  if (hi == nullptr || lo == nullptr || out == nullptr || n % 8 != 0 ||
+      reinterpret_cast<uintptr_t>(hi) % 16 != 0 || reinterpret_cast<uintptr_t>(lo) % 16 != 0 ||
+      reinterpret_cast<uintptr_t>(out) % 16 != 0)
+    return {ErrorCode::kInvalidArgument,
+            "planes_to_f16: 16-byte aligned planes of a multiple of 8 elements required"};
+  const size_t n8 = n / 8;
+  const unsigned blocks = static_cast<unsigned>(std::min<size_t>((n8 + 255) / 256, 16384));
+  hipLaunchKernelGGL(planes_to_f16_kernel, dim3(blocks), dim3(256), 0, stream, hi, lo, n8,
+                     reinterpret_cast<_Float16 *>(out));
+  return launch_status("planes_to_f16_kernel");
+}
+
+Status bf16_to_f16(const uint16_t *x, size_t n, uint16_t *out, hipStream_t stream) {
+  if (x == nullptr || out == nullptr)
+    return {ErrorCode::kInvalidArgument, "bf16_to_f16: null buffer"};
+  const unsigned blocks = static_cast<unsigned>(std::min<size_t>((n + 255) / 256, 16384));
+  hipLaunchKernelGGL(bf16_to_f16_kernel, dim3(blocks), dim3(256), 0, stream, x, n,
+                     reinterpret_cast<_Float16 *>(out));
+  return launch_status("bf16_to_f16_kernel");
+}
+
 Status split_planes(const float *x, size_t n, uint16_t *hi, uint16_t *lo,
                     hipStream_t stream) {
   if (x == nullptr || hi == nullptr || n == 0)
@@ -861,6 +921,11 @@ Status gemm_impl(const Activation &a, const RowNorm *norm, bool split, const uin
   } else if (out.f32 == nullptr || out.ld < N) {
     return {ErrorCode::kInvalidArgument, "gemm_bf16w: F32 output with ldc >= N required"};
   }
+  if (a.f16 && (norm != nullptr || split || M <= static_cast<size_t>(kGemvMaxM) ||
+                K % kBK != 0 || mode == kGemmGated))
+    return {ErrorCode::kInvalidArgument,
+            "gemm_bf16w: FP16 activations need one plane, more than 4 rows, K a multiple of 32 "
+            "and a non-gated epilogue"};
   Epilogue epi{static_cast<int>(mode), bias, residual, gelu ? 1 : 0,
                static_cast<int>(gated_width)};
   const size_t tiles = static_cast<size_t>(ceil_div(M, kBM)) * ceil_div(N, kBN);
@@ -911,6 +976,10 @@ Status gemm_impl(const Activation &a, const RowNorm *norm, bool split, const uin
         hipLaunchKernelGGL(gemm_kernel<true>, split_grid, dim3(512), 0, stream, a.hi, a.lo,
                            lda, W, k, m, n, ks, split_workspace, plane, nullptr, nullptr, n,
                            store, all, nullptr);
+      else if (a.f16)
+        hipLaunchKernelGGL((gemm_kernel<false, true>), split_grid, dim3(512), 0, stream, a.hi,
+                           a.lo, lda, W, k, m, n, ks, split_workspace, plane, nullptr, nullptr, n,
+                           store, all, nullptr);
       else
         hipLaunchKernelGGL(gemm_kernel<false>, split_grid, dim3(512), 0, stream, a.hi, a.lo,
                            lda, W, k, m, n, ks, split_workspace, plane, nullptr, nullptr, n,
@@ -946,6 +1015,10 @@ Status gemm_impl(const Activation &a, const RowNorm *norm, bool split, const uin
     if (split)
       hipLaunchKernelGGL(gemm_kernel<true>, main_grid, dim3(512), 0, stream, a.hi, a.lo, lda,
                          W, k, m, n, k, out.f32, size_t{0}, out.hi, out.lo, ldc, epi, full,
+                         split_workspace);
+    else if (a.f16)
+      hipLaunchKernelGGL((gemm_kernel<false, true>), main_grid, dim3(512), 0, stream, a.hi, a.lo,
+                         lda, W, k, m, n, k, out.f32, size_t{0}, out.hi, out.lo, ldc, epi, full,
                          split_workspace);
     else
       hipLaunchKernelGGL(gemm_kernel<false>, main_grid, dim3(512), 0, stream, a.hi, a.lo, lda,

@@ -107,6 +107,19 @@ void DeviceBuffer::reset() {
 
 // ---------------------------------------------------------------- Model load
 // Tensor set, shapes and dtypes: evo.cpp `src/cpu/model.cpp:2651-2874`.
+namespace {
+// FP16 copy of a BF16 weight for the one-pass FP16 products (widths that
+// are a multiple of 32, the tiled kernel's K step; others keep BF16 only).
+Status make_f16_copy(const DeviceBuffer &bf16, size_t count, DeviceBuffer *f16,
+                     const char *what) {
+  if (count % 32 != 0)
+    return Status::Ok();
+  EVO_TRY(f16->allocate(count * 2, what));
+  EVO_TRY(bf16_to_f16(bf16.as<uint16_t>(), count, f16->as<uint16_t>(), nullptr));
+  return hip_check(hipDeviceSynchronize(), what);
+}
+}  // namespace
+
 Status Model::load(const Artifact &a, int device, bool allow_synthetic,
                    bool fp8_projections) {
   device_ = device;
@@ -233,8 +246,10 @@ Status Model::load(const Artifact &a, int device, bool allow_synthetic,
     if (L.type == Mixer::kAttention) {
       EVO_TRY(view(a, p + ".inner_mha_cls.Wqkv.weight", {3 * w, w}, DType::kBF16, &t));
       EVO_TRY(upload_view(&L.projection, *t, p + ".Wqkv"));
+      EVO_TRY(make_f16_copy(L.projection, 3 * w * w, &L.projection16, "Wqkv FP16"));
       EVO_TRY(view(a, p + ".inner_mha_cls.out_proj.weight", {w, w}, DType::kBF16, &t));
       EVO_TRY(upload_view(&L.out_weight, *t, p + ".out_proj.weight"));
+    EVO_TRY(make_f16_copy(L.out_weight, w * w, &L.out_weight16, "out-projection FP16"));
       EVO_TRY(view(a, p + ".inner_mha_cls.out_proj.bias", {w}, DType::kBF16, &t));
       EVO_TRY(upload_view(&L.out_bias, *t, p + ".out_proj.bias"));
       EVO_TRY(view(a, p + ".inner_mha_cls.rotary_emb.inv_freq", {hd / 2}, DType::kF32, &t));
@@ -290,6 +305,7 @@ Status Model::load(const Artifact &a, int device, bool allow_synthetic,
       return {ErrorCode::kUnsupported, "unsupported: FP8 projections need width % 32 == 0"};
     EVO_TRY(view(a, p + ".out_filter_dense.weight", {w, w}, DType::kBF16, &t));
     EVO_TRY(upload_view(&L.out_weight, *t, p + ".out_filter_dense.weight"));
+    EVO_TRY(make_f16_copy(L.out_weight, w * w, &L.out_weight16, "out-projection FP16"));
     EVO_TRY(view(a, p + ".out_filter_dense.bias", {w}, DType::kBF16, &t));
     EVO_TRY(upload_view(&L.out_bias, *t, p + ".out_filter_dense.bias"));
     EVO_TRY(view(a, p + ".filter.short_filter_weight", {3 * w, 1, c.short_len}, DType::kBF16, &t));
@@ -398,6 +414,8 @@ Status Context::initialize(std::shared_ptr<const Model> model, size_t capacity,
     profile_ += "+fp8-exact";
   else if (options.fp8_mode == kFp8MfmaK32)
     profile_ += "+fp8-k32";
+  if (options.f16_proj && options.split_activations)
+    profile_ += "+f16-proj";
   EVO_TRY(hip_check(hipSetDevice(model_->device()), "select device"));
   EVO_TRY(hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "create stream"));
   const size_t R = arena_rows_, w = c.width;
@@ -520,10 +538,21 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
       EVO_TRY(rms_norm_partials(pending_, hidden, rows, w, L.pre_norm.as<float>(), c.eps,
                                 normed_hi, split ? normed_lo : nullptr, stream_));
       pending_ = SplitPartials{};
-      EVO_TRY(gemm_bf16w(hi_only_ & 1U ? Activation{normed_hi, nullptr, w} : normed,
-                         L.projection.as<uint16_t>(),
-                         GemmOutput{projected, nullptr, nullptr, 3 * w}, rows, 3 * w, w,
-                         kGemmStore, nullptr, nullptr, false, 0, stream_));
+      if (options_.f16_proj && split && L.projection16.bytes() != 0 && (rows * w) % 8 == 0) {
+        // The normed rows as one FP16 plane (in the mixer output's buffer,
+        // written only after this product) times the FP16 weight copy.
+        uint16_t *normed16 = mixed_.as<uint16_t>();
+        EVO_TRY(planes_to_f16(normed_hi, normed_lo, rows * w, normed16, stream_));
+        EVO_TRY(gemm_bf16w(Activation{normed16, nullptr, w, true},
+                           L.projection16.as<uint16_t>(),
+                           GemmOutput{projected, nullptr, nullptr, 3 * w}, rows, 3 * w, w,
+                           kGemmStore, nullptr, nullptr, false, 0, stream_));
+      } else {
+        EVO_TRY(gemm_bf16w(hi_only_ & 1U ? Activation{normed_hi, nullptr, w} : normed,
+                           L.projection.as<uint16_t>(),
+                           GemmOutput{projected, nullptr, nullptr, 3 * w}, rows, 3 * w, w,
+                           kGemmStore, nullptr, nullptr, false, 0, stream_));
+      }
     }
     EVO_TRY(workspace_free("the mixer"));
     if (L.type == Mixer::kAttention) {
@@ -570,12 +599,25 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
     // Short chunks split K here; the post-mixer norm then sums the partials
     // (with bias and hidden) into residual as it reads them.
     SplitPartials out_partials;
-    EVO_TRY(gemm_bf16w(hi_only_ & 2U ? Activation{mixed_hi, nullptr, w} : mixed,
-                       L.out_weight.as<uint16_t>(),
-                       GemmOutput{residual, nullptr, nullptr, w}, rows, w, w,
-                       kGemmBiasResidual, L.out_bias.as<uint16_t>(), hidden, false, 0,
-                       stream_, workspace_.as<float>(), workspace_.bytes(),
-                       fold ? nullptr : &out_partials));
+    // "+f16-proj": the mixer output as one FP16 plane (in the projection's
+    // buffer, free after the mixer) times the FP16 copy of the weight.
+    const bool f16_out = options_.f16_proj && split && !fold &&
+                         L.out_weight16.bytes() != 0 && (rows * w) % 8 == 0;
+    if (f16_out) {
+      uint16_t *mixed16 = projected_.as<uint16_t>();
+      EVO_TRY(planes_to_f16(mixed_hi, mixed_lo, rows * w, mixed16, stream_));
+      EVO_TRY(gemm_bf16w(Activation{mixed16, nullptr, w, true}, L.out_weight16.as<uint16_t>(),
+                         GemmOutput{residual, nullptr, nullptr, w}, rows, w, w,
+                         kGemmBiasResidual, L.out_bias.as<uint16_t>(), hidden, false, 0,
+                         stream_, workspace_.as<float>(), workspace_.bytes(), &out_partials));
+    } else {
+      EVO_TRY(gemm_bf16w(hi_only_ & 2U ? Activation{mixed_hi, nullptr, w} : mixed,
+                         L.out_weight.as<uint16_t>(),
+                         GemmOutput{residual, nullptr, nullptr, w}, rows, w, w,
+                         kGemmBiasResidual, L.out_bias.as<uint16_t>(), hidden, false, 0,
+                         stream_, workspace_.as<float>(), workspace_.bytes(),
+                         fold ? nullptr : &out_partials));
+    }
     // gated = act(l1 x) * (l2 x), act = erf-GELU in block 0 only (`:650-667`).
     // This norm stays a kernel of its own for few rows too: folded into the
     // l1/l2 product, each of its N/8 blocks (2816 at 7B) normalises the row

@@ -62,6 +62,8 @@ struct Layer {
   bool fp8{false};
   float fp8_input_scale{0}, fp8_output_scale{0};
   DeviceBuffer out_weight, out_bias;       // BF16 [W, W], [W]
+  DeviceBuffer out_weight16;               // FP16 copy of out_weight (W % 32 == 0)
+  DeviceBuffer projection16;               // FP16 copy of an attention Wqkv
   DeviceBuffer short_filter;               // BF16 [3W, short_len]
   DeviceBuffer inner_filter;               // F32 [groups, len]
   DeviceBuffer direct;                     // F32 [W]
@@ -101,6 +103,7 @@ private:
 
 struct ContextOptions {
   bool split_activations{true};   // "hip-f32" (true) or "hip-bf16" (false)
+  bool f16_proj{false};  // out- and attention projections on one FP16 pass ("+f16-proj")
   Fp8Mode fp8_mode{kFp8MfmaK128};
 };
 

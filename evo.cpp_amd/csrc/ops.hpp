@@ -34,6 +34,7 @@ struct Activation {
   const uint16_t *hi;
   const uint16_t *lo;
   size_t ld;
+  bool f16 = false;  // hi holds FP16 bits (lo null) and W is FP16
 };
 // GEMM output: F32 (store/bias/residual modes) or split planes (gated mode,
 // lo may be null), row stride ld elements.
@@ -86,6 +87,11 @@ Status gemm_bf16w_normed(const RowNorm &norm, bool split, const uint16_t *W,
                          GemmEpilogue mode, const uint16_t *bias, const float *residual,
                          bool gelu, size_t gated_width, hipStream_t stream);
 // hi[i] = bf16(x[i]), lo[i] = bf16(x[i] - hi[i]) (lo may be null).
+// hi + lo (split BF16 planes) -> FP16 bits (RNE, saturating at 65504).
+Status planes_to_f16(const uint16_t *hi, const uint16_t *lo, size_t n, uint16_t *out,
+                     hipStream_t stream);
+// BF16 -> FP16 bits (RNE, saturating), e.g. a weight for FP16 products.
+Status bf16_to_f16(const uint16_t *x, size_t n, uint16_t *out, hipStream_t stream);
 Status split_planes(const float *x, size_t n, uint16_t *hi, uint16_t *lo,
                     hipStream_t stream);
 

@@ -84,7 +84,13 @@ enum {
   EVO_CONTEXT_FLAG_HIP_FP8_EXACT = 1u << 9u,
   /* E4M3 MFMA path promoting every 32-K chunk (the reference's QGMMA group
    * size) instead of every 128 K ("+fp8-k32"); exclusive with FP8_EXACT. */
-  EVO_CONTEXT_FLAG_HIP_FP8_K32 = 1u << 10u
+  EVO_CONTEXT_FLAG_HIP_FP8_K32 = 1u << 10u,
+  /* "+f16-proj": the out-projections (mixer output times out_proj /
+   * out_filter_dense) and the attention input projections (Wqkv) run as one
+   * FP16 MFMA pass (activation rounded to FP16, weight converted to FP16 at
+   * load) instead of two split-BF16 passes. The MLP products and the FP8
+   * Hyena projections are unchanged. */
+  EVO_CONTEXT_FLAG_HIP_F16_PROJ = 1u << 11u
 };
 
 typedef struct evo_model evo_model;

@@ -157,6 +157,40 @@ def test_evo2_1b_shape_config1(hip, tmp_path, init):
     assert np.array_equal(actual.argmax(1), expected.argmax(1))
 
 
+F16_PROJ = 1 << 11  # EVO_CONTEXT_FLAG_HIP_F16_PROJ
+
+
+@pytest.mark.parametrize("init", ["survey", "unit"])
+def test_f16_projection_profile_config1(hip, tmp_path, init):
+    """"+f16-proj": out- and attention projections on one FP16 pass (the
+    mixer output and the attention block's normed input rounded to FP16,
+    weights converted to FP16 at load) on the 1B shape, 128 tokens, against
+    the oracle: logits within 1e-3 of their scale, top-1 100 %."""
+    shape = A.evo2_1b_shape()
+    path = make(tmp_path, shape, seed=1, init=init)
+    tokens = A.acgt_tokens(128, seed=1)
+    expected = O.OracleModel(path).prefill(tokens, threads=16)
+    actual, profile = run_hip(hip, path, tokens, flags=F16_PROJ)
+    assert profile == "hip-f32+f16-proj"
+    print(f"f16-proj config 1 ({init}): relmax {relmax(actual, expected):.3g}")
+    assert relmax(actual, expected) <= TOL
+    assert np.array_equal(actual.argmax(1), expected.argmax(1))
+
+
+@pytest.mark.parametrize("length,arena", [(300, 64), (200, None)])
+def test_f16_projection_profile_tiny_chunks(hip, tmp_path, length, arena):
+    """The FP16 products through the split-K paths of short chunks (partials
+    summed by the next RMSNorm) and through whole chunks."""
+    shape = A.tiny_shape(width=64, layers=8, heads=2, inner=96, groups=16, attn=(3,))
+    path = make(tmp_path, shape, seed=13)
+    tokens = A.acgt_tokens(length, seed=length)
+    expected = O.OracleModel(path).prefill(tokens)
+    actual, profile = run_hip(hip, path, tokens, flags=F16_PROJ, arena=arena)
+    assert profile == "hip-f32+f16-proj"
+    assert relmax(actual, expected) <= TOL
+    assert np.array_equal(actual.argmax(1), expected.argmax(1))
+
+
 def open_context(hip, path, capacity, flags=0):
     import ctypes
     model = hip.load(path, capi.BACKEND_HIP)
