@@ -210,15 +210,6 @@ __global__ __launch_bounds__(kWaves * 64, 2) void fp8_mfma_kernel(
 #pragma unroll
       for (int e = 0; e < 16; ++e)
         acc[i][j][e] = 0.0F;
-  auto truncate_all = [&]() {
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 3; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e)
-          acc[i][j][e] = truncate_e8m13(acc[i][j][e]);
-  };
   auto frag32 = [&](const uint8_t *base, int row, int unit) {
     const uint4 lo = *reinterpret_cast<const uint4 *>(base + fp8_unit(row, unit) * 16);
     const uint4 hi = *reinterpret_cast<const uint4 *>(base + fp8_unit(row, unit + 1) * 16);
@@ -279,34 +270,66 @@ __global__ __launch_bounds__(kWaves * 64, 2) void fp8_mfma_kernel(
       for (int e = 0; e < 16; ++e)
         acc[1][2][e] = truncate_e8m13(acc[1][2][e]);
     } else {
-      if (s + 1 < steps)
-        issue(s + 1);
-      // Four 32-K chunks, each two K=16 MFMAs then a promotion.
+      // Four 32-K chunks, each two K=16 MFMAs per tile then a promotion.
+      // A tile's promotion is issued right behind the next tile's second
+      // MFMA, so the truncations run under the matrix core's work instead
+      // of after it; the last tile's promotion waits until just before its
+      // first MFMA of the next chunk (same values: each truncation still
+      // sits between the chunk that produced it and the next one).
 #pragma unroll
       for (int c = 0; c < kBK / 32; ++c) {
+        long bv[2][3], av[2][2];
 #pragma unroll
-        for (int ks = 2 * c; ks < 2 * c + 2; ++ks) {
-          long bv[3], av[2];
+        for (int h = 0; h < 2; ++h) {
 #pragma unroll
           for (int j = 0; j < 3; ++j) {
             const int row = wave_n * 96 + j * 32 + col;
-            bv[j] = *reinterpret_cast<const long *>(w_s + fp8_unit(row, ks) * 16 + half * 8);
+            bv[h][j] =
+                *reinterpret_cast<const long *>(w_s + fp8_unit(row, 2 * c + h) * 16 + half * 8);
           }
 #pragma unroll
           for (int i = 0; i < 2; ++i) {
             const int row = wave_m * 64 + i * 32 + col;
-            av[i] = *reinterpret_cast<const long *>(a_s + fp8_unit(row, ks) * 16 + half * 8);
+            av[h][i] =
+                *reinterpret_cast<const long *>(a_s + fp8_unit(row, 2 * c + h) * 16 + half * 8);
           }
-#pragma unroll
-          for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 3; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(av[i], bv[j], acc[i][j],
-                                                                     0, 0, 0);
         }
-        truncate_all();
+#pragma unroll
+        for (int t = 0; t < 6; ++t) {
+          if (t == 5) {  // truncating the initial zeros is harmless
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+              acc[1][2][e] = truncate_e8m13(acc[1][2][e]);
+          }
+          acc[t / 3][t % 3] = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(
+              av[0][t / 3], bv[0][t % 3], acc[t / 3][t % 3], 0, 0, 0);
+        }
+        if (c == 0) {
+          // The next step's DMA goes out under the first chunk's MFMAs.
+          __builtin_amdgcn_sched_barrier(0);
+          if (s + 1 < steps)
+            issue(s + 1);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int t = 0; t < 6; ++t) {
+          acc[t / 3][t % 3] = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(
+              av[1][t / 3], bv[1][t % 3], acc[t / 3][t % 3], 0, 0, 0);
+          if (t > 0) {
+            const int pi = (t - 1) / 3, pj = (t - 1) % 3;
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+              acc[pi][pj][e] = truncate_e8m13(acc[pi][pj][e]);
+          }
+        }
       }
     }
+  }
+  if constexpr (kChunk == 32) {
+    // The last chunk's deferred promotion of the last tile.
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      acc[1][2][e] = truncate_e8m13(acc[1][2][e]);
   }
   if constexpr (std::is_same<Out, uint16_t>::value) {
     if (N % 2 == 0 && reinterpret_cast<uintptr_t>(out) % 4 == 0) {
