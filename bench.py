@@ -37,6 +37,7 @@ METRIC = "prefill tok/s at 1 GPU, 7B-shape @1k/8k tok; % HBM BW and % FP8 MFMA p
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 F16_PROJ_FLAG = 1 << 11  # EVO_CONTEXT_FLAG_HIP_F16_PROJ
+F16_OUT_FLAG = 1 << 12   # EVO_CONTEXT_FLAG_HIP_F16_OUT
 FP8_PEAK_TFLOPS = 5000.0
 LIB = os.path.join(ROOT, "evo.cpp_amd", "lib", "libevo_hip.so")
 REF_LIB = os.path.join(ROOT, "oracle", "_ref", "libevo_ref.so")
@@ -350,6 +351,9 @@ def main():
     parser.add_argument("--f16-projections", action="store_true",
                         help="out- and attention projections on one FP16 pass (the "
                              "+f16-proj context flag) instead of split BF16")
+    parser.add_argument("--split-out", action="store_true",
+                        help="out-projections on split BF16 too (context without the "
+                             "+f16-out flag: every product except the FP8 ones split BF16)")
     parser.add_argument("--artifact-dir", default="/tmp/evo_bench")
     parser.add_argument("--cpu-sample", type=int, default=16)
     parser.add_argument("--no-cpu-baseline", action="store_true")
@@ -388,10 +392,13 @@ def main():
     model = hip.load(path, capi.BACKEND_HIP, flags=1 << 8)
     params = hip.lib.evo_context_default_params()
     params.context_size = max(args.tokens, 1024)
-    # The benchmarked context: FP8 K128 projections, every other product on
-    # split BF16 (flags 0); --f16-projections adds EVO_CONTEXT_FLAG_HIP_F16_PROJ.
+    # The benchmarked context: FP8 K128 Hyena projections, out-projections on
+    # one FP16 pass (EVO_CONTEXT_FLAG_HIP_F16_OUT: logits within 1.9e-4 of the
+    # oracle, top-1 100 %), every other product split BF16. --split-out drops
+    # the flag; --f16-projections adds the attention projections.
+    f16_out = args.profile == "f32" and not args.split_out
     params.flags = (0 if args.profile == "f32" else (1 << 8)) | \
-        (F16_PROJ_FLAG if args.f16_projections else 0)
+        (F16_PROJ_FLAG if args.f16_projections else 0) | (F16_OUT_FLAG if f16_out else 0)
     handle = ctypes.c_void_p()
     hip.check(hip.lib.evo_context_create(model.handle, ctypes.byref(params),
                                          ctypes.byref(handle)))
@@ -510,7 +517,8 @@ def main():
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 3),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": ("fp8-e4m3 projections + f32 (split-bf16 MFMA"
-                  + ("; fp16 out/attention projections" if args.f16_projections else "") + ")")
+                  + ("; fp16 out/attention projections" if args.f16_projections
+                     else "; fp16 out-projections" if f16_out else "") + ")")
                  if args.profile == "f32"
                  else "fp8-e4m3 projections + bf16 MFMA",
         "data": "synthetic (seeded random-init weights, uniform ACGT tokens)",

@@ -325,7 +325,8 @@ evo_status evo_context_create(const evo_model *model, const evo_context_params *
                      "invalid_argument: evo_context_params is too small");
     const evo_context_params options = params == nullptr ? evo_context_default_params() : *params;
     const uint32_t known = EVO_CONTEXT_FLAG_HIP_BF16 | EVO_CONTEXT_FLAG_HIP_FP8_EXACT |
-                           EVO_CONTEXT_FLAG_HIP_FP8_K32 | EVO_CONTEXT_FLAG_HIP_F16_PROJ;
+                           EVO_CONTEXT_FLAG_HIP_FP8_K32 | EVO_CONTEXT_FLAG_HIP_F16_PROJ |
+                           EVO_CONTEXT_FLAG_HIP_F16_OUT;
     const uint32_t fp8_modes = EVO_CONTEXT_FLAG_HIP_FP8_EXACT | EVO_CONTEXT_FLAG_HIP_FP8_K32;
     if (options.context_size == 0 || (options.flags & ~known) != 0 ||
         (options.flags & fp8_modes) == fp8_modes)
@@ -338,6 +339,7 @@ evo_status evo_context_create(const evo_model *model, const evo_context_params *
     evo::hip::ContextOptions hip_options;
     hip_options.split_activations = (options.flags & EVO_CONTEXT_FLAG_HIP_BF16) == 0;
     hip_options.f16_proj = (options.flags & EVO_CONTEXT_FLAG_HIP_F16_PROJ) != 0;
+    hip_options.f16_out = (options.flags & EVO_CONTEXT_FLAG_HIP_F16_OUT) != 0;
     hip_options.fp8_mode = (options.flags & EVO_CONTEXT_FLAG_HIP_FP8_EXACT) != 0
                                ? evo::hip::kFp8Exact
                            : (options.flags & EVO_CONTEXT_FLAG_HIP_FP8_K32) != 0

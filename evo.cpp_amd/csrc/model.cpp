@@ -249,7 +249,7 @@ Status Model::load(const Artifact &a, int device, bool allow_synthetic,
       EVO_TRY(make_f16_copy(L.projection, 3 * w * w, &L.projection16, "Wqkv FP16"));
       EVO_TRY(view(a, p + ".inner_mha_cls.out_proj.weight", {w, w}, DType::kBF16, &t));
       EVO_TRY(upload_view(&L.out_weight, *t, p + ".out_proj.weight"));
-    EVO_TRY(make_f16_copy(L.out_weight, w * w, &L.out_weight16, "out-projection FP16"));
+      EVO_TRY(make_f16_copy(L.out_weight, w * w, &L.out_weight16, "out-projection FP16"));
       EVO_TRY(view(a, p + ".inner_mha_cls.out_proj.bias", {w}, DType::kBF16, &t));
       EVO_TRY(upload_view(&L.out_bias, *t, p + ".out_proj.bias"));
       EVO_TRY(view(a, p + ".inner_mha_cls.rotary_emb.inv_freq", {hd / 2}, DType::kF32, &t));
@@ -416,6 +416,8 @@ Status Context::initialize(std::shared_ptr<const Model> model, size_t capacity,
     profile_ += "+fp8-k32";
   if (options.f16_proj && options.split_activations)
     profile_ += "+f16-proj";
+  else if (options.f16_out && options.split_activations)
+    profile_ += "+f16-out";
   EVO_TRY(hip_check(hipSetDevice(model_->device()), "select device"));
   EVO_TRY(hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "create stream"));
   const size_t R = arena_rows_, w = c.width;
@@ -599,9 +601,10 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
     // Short chunks split K here; the post-mixer norm then sums the partials
     // (with bias and hidden) into residual as it reads them.
     SplitPartials out_partials;
-    // "+f16-proj": the mixer output as one FP16 plane (in the projection's
-    // buffer, free after the mixer) times the FP16 copy of the weight.
-    const bool f16_out = options_.f16_proj && split && !fold &&
+    // "+f16-out" / "+f16-proj": the mixer output as one FP16 plane (in the
+    // projection's buffer, free after the mixer; saturating at +-65504) times
+    // the FP16 copy of the weight.
+    const bool f16_out = (options_.f16_proj || options_.f16_out) && split && !fold &&
                          L.out_weight16.bytes() != 0 && (rows * w) % 8 == 0;
     if (f16_out) {
       uint16_t *mixed16 = projected_.as<uint16_t>();

@@ -104,6 +104,7 @@ private:
 struct ContextOptions {
   bool split_activations{true};   // "hip-f32" (true) or "hip-bf16" (false)
   bool f16_proj{false};  // out- and attention projections on one FP16 pass ("+f16-proj")
+  bool f16_out{false};   // out-projections only on one FP16 pass ("+f16-out")
   Fp8Mode fp8_mode{kFp8MfmaK128};
 };
 

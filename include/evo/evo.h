@@ -90,7 +90,10 @@ enum {
    * FP16 MFMA pass (activation rounded to FP16, weight converted to FP16 at
    * load) instead of two split-BF16 passes. The MLP products and the FP8
    * Hyena projections are unchanged. */
-  EVO_CONTEXT_FLAG_HIP_F16_PROJ = 1u << 11u
+  EVO_CONTEXT_FLAG_HIP_F16_PROJ = 1u << 11u,
+  /* "+f16-out": only the out-projections run as one FP16 MFMA pass (the
+   * attention input projections stay split BF16); implied by F16_PROJ. */
+  EVO_CONTEXT_FLAG_HIP_F16_OUT = 1u << 12u
 };
 
 typedef struct evo_model evo_model;

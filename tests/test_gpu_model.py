@@ -158,35 +158,41 @@ def test_evo2_1b_shape_config1(hip, tmp_path, init):
 
 
 F16_PROJ = 1 << 11  # EVO_CONTEXT_FLAG_HIP_F16_PROJ
+F16_OUT = 1 << 12   # EVO_CONTEXT_FLAG_HIP_F16_OUT
+F16_PROFILES = [pytest.param(F16_PROJ, "hip-f32+f16-proj", id="f16-proj"),
+                pytest.param(F16_OUT, "hip-f32+f16-out", id="f16-out")]
 
 
+@pytest.mark.parametrize("flags,name", F16_PROFILES)
 @pytest.mark.parametrize("init", ["survey", "unit"])
-def test_f16_projection_profile_config1(hip, tmp_path, init):
+def test_f16_projection_profile_config1(hip, tmp_path, init, flags, name):
     """"+f16-proj": out- and attention projections on one FP16 pass (the
     mixer output and the attention block's normed input rounded to FP16,
-    weights converted to FP16 at load) on the 1B shape, 128 tokens, against
-    the oracle: logits within 1e-3 of their scale, top-1 100 %."""
+    weights converted to FP16 at load); "+f16-out": the out-projections
+    only. 1B shape, 128 tokens, against the oracle: logits within 1e-3 of
+    their scale, top-1 100 %."""
     shape = A.evo2_1b_shape()
     path = make(tmp_path, shape, seed=1, init=init)
     tokens = A.acgt_tokens(128, seed=1)
     expected = O.OracleModel(path).prefill(tokens, threads=16)
-    actual, profile = run_hip(hip, path, tokens, flags=F16_PROJ)
-    assert profile == "hip-f32+f16-proj"
-    print(f"f16-proj config 1 ({init}): relmax {relmax(actual, expected):.3g}")
+    actual, profile = run_hip(hip, path, tokens, flags=flags)
+    assert profile == name
+    print(f"{name} config 1 ({init}): relmax {relmax(actual, expected):.3g}")
     assert relmax(actual, expected) <= TOL
     assert np.array_equal(actual.argmax(1), expected.argmax(1))
 
 
+@pytest.mark.parametrize("flags,name", F16_PROFILES)
 @pytest.mark.parametrize("length,arena", [(300, 64), (200, None)])
-def test_f16_projection_profile_tiny_chunks(hip, tmp_path, length, arena):
+def test_f16_projection_profile_tiny_chunks(hip, tmp_path, length, arena, flags, name):
     """The FP16 products through the split-K paths of short chunks (partials
     summed by the next RMSNorm) and through whole chunks."""
     shape = A.tiny_shape(width=64, layers=8, heads=2, inner=96, groups=16, attn=(3,))
     path = make(tmp_path, shape, seed=13)
     tokens = A.acgt_tokens(length, seed=length)
     expected = O.OracleModel(path).prefill(tokens)
-    actual, profile = run_hip(hip, path, tokens, flags=F16_PROJ, arena=arena)
-    assert profile == "hip-f32+f16-proj"
+    actual, profile = run_hip(hip, path, tokens, flags=flags, arena=arena)
+    assert profile == name
     assert relmax(actual, expected) <= TOL
     assert np.array_equal(actual.argmax(1), expected.argmax(1))
 
