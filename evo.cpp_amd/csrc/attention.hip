@@ -630,7 +630,8 @@ Status causal_attention(const uint16_t *q, size_t q_plane, const uint16_t *k_cac
                         const uint16_t *v_cache, size_t cache_plane, size_t capacity,
                         size_t rows, size_t prefix, size_t heads, size_t head_dim,
                         float *out_f32, uint16_t *out_hi, uint16_t *out_lo,
-                        hipStream_t stream, float *workspace, size_t workspace_bytes) {
+                        hipStream_t stream, float *workspace, size_t workspace_bytes,
+                        bool out_f16) {
   if (q == nullptr || k_cache == nullptr || v_cache == nullptr ||
       (out_f32 == nullptr && out_hi == nullptr) || rows == 0 || heads == 0 ||
       heads > 65535 || q_plane < rows * heads * head_dim || capacity % kKeys != 0 ||
@@ -656,11 +657,16 @@ Status causal_attention(const uint16_t *q, size_t q_plane, const uint16_t *k_cac
     };
     if (out_f32 != nullptr)
       return run(out_f32);
+    if (out_f16)
+      return run(F16Out{out_hi});
     return run(SplitOut{out_hi, out_lo});
   }
   if (out_f32 != nullptr)
     return launch_attention(q, q_plane, k_cache, v_cache, cache_plane, capacity, rows, prefix,
                             heads, head_dim, out_f32, stream);
+  if (out_f16)
+    return launch_attention(q, q_plane, k_cache, v_cache, cache_plane, capacity, rows, prefix,
+                            heads, head_dim, F16Out{out_hi}, stream);
   return launch_attention(q, q_plane, k_cache, v_cache, cache_plane, capacity, rows, prefix,
                           heads, head_dim, SplitOut{out_hi, out_lo}, stream);
 }

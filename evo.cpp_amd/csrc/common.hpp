@@ -162,6 +162,11 @@ __device__ inline void put(const SplitOut &out, size_t i, float v) {
     out.lo[i] = f32_to_bf16(v - bf16_to_f32(hi));
 }
 
+__device__ inline uint16_t f32_to_f16_sat(const float v) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(fminf(fmaxf(v, -65504.0F), 65504.0F)));
+}
+__device__ inline void put(const F16Out &out, size_t i, float v) { out.out[i] = f32_to_f16_sat(v); }
+
 // Non-temporal variants for outputs no later part of the producing kernel
 // reads: the stores stream past the L2 instead of evicting its input lines.
 __device__ inline void put_nt(float *out, size_t i, float v) {
@@ -169,6 +174,9 @@ __device__ inline void put_nt(float *out, size_t i, float v) {
 }
 __device__ inline void put_nt(uint16_t *out, size_t i, float v) {
   __builtin_nontemporal_store(f32_to_bf16(v), out + i);
+}
+__device__ inline void put_nt(const F16Out &out, size_t i, float v) {
+  __builtin_nontemporal_store(f32_to_f16_sat(v), out.out + i);
 }
 __device__ inline void put_nt(const SplitOut &out, size_t i, float v) {
   const uint16_t hi = f32_to_bf16(v);

@@ -411,6 +411,22 @@ __device__ inline uint32_t pack_bf16(float a, float b) {
   const f32x2 v = {a, b};
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+// {fp16(a), fp16(b)}, round to nearest even, saturated to +-65504.
+__device__ inline uint32_t pack_f16(float a, float b) {
+  const f32x2 v = {fminf(fmaxf(a, -65504.0F), 65504.0F), fminf(fmaxf(b, -65504.0F), 65504.0F)};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+}
+// One 16-bit plane: BF16 (uint16_t *) or FP16 (F16Out).
+template <typename O> struct Plane16;
+template <> struct Plane16<uint16_t *> {
+  static __device__ uint16_t *ptr(uint16_t *o) { return o; }
+  static __device__ uint32_t pack(float a, float b) { return pack_bf16(a, b); }
+};
+template <> struct Plane16<F16Out> {
+  static __device__ uint16_t *ptr(const F16Out &o) { return o.out; }
+  static __device__ uint32_t pack(float a, float b) { return pack_f16(a, b); }
+};
 
 // Output of a channel pair through segment-bounded buffer resources:
 // `lane` is the pair's byte offset within a row of one plane, `row` the
@@ -430,15 +446,21 @@ template <> struct PairOut<float *> {
                                           static_cast<int>(2 * (lane + row) + 4), 0, kStreamStore);
   }
 };
-template <> struct PairOut<uint16_t *> {
+template <typename O> struct PairOut16 {
   __amdgpu_buffer_rsrc_t out;
-  __device__ PairOut(uint16_t *o, size_t first, size_t rows, size_t W) {
-    out = buffer_resource(o + first * W, static_cast<uint32_t>(rows * W * 2));
+  __device__ PairOut16(const O &o, size_t first, size_t rows, size_t W) {
+    out = buffer_resource(Plane16<O>::ptr(o) + first * W, static_cast<uint32_t>(rows * W * 2));
   }
   __device__ void put(uint32_t lane, uint32_t row, float a, float b) const {
-    __builtin_amdgcn_raw_buffer_store_b32(pack_bf16(a, b), out, static_cast<int>(lane + row), 0,
-                                          kStreamStore);
+    __builtin_amdgcn_raw_buffer_store_b32(Plane16<O>::pack(a, b), out,
+                                          static_cast<int>(lane + row), 0, kStreamStore);
   }
+};
+template <> struct PairOut<uint16_t *> : PairOut16<uint16_t *> {
+  using PairOut16<uint16_t *>::PairOut16;
+};
+template <> struct PairOut<F16Out> : PairOut16<F16Out> {
+  using PairOut16<F16Out>::PairOut16;
 };
 template <> struct PairOut<SplitOut> {
   __amdgpu_buffer_rsrc_t hi, lo;
@@ -1080,19 +1102,25 @@ template <> struct HalfOut<float *> {
     put(half, lane, row + row_bytes, a1, b1);
   }
 };
-template <> struct HalfOut<uint16_t *> {
+template <typename O> struct HalfOut16 {
   __amdgpu_buffer_rsrc_t out;
-  __device__ HalfOut(uint16_t *o, size_t first, size_t rows, size_t W) {
-    out = buffer_resource(o + first * W, static_cast<uint32_t>(rows * W * 2));
+  __device__ HalfOut16(const O &o, size_t first, size_t rows, size_t W) {
+    out = buffer_resource(Plane16<O>::ptr(o) + first * W, static_cast<uint32_t>(rows * W * 2));
   }
   __device__ void put_rows(int half, uint32_t lane, uint32_t row, uint32_t row_bytes, float a0,
                            float b0, float a1, float b1) const {
     // Even lane row `row`, odd lane the next one.
-    const uint32_t word = half == 0 ? pack_bf16(a0, b0) : pack_bf16(a1, b1);
+    const uint32_t word = half == 0 ? Plane16<O>::pack(a0, b0) : Plane16<O>::pack(a1, b1);
     __builtin_amdgcn_raw_buffer_store_b32(word, out,
                                           static_cast<int>(lane + row + half * row_bytes), 0,
                                           kStreamStore);
   }
+};
+template <> struct HalfOut<uint16_t *> : HalfOut16<uint16_t *> {
+  using HalfOut16<uint16_t *>::HalfOut16;
+};
+template <> struct HalfOut<F16Out> : HalfOut16<F16Out> {
+  using HalfOut16<F16Out>::HalfOut16;
 };
 template <> struct HalfOut<SplitOut> {
   // Both resources are uniform; a missing lo plane gets an empty one (its
@@ -1266,17 +1294,19 @@ template <> struct MsOut<float *> {
     store16_nt(out + index + 4, src + 4);
   }
 };
-template <> struct MsOut<uint16_t *> {
-  __device__ static void flush(const float *src, uint16_t *out, size_t index) {
+template <typename O> struct MsOut16 {
+  __device__ static void flush(const float *src, const O &out, size_t index) {
     float v[8];
     load8(src, v);
     uint32_t w[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      w[i] = pack_bf16(v[2 * i], v[2 * i + 1]);
-    store16_words(out + index, w);
+      w[i] = Plane16<O>::pack(v[2 * i], v[2 * i + 1]);
+    store16_words(Plane16<O>::ptr(out) + index, w);
   }
 };
+template <> struct MsOut<uint16_t *> : MsOut16<uint16_t *> {};
+template <> struct MsOut<F16Out> : MsOut16<F16Out> {};
 template <> struct MsOut<SplitOut> {
   __device__ static void flush(const float *src, const SplitOut &out, size_t index) {
     float v[8];
@@ -1824,16 +1854,18 @@ template <> struct HmOut<float *> {
     *reinterpret_cast<f32x4 *>(out + index + 4) = f32x4{v[4], v[5], v[6], v[7]};
   }
 };
-template <> struct HmOut<uint16_t *> {
-  __device__ static int stores(uint16_t *) { return 1; }
-  __device__ static void put(const float (&v)[8], uint16_t *out, size_t index) {
+template <typename O> struct HmOut16 {
+  __device__ static int stores(const O &) { return 1; }
+  __device__ static void put(const float (&v)[8], const O &out, size_t index) {
     u32x4 w;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      w[i] = pack_bf16(v[2 * i], v[2 * i + 1]);
-    *reinterpret_cast<u32x4 *>(out + index) = w;
+      w[i] = Plane16<O>::pack(v[2 * i], v[2 * i + 1]);
+    *reinterpret_cast<u32x4 *>(Plane16<O>::ptr(out) + index) = w;
   }
 };
+template <> struct HmOut<uint16_t *> : HmOut16<uint16_t *> {};
+template <> struct HmOut<F16Out> : HmOut16<F16Out> {};
 template <> struct HmOut<SplitOut> {
   __device__ static int stores(const SplitOut &out) { return out.lo != nullptr ? 2 : 1; }
   __device__ static void put(const float (&v)[8], const SplitOut &out, size_t index) {
@@ -2877,6 +2909,14 @@ template Status hyena_forward<float, SplitOut>(int, const float *, size_t, size_
                                                const HyenaWeights &, float *, float *,
                                                float *, void *, size_t, SplitOut,
                                                hipStream_t);
+template Status hyena_forward<uint16_t, F16Out>(int, const uint16_t *, size_t, size_t, bool,
+                                                const HyenaWeights &, float *, float *,
+                                                float *, void *, size_t, F16Out,
+                                                hipStream_t);
+template Status hyena_forward<float, F16Out>(int, const float *, size_t, size_t, bool,
+                                             const HyenaWeights &, float *, float *,
+                                             float *, void *, size_t, F16Out,
+                                             hipStream_t);
 
 // ---- Fixed scratch of the allocation-free operator entry point.
 // One array per device, alive until the process ends. Its host-side name is

@@ -557,6 +557,10 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
       }
     }
     EVO_TRY(workspace_free("the mixer"));
+    // "+f16-out" / "+f16-proj": the mixer writes its output as one FP16 plane
+    // (fp16(v), saturating at +-65504) for the FP16 copy of the out-projection.
+    const bool f16_out = (options_.f16_proj || options_.f16_out) && split && !fold &&
+                         L.out_weight16.bytes() != 0;
     if (L.type == Mixer::kAttention) {
       uint16_t *query = query_.as<uint16_t>();
       const size_t cache_plane = cache_capacity_ * w;
@@ -567,7 +571,7 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
                                k.values.as<uint16_t>(), cache_plane, cache_capacity_, rows,
                                position_,
                                c.heads, c.head_dim(), nullptr, mixed_out.hi, mixed_out.lo,
-                               stream_, workspace_.as<float>(), workspace_.bytes()));
+                               stream_, workspace_.as<float>(), workspace_.bytes(), f16_out));
     } else {
       HyenaWeights hw{};
       hw.short_filter = L.short_filter.as<uint16_t>();
@@ -582,34 +586,31 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
       hw.taps_bf16 = true;  // `.filter.h` is BF16 in the artifact
       const int kind = L.type == Mixer::kHcs ? kHyenaHcs
                        : L.type == Mixer::kHcm ? kHyenaHcm : kHyenaHcl;
-      if (L.fp8)
-        EVO_TRY((hyena_forward<uint16_t, SplitOut>(kind, projected_.as<uint16_t>(), rows, w,
-                                                   false, hw, k.short_history.as<float>(),
-                                                   k.inner_history.as<float>(),
-                                                   k.modal_state.as<float>(),
-                                                   workspace_.as<void>(), workspace_.bytes(),
-                                                   mixed_out, stream_)));
+      auto mixer = [&](auto out) -> Status {
+        using O = decltype(out);
+        if (L.fp8)
+          return hyena_forward<uint16_t, O>(kind, projected_.as<uint16_t>(), rows, w, false, hw,
+                                            k.short_history.as<float>(),
+                                            k.inner_history.as<float>(),
+                                            k.modal_state.as<float>(), workspace_.as<void>(),
+                                            workspace_.bytes(), out, stream_);
+        return hyena_forward<float, O>(kind, projected, rows, w, false, hw,
+                                       k.short_history.as<float>(), k.inner_history.as<float>(),
+                                       k.modal_state.as<float>(), workspace_.as<void>(),
+                                       workspace_.bytes(), out, stream_);
+      };
+      if (f16_out)
+        EVO_TRY(mixer(F16Out{mixed_hi}));
       else
-        EVO_TRY((hyena_forward<float, SplitOut>(kind, projected, rows, w, false, hw,
-                                                k.short_history.as<float>(),
-                                                k.inner_history.as<float>(),
-                                                k.modal_state.as<float>(),
-                                                workspace_.as<void>(), workspace_.bytes(),
-                                                mixed_out, stream_)));
+        EVO_TRY(mixer(mixed_out));
     }
     // residual = (mixed . Wout^T + bias) + hidden   (`src/cpu/model.cpp:641-645`)
     // Short chunks split K here; the post-mixer norm then sums the partials
     // (with bias and hidden) into residual as it reads them.
     SplitPartials out_partials;
-    // "+f16-out" / "+f16-proj": the mixer output as one FP16 plane (in the
-    // projection's buffer, free after the mixer; saturating at +-65504) times
-    // the FP16 copy of the weight.
-    const bool f16_out = (options_.f16_proj || options_.f16_out) && split && !fold &&
-                         L.out_weight16.bytes() != 0 && (rows * w) % 8 == 0;
     if (f16_out) {
-      uint16_t *mixed16 = projected_.as<uint16_t>();
-      EVO_TRY(planes_to_f16(mixed_hi, mixed_lo, rows * w, mixed16, stream_));
-      EVO_TRY(gemm_bf16w(Activation{mixed16, nullptr, w, true}, L.out_weight16.as<uint16_t>(),
+      // The mixer's FP16 plane times the FP16 copy of the weight.
+      EVO_TRY(gemm_bf16w(Activation{mixed_hi, nullptr, w, true}, L.out_weight16.as<uint16_t>(),
                          GemmOutput{residual, nullptr, nullptr, w}, rows, w, w,
                          kGemmBiasResidual, L.out_bias.as<uint16_t>(), hidden, false, 0,
                          stream_, workspace_.as<float>(), workspace_.bytes(), &out_partials));

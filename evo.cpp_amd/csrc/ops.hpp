@@ -28,6 +28,12 @@ struct SplitOut {
   uint16_t *lo;
 };
 
+// Output of a producer kernel as one FP16 plane, fp16(v) rounded to nearest
+// even and saturated to +-65504, for the one-pass FP16 products.
+struct F16Out {
+  uint16_t *out;
+};
+
 // A GEMM activation as split BF16 planes: hi = bf16(a), lo = bf16(a - hi)
 // (lo null: BF16 activations), row stride ld elements.
 struct Activation {
@@ -192,12 +198,13 @@ Status qkv_rope(const float *projected, size_t rows, size_t width, size_t heads,
                 uint16_t *v_cache, size_t cache_plane, size_t capacity, hipStream_t stream);
 // Causal attention of `rows` queries at positions prefix.. against keys
 // [0, prefix + rows). Layout [time, heads, head_dim] = [time, W]. Output F32
-// (out_f32) or split planes (out_hi, out_lo).
+// (out_f32), split planes (out_hi, out_lo), or with out_f16 one saturated
+// FP16 plane in out_hi.
 Status causal_attention(const uint16_t *q, size_t q_plane, const uint16_t *k_cache,
                         const uint16_t *v_cache, size_t cache_plane, size_t capacity,
                         size_t rows, size_t prefix, size_t heads, size_t head_dim,
                         float *out_f32, uint16_t *out_hi, uint16_t *out_lo,
                         hipStream_t stream, float *workspace = nullptr,
-                        size_t workspace_bytes = 0);
+                        size_t workspace_bytes = 0, bool out_f16 = false);
 
 }  // namespace evo::hip
