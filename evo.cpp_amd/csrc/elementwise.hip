@@ -278,6 +278,27 @@ Status rms_norm_partials(const SplitPartials &src, float *sum, size_t rows, size
   return launch_status("rms_norm_reg_kernel (split-K partials)");
 }
 
+namespace {
+__global__ __launch_bounds__(256) void zero_regions_kernel(const ZeroRegion *__restrict__ regions) {
+  const ZeroRegion r = regions[blockIdx.y];
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < r.words;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x)
+    r.ptr[i] = 0U;
+}
+}  // namespace
+
+Status zero_regions(const ZeroRegion *regions, size_t count, size_t max_words,
+                    hipStream_t stream) {
+  if (count == 0 || max_words == 0)
+    return Status::Ok();
+  if (regions == nullptr || count > 65535)
+    return {ErrorCode::kInvalidArgument, "zero_regions: invalid arguments"};
+  const unsigned blocks = static_cast<unsigned>(std::min<size_t>(ceil_div(max_words, 256), 64));
+  hipLaunchKernelGGL(zero_regions_kernel, dim3(blocks, static_cast<unsigned>(count)), dim3(256),
+                     0, stream, regions);
+  return launch_status("zero_regions_kernel");
+}
+
 Status update_history(const float *x, size_t rows, size_t channels,
                       float *history, size_t history_rows, float *scratch,
                       hipStream_t stream) {

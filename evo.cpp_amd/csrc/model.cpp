@@ -470,15 +470,26 @@ Status Context::initialize(std::shared_ptr<const Model> model, size_t capacity,
     else
       EVO_TRY(k.modal_state.allocate(w * c.state * 4, "HCL state"));
   }
+  std::vector<ZeroRegion> regions;
+  for (auto &k : cache_)
+    for (DeviceBuffer *b : {&k.short_history, &k.inner_history, &k.modal_state})
+      if (b->bytes() != 0) {
+        regions.push_back(ZeroRegion{b->as<uint32_t>(), b->bytes() / 4});
+        reset_max_words_ = std::max(reset_max_words_, b->bytes() / 4);
+      }
+  reset_count_ = regions.size();
+  if (reset_count_ != 0) {
+    EVO_TRY(reset_table_.allocate(reset_count_ * sizeof(ZeroRegion), "cache reset table"));
+    EVO_TRY(reset_table_.upload(regions.data(), reset_count_ * sizeof(ZeroRegion),
+                                "cache reset table"));
+  }
   reset_caches();
   return hip_check(hipStreamSynchronize(stream_), "context initialise");
 }
 
 void Context::reset_caches() {
-  for (auto &k : cache_)
-    for (DeviceBuffer *b : {&k.short_history, &k.inner_history, &k.modal_state})
-      if (b->bytes() != 0)
-        (void)hipMemsetAsync(b->as<void>(), 0, b->bytes(), stream_);
+  // Every Hyena cache (all sizes are whole 32-bit words) in one launch.
+  (void)zero_regions(reset_table_.as<ZeroRegion>(), reset_count_, reset_max_words_, stream_);
   position_ = 0;
   valid_ = false;
 }

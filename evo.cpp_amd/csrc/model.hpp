@@ -157,8 +157,8 @@ private:
   // (short chunks): the next RMSNorm of hidden_ sums them as it reads them.
   SplitPartials pending_{};
   std::vector<hipEvent_t> timing_events_;  // start / stop per layer, or empty
-  size_t timed_pairs_{0};
-  unsigned hi_only_{0};  // diagnostic: GEMM classes run on the hi plane only  // event pairs the last enqueued chunk recorded
+  size_t timed_pairs_{0};  // event pairs the last enqueued chunk recorded
+  unsigned hi_only_{0};    // diagnostic: GEMM classes run on the hi plane only
   ContextOptions options_;
   std::string profile_;
   hipStream_t stream_{nullptr};
@@ -171,6 +171,10 @@ private:
     DeviceBuffer short_history, inner_history, modal_state, keys, values;
   };
   std::vector<Cache> cache_;
+  // Device table of the Hyena caches (ZeroRegion entries) that reset_caches
+  // clears in one launch.
+  DeviceBuffer reset_table_;
+  size_t reset_count_{0}, reset_max_words_{0};
   float *host_logits_{nullptr};
   int *host_flag_{nullptr};
 };

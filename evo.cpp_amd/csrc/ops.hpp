@@ -150,6 +150,15 @@ Status rms_norm_partials(const SplitPartials &src, float *sum, size_t rows, size
 Status update_history(const float *x, size_t rows, size_t channels,
                       float *history, size_t history_rows, float *scratch,
                       hipStream_t stream);
+// A device region of `words` 32-bit words for zero_regions.
+struct ZeroRegion {
+  uint32_t *ptr;
+  size_t words;
+};
+// Clears the `count` regions listed in the device table `regions` (the
+// largest `max_words` words long) in one launch.
+Status zero_regions(const ZeroRegion *regions, size_t count, size_t max_words,
+                    hipStream_t stream);
 
 // ---- Hyena operator (hyena.hip). Projection P [L, 3W] interleaved triples
 // (x2, x1, v) per channel. Caches (may be null for a fresh sequence):
