@@ -460,7 +460,7 @@ def main():
     hip.check(hip.lib.evo_batch_add_sequence(batch, seq, len(seq)))
     cabi_seconds = []
     for run in range(4):
-        ctx2 = model.context(args.tokens)
+        ctx2 = model.context(args.tokens, params.flags)
         start = time.perf_counter()
         hip.check(hip.lib.evo_context_prefill(ctx2.handle, batch, noop, None))
         if run > 0:
@@ -473,7 +473,7 @@ def main():
     decode_rate = None
     if args.decode_steps > 0:
         log(f"timing {args.decode_steps} decode steps after a 1024-token prefill")
-        ctx3 = model.context(1024 + args.decode_steps + 8)
+        ctx3 = model.context(1024 + args.decode_steps + 8, params.flags)
         token = int(ctx3.prefill(A.acgt_tokens(1024, seed=3).astype(np.uint8)
                                  .tobytes())[-1].argmax())
         for _ in range(4):

@@ -140,10 +140,11 @@ class Model:
     def width(self) -> int:
         return self.library.lib.evo_model_embedding_width(self.handle)
 
-    def context(self, context_size: int) -> "Context":
+    def context(self, context_size: int, flags: int = 0) -> "Context":
         lib = self.library.lib
         params = lib.evo_context_default_params()
         params.context_size = context_size
+        params.flags = flags
         handle = ctypes.c_void_p()
         self.library.check(lib.evo_context_create(self.handle, ctypes.byref(params),
                                                   ctypes.byref(handle)))
