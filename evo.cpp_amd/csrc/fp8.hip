@@ -278,21 +278,26 @@ __global__ __launch_bounds__(kWaves * 64, 2) void fp8_mfma_kernel(
       // sits between the chunk that produced it and the next one).
 #pragma unroll
       for (int c = 0; c < kBK / 32; ++c) {
+        // Lane half h reads the 16 codes [32c + 16h, 32c + 16h + 16) of its
+        // row in one 16-byte read (the conflict-free pattern of the K128
+        // path; two 8-byte reads per chunk put rows r and r + 16 on the same
+        // banks): the chunk's first MFMA takes codes 0-7 of each half, the
+        // second codes 8-15. A and W are split the same way, so the chunk
+        // still sums exactly its 32 products before the promotion.
         long bv[2][3], av[2][2];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int j = 0; j < 3; ++j) {
+          const int row = wave_n * 96 + j * 32 + col;
+          const uint4 v = *reinterpret_cast<const uint4 *>(w_s + fp8_unit(row, 2 * c + half) * 16);
+          bv[0][j] = static_cast<long>((static_cast<unsigned long>(v.y) << 32) | v.x);
+          bv[1][j] = static_cast<long>((static_cast<unsigned long>(v.w) << 32) | v.z);
+        }
 #pragma unroll
-          for (int j = 0; j < 3; ++j) {
-            const int row = wave_n * 96 + j * 32 + col;
-            bv[h][j] =
-                *reinterpret_cast<const long *>(w_s + fp8_unit(row, 2 * c + h) * 16 + half * 8);
-          }
-#pragma unroll
-          for (int i = 0; i < 2; ++i) {
-            const int row = wave_m * 64 + i * 32 + col;
-            av[h][i] =
-                *reinterpret_cast<const long *>(a_s + fp8_unit(row, 2 * c + h) * 16 + half * 8);
-          }
+        for (int i = 0; i < 2; ++i) {
+          const int row = wave_m * 64 + i * 32 + col;
+          const uint4 v = *reinterpret_cast<const uint4 *>(a_s + fp8_unit(row, 2 * c + half) * 16);
+          av[0][i] = static_cast<long>((static_cast<unsigned long>(v.y) << 32) | v.x);
+          av[1][i] = static_cast<long>((static_cast<unsigned long>(v.w) << 32) | v.z);
         }
 #pragma unroll
         for (int t = 0; t < 6; ++t) {
