@@ -367,7 +367,10 @@ __global__ __launch_bounds__(512) void gemm_kernel(
   constexpr int kMI = kGemmMI, kNJ = kGemmNJ;
   constexpr int kPlanes = kSplit ? 3 : 2;  // A hi, (A lo), W
   constexpr int kStage = kPlanes * kPlane;
-  __shared__ __attribute__((aligned(16))) uint16_t lds[kStages * kStage];
+  // One-plane products stage 32 KB per K step: four stages (three steps of
+  // DMA in flight) fit the LDS that three split stages take.
+  constexpr int kSt = kSplit ? kStages : 4;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[kSt * kStage];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -390,7 +393,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(
   // The A planes' DMAs go out before the weight's (issuing them
   // interleaved per row group measured 4 % slower on the MLP shape).
   auto issue = [&](int step) {
-    uint16_t *stage = lds + (step % kStages) * kStage;
+    uint16_t *stage = lds + (step % kSt) * kStage;
     const int k0 = step * kBK;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -417,25 +420,33 @@ __global__ __launch_bounds__(512) void gemm_kernel(
   issue(0);
   if (steps > 1)
     issue(1);
+  if (kSt > 3 && steps > 2)
+    issue(2);
   const int seg = lane >> 4;
   const int r16 = lane & 15;
   for (int s = 0; s < steps; ++s) {
-    // Wait for this wave's DMA of step s (the step s+1 batch may stay in
-    // flight), then for every wave's.
-    if (s + 1 < steps) {
-      if (kSplit)
+    // Wait for this wave's DMA of step s (the later steps' batches may stay
+    // in flight: 6 DMAs per wave and step split, 4 one-plane), then for
+    // every wave's.
+    if constexpr (kSplit) {
+      if (s + 1 < steps)
         asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
       else
-        asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     } else {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      if (s + 2 < steps)
+        asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+      else if (s + 1 < steps)
+        asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
     __syncthreads();
-    // The DMA of step s+2 (into the buffer of step s-1, which every wave has
-    // left) is issued between the two MFMA halves, not here: the VMEM issue
+    // The DMA of step s+kSt-1 (into the buffer of step s-1, which every
+    // wave has left) is issued between the two MFMA halves, not here: the VMEM issue
     // then overlaps MFMAs instead of delaying the first fragment reads
     // (+2-6 %; raising the wave priority around the MFMAs measured neutral).
-    const uint16_t *stage = lds + (s % kStages) * kStage;
+    const uint16_t *stage = lds + (s % kSt) * kStage;
     const uint16_t *sa_hi = stage;
     const uint16_t *sa_lo = stage + kPlane;
     const uint16_t *sw = stage + (kPlanes - 1) * kPlane;
@@ -492,8 +503,8 @@ __global__ __launch_bounds__(512) void gemm_kernel(
         __builtin_amdgcn_sched_group_barrier(0x008, kMfmas / kReads, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
-      if (s + 2 < steps)
-        issue(s + 2);
+      if (s + kSt - 1 < steps)
+        issue(s + kSt - 1);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = kMI / 2; i < kMI; ++i)
@@ -525,8 +536,8 @@ __global__ __launch_bounds__(512) void gemm_kernel(
         __builtin_amdgcn_sched_group_barrier(0x008, kMfmas / kReads, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
-      if (s + 2 < steps)
-        issue(s + 2);
+      if (s + kSt - 1 < steps)
+        issue(s + kSt - 1);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int j = kNJ / 2; j < kNJ; ++j)
