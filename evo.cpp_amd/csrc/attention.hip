@@ -53,23 +53,24 @@ __device__ inline size_t qkv_column(int column_split, size_t width, size_t head,
                       : component * width + head * head_dim + dim;
 }
 
-__global__ void qkv_rope_kernel(const float *__restrict__ projected, size_t rows,
-                                size_t width, size_t heads, size_t head_dim,
-                                int column_split, const float *__restrict__ inv_freq,
-                                float rope_scale, size_t prefix, uint16_t *__restrict__ q,
-                                size_t q_plane, uint16_t *__restrict__ k_cache,
-                                size_t cache_plane) {
-  const size_t half = head_dim / 2;
-  const size_t n = rows * heads * half;
-  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
-       i < n; i += static_cast<size_t>(gridDim.x) * blockDim.x) {
-    const size_t pair = i % half;
-    const size_t head = (i / half) % heads;
-    const size_t row = i / (half * heads);
-    const float *src = projected + row * width * 3;
-    const float position = static_cast<float>(prefix + row) / rope_scale;
-    const float angle = position * inv_freq[pair];
-    const float cosine = cosf(angle), sine = sinf(angle);
+// One block per row; thread t owns rotation pair t % (head_dim / 2) of
+// heads t / (head_dim / 2) + k * (512 / head_dim), so the pair's cosine and
+// sine are evaluated once per row (head_dim / 2 divides 256 for head_dim 16
+// to 128) and every wave reads and writes whole runs of consecutive dims.
+__global__ __launch_bounds__(256) void qkv_rope_kernel(
+    const float *__restrict__ projected, size_t width, size_t heads, int half,
+    int column_split, const float *__restrict__ inv_freq, float rope_scale, size_t prefix,
+    uint16_t *__restrict__ q, size_t q_plane, uint16_t *__restrict__ k_cache,
+    size_t cache_plane) {
+  const size_t row = blockIdx.x;
+  const size_t head_dim = 2 * static_cast<size_t>(half);
+  const int pair = static_cast<int>(threadIdx.x) % half;
+  const int head_step = 256 / half;
+  const float *src = projected + row * width * 3;
+  const float position = static_cast<float>(prefix + row) / rope_scale;
+  const float angle = position * inv_freq[pair];
+  const float cosine = cosf(angle), sine = sinf(angle);
+  for (size_t head = threadIdx.x / half; head < heads; head += head_step) {
     const size_t qi = row * width + head * head_dim;
     const size_t ki = (prefix + row) * width + head * head_dim;
     {
@@ -108,6 +109,31 @@ __global__ __launch_bounds__(256) void v_transpose_kernel(
     tile[tid & 63][i] = value;
   }
   __syncthreads();
+  if (prefix % 16 == 0 && r0 + 64 <= rows && c0 + 64 <= width) {
+    // Whole tile from a 16-aligned position: its 64 V^T columns per channel
+    // are [prefix + r0, +64) in the permuted order; each lane packs 8 of
+    // them (column j holds row vt_column(j), the permutation being its own
+    // inverse) into one 16-byte store per plane.
+    uint16_t *base = vt_cache + prefix + r0;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int idx = tid + 256 * k, i = idx >> 3, unit = idx & 7;
+      uint32_t hi[4], lo[4];
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const float a = tile[i][vt_column(8 * unit + e)];
+        const float b = tile[i][vt_column(8 * unit + e + 1)];
+        const uint16_t ha = f32_to_bf16(a), hb = f32_to_bf16(b);
+        hi[e / 2] = ha | (static_cast<uint32_t>(hb) << 16);
+        lo[e / 2] = f32_to_bf16(a - bf16_to_f32(ha)) |
+                    (static_cast<uint32_t>(f32_to_bf16(b - bf16_to_f32(hb))) << 16);
+      }
+      const size_t at = (c0 + i) * capacity + 8 * unit;
+      *reinterpret_cast<uint4 *>(base + at) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+      *reinterpret_cast<uint4 *>(base + cache_plane + at) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+    }
+    return;
+  }
   for (int i = tid >> 6; i < 64; i += 4) {
     const size_t ch = c0 + i, row = r0 + (tid & 63);
     if (row < rows && ch < width)
@@ -614,11 +640,12 @@ Status qkv_rope(const float *projected, size_t rows, size_t width, size_t heads,
       q_plane < rows * width || capacity % kKeys != 0 || prefix + rows > capacity ||
       cache_plane < capacity * width)
     return {ErrorCode::kInvalidArgument, "qkv_rope: invalid arguments"};
-  const size_t n = rows * heads * (width / heads / 2);
-  const unsigned grid = static_cast<unsigned>(std::min<size_t>((n + 255) / 256, 16384));
-  hipLaunchKernelGGL(qkv_rope_kernel, dim3(grid), dim3(256), 0, stream, projected, rows,
-                     width, heads, width / heads, column_split ? 1 : 0, inv_freq,
-                     rope_scale, prefix, q, q_plane, k_cache, cache_plane);
+  const size_t half = width / heads / 2;
+  if (256 % half != 0 || rows > (1U << 31))
+    return {ErrorCode::kInvalidArgument, "qkv_rope: head_dim / 2 must divide 256"};
+  hipLaunchKernelGGL(qkv_rope_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, stream,
+                     projected, width, heads, static_cast<int>(half), column_split ? 1 : 0,
+                     inv_freq, rope_scale, prefix, q, q_plane, k_cache, cache_plane);
   EVO_TRY(launch_status("qkv_rope_kernel"));
   hipLaunchKernelGGL(v_transpose_kernel, dim3(ceil_div(rows, 64), ceil_div(width, 64)),
                      dim3(256), 0, stream, projected, rows, width, width / heads,
