@@ -269,13 +269,18 @@ def test_config4_full_7b_fp8_projections(hip, evo2_7b):
 
 
 # -------------------------------------------------------------- config 5
-def test_config5_131072_tokens_arena_consistency(hip, evo2_7b):
+@pytest.mark.parametrize("model_flags,flags", [
+    pytest.param(0, 0, id="bf16-projections"),
+    # bench.py's configuration: FP8 projections, FP16 out-projections
+    pytest.param(1 << 8, 1 << 12, id="fp8+f16-out")])
+def test_config5_131072_tokens_arena_consistency(hip, evo2_7b, model_flags, flags):
     tokens = A.acgt_tokens(131072, seed=5)
-    whole = resident_prefill(hip, evo2_7b, tokens)
+    whole = resident_prefill(hip, evo2_7b, tokens, flags=flags, model_flags=model_flags)
     assert np.isfinite(whole).all()
-    chunked = resident_prefill(hip, evo2_7b, tokens, arena=4096)
+    chunked = resident_prefill(hip, evo2_7b, tokens, arena=4096, flags=flags,
+                               model_flags=model_flags)
     error = relmax(chunked, whole)
-    say(f"config 5 (131072 tokens): arena 4096 vs 8192 max err {error:.3g}")
+    say(f"config 5 (131072 tokens, flags {flags:#x}): arena 4096 vs 8192 max err {error:.3g}")
     assert error <= 1e-4
 
 
