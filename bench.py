@@ -125,9 +125,12 @@ def kernel_rooflines(split):
     out["gemm"] = dict(kernel="gemm_kernel<%s>" % ("true" if split else "false"),
                        ms=ms, flops=flops, tflops=flops / ms / 1e9)
     del x, w, y, planes
-    # Hyena operators on the model's path: BF16 projection [8192, 12288] in
-    # (the FP8 projection's output), split BF16 planes [2, 8192, 4096] out,
-    # 7B filter groups (256) and tap counts (HCS 7, HCM 128, HCL 16 states).
+    # Hyena operators at the model's shape: BF16 projection [8192, 12288] in
+    # (the FP8 projection's output), one 16-bit plane [8192, 4096] out (BF16
+    # here; the benchmarked context's FP16 plane has the same bytes and code
+    # path) and split BF16 planes [2, 8192, 4096] out (contexts without
+    # +f16-out), 7B filter groups (256) and tap counts (HCS 7, HCM 128, HCL
+    # 16 states).
     length, width, state, groups = 8192, 4096, 16, 256
     proj = torch.randn(length, 3 * width, device="cuda", generator=g).to(torch.bfloat16)
     short = (torch.randn(3 * width, 3, device="cuda", generator=g) * 0.3).to(torch.bfloat16)
@@ -558,9 +561,10 @@ def main():
                               "standalone_achieved": round(g["tflops"], 1),
                               "per_launch": "2*8192*22528*4096 flop (MLP l1/l2 of one block)"}
         # Config 2 is timed in the operator's own format (BF16 [8192, 12288]
-        # in, BF16 [8192, 4096] out: 268435456 B per launch) -- `frac` --
-        # and in the model path's format (same input, split BF16 planes
-        # out: 335544320 B) -- `frac_split_planes`, from its own launch time.
+        # in, BF16 [8192, 4096] out: 268435456 B per launch, the bytes of the
+        # benchmarked context's FP16 mixer output) -- `frac` -- and with split
+        # BF16 planes out (335544320 B, the hip-f32 context without
+        # +f16-out) -- `frac_split_planes`, from its own launch time.
         hyena = []
         for h in kernels["hyena"]:
             extra = {}
