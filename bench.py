@@ -126,11 +126,10 @@ def kernel_rooflines(split):
                        ms=ms, flops=flops, tflops=flops / ms / 1e9)
     del x, w, y, planes
     # Hyena operators at the model's shape: BF16 projection [8192, 12288] in
-    # (the FP8 projection's output), one 16-bit plane [8192, 4096] out (BF16
-    # here; the benchmarked context's FP16 plane has the same bytes and code
-    # path) and split BF16 planes [2, 8192, 4096] out (contexts without
-    # +f16-out), 7B filter groups (256) and tap counts (HCS 7, HCM 128, HCL
-    # 16 states).
+    # (the FP8 projection's output), out as one BF16 plane (config 2's
+    # format), one FP16 plane (the benchmarked context's) and split BF16
+    # planes [2, 8192, 4096] (contexts without +f16-out), 7B filter groups
+    # (256) and tap counts (HCS 7, HCM 128, HCL 16 states).
     length, width, state, groups = 8192, 4096, 16, 256
     proj = torch.randn(length, 3 * width, device="cuda", generator=g).to(torch.bfloat16)
     short = (torch.randn(3 * width, 3, device="cuda", generator=g) * 0.3).to(torch.bfloat16)
@@ -154,7 +153,7 @@ def kernel_rooflines(split):
         ws_bytes = native.call("evo_hip_hyena_workspace_bytes", kind, length, width, st)
         ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device="cuda")
         times = {}
-        for dtype in (native.DTYPE_BF16, native.DTYPE_BF16_SPLIT):
+        for dtype in (native.DTYPE_BF16, native.DTYPE_BF16_SPLIT, native.DTYPE_BF16_F16):
             times[dtype] = event_time(lambda: native.call(
                 "evo_hip_hyena_forward", kind, dtype | native.DTYPE_BF16_TAPS,
                 proj.data_ptr(), length,
@@ -162,9 +161,11 @@ def kernel_rooflines(split):
                 poles.data_ptr(), residues.data_ptr(), st, None, None, None, ws.data_ptr(),
                 ws_bytes, planes_out.data_ptr(), stream), 10)
         ms, ms_split = times[native.DTYPE_BF16], times[native.DTYPE_BF16_SPLIT]
+        ms_f16 = times[native.DTYPE_BF16_F16]
         out["hyena"].append(dict(kernel=name, profiled=profiled, ms=ms, bytes=bf16_bytes, gbs=bf16_bytes / ms / 1e6,
                                  ms_split=ms_split, bytes_split=hbm_bytes,
-                                 gbs_split=hbm_bytes / ms_split / 1e6))
+                                 gbs_split=hbm_bytes / ms_split / 1e6,
+                                 ms_f16=ms_f16, gbs_f16=bf16_bytes / ms_f16 / 1e6))
     del proj, planes_out
     # config 3: FP8 projection GEMM M=1024 K=4096 N=12288 (promotion every 32 K)
     m, k, n = 1024, 4096, 12288
@@ -561,10 +562,11 @@ def main():
                               "standalone_achieved": round(g["tflops"], 1),
                               "per_launch": "2*8192*22528*4096 flop (MLP l1/l2 of one block)"}
         # Config 2 is timed in the operator's own format (BF16 [8192, 12288]
-        # in, BF16 [8192, 4096] out: 268435456 B per launch, the bytes of the
-        # benchmarked context's FP16 mixer output) -- `frac` -- and with split
-        # BF16 planes out (335544320 B, the hip-f32 context without
-        # +f16-out) -- `frac_split_planes`, from its own launch time.
+        # in, BF16 [8192, 4096] out: 268435456 B per launch) -- `frac` --,
+        # with one FP16 plane out (the same bytes; the benchmarked context's
+        # mixer output) -- `frac_f16_out` -- and with split BF16 planes out
+        # (335544320 B, the hip-f32 context without +f16-out) --
+        # `frac_split_planes`, each from its own launch time.
         hyena = []
         for h in kernels["hyena"]:
             extra = {}
@@ -579,9 +581,11 @@ def main():
                           "frac": round(h["gbs"] / HBM_PEAK_GBS, 4),
                           "traffic": measured_traffic(h["profiled"]), "ms": round(h["ms"], 4),
                           "ms_split_planes": round(h["ms_split"], 4),
-                          "frac_split_planes": round(h["gbs_split"] / HBM_PEAK_GBS, 4)})
+                          "frac_split_planes": round(h["gbs_split"] / HBM_PEAK_GBS, 4),
+                          "ms_f16_out": round(h["ms_f16"], 4),
+                          "frac_f16_out": round(h["gbs_f16"] / HBM_PEAK_GBS, 4)})
         per_launch = ("268435456 B: read BF16 [8192, 12288] projection, write BF16 "
-                      "[8192, 4096]; split planes out: 335544320 B")
+                      "(or FP16) [8192, 4096]; split planes out: 335544320 B")
         worst = min(hyena, key=lambda h: h["frac"])
         result["hyena_roofline"] = dict(worst, bound="hbm", per_launch=per_launch)
         result["hyena_kernels"] = hyena

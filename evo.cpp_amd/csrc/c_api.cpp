@@ -615,6 +615,8 @@ evo::Status hyena_dispatch(evo_hip_hyena_kind kind, evo_hip_dtype dtype,
                            const evo::hip::HyenaWeights &w, float *short_history,
                            float *inner_history, float *modal_state, void *workspace,
                            size_t workspace_bytes, void *output, hipStream_t s) {
+  if (output == nullptr)
+    return {evo::ErrorCode::kInvalidArgument, "invalid_argument: hyena output is NULL"};
   const bool planar = (static_cast<int>(dtype) & EVO_HIP_PLANAR) != 0;
   dtype = static_cast<evo_hip_dtype>(static_cast<int>(dtype) &
                                      ~(EVO_HIP_PLANAR | EVO_HIP_BF16_TAPS));
@@ -627,8 +629,18 @@ evo::Status hyena_dispatch(evo_hip_hyena_kind kind, evo_hip_dtype dtype,
         kind, static_cast<const uint16_t *>(projection), length, width, planar, w, short_history,
         inner_history, modal_state, workspace, workspace_bytes,
         static_cast<uint16_t *>(output), s);
+  if (dtype == EVO_HIP_F16)
+    return evo::hip::hyena_forward<float, evo::hip::F16Out>(
+        kind, static_cast<const float *>(projection), length, width, planar, w, short_history,
+        inner_history, modal_state, workspace, workspace_bytes,
+        evo::hip::F16Out{static_cast<uint16_t *>(output)}, s);
+  if (dtype == EVO_HIP_BF16_F16)
+    return evo::hip::hyena_forward<uint16_t, evo::hip::F16Out>(
+        kind, static_cast<const uint16_t *>(projection), length, width, planar, w, short_history,
+        inner_history, modal_state, workspace, workspace_bytes,
+        evo::hip::F16Out{static_cast<uint16_t *>(output)}, s);
   auto *hi = static_cast<uint16_t *>(output);
-  const evo::hip::SplitOut split{hi, hi == nullptr ? nullptr : hi + length * width};
+  const evo::hip::SplitOut split{hi, hi + length * width};
   if (dtype == EVO_HIP_SPLIT)
     return evo::hip::hyena_forward<float, evo::hip::SplitOut>(
         kind, static_cast<const float *>(projection), length, width, planar, w, short_history,

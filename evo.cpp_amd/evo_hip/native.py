@@ -16,7 +16,7 @@ c_size, c_void, c_float, c_int = (ctypes.c_size_t, ctypes.c_void_p,
                                    ctypes.c_float, ctypes.c_int)
 
 HYENA_HCS, HYENA_HCM, HYENA_HCL = 0, 1, 2
-DTYPE_F32, DTYPE_BF16, DTYPE_SPLIT, DTYPE_BF16_SPLIT = 0, 1, 2, 3
+DTYPE_F32, DTYPE_BF16, DTYPE_SPLIT, DTYPE_BF16_SPLIT, DTYPE_F16, DTYPE_BF16_F16 = 0, 1, 2, 3, 4, 5
 DTYPE_PLANAR = 0x100  # OR-ed into the Hyena dtype: planar projection columns
 DTYPE_BF16_TAPS = 0x200  # OR-ed into the Hyena dtype: inner taps are BF16 values
 FP8_MFMA_K32, FP8_MFMA_K128, FP8_EXACT = 0, 1, 2

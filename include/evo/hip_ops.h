@@ -52,12 +52,18 @@ EVO_API evo_status evo_hip_context_product_time(const evo_context *context, floa
 /* EVO_HIP_SPLIT: F32 input, output as split BF16 planes [2][rows][cols]
  * (hi = bf16(y), lo = bf16(y - hi)), the GEMM activation layout.
  * EVO_HIP_BF16_SPLIT: BF16 input (the FP8 projection's output), split
- * output; Hyena operator only. */
+ * output; Hyena operator only.
+ * EVO_HIP_F16 / EVO_HIP_BF16_F16: F32 / BF16 input, output one FP16 plane
+ * [rows][cols], fp16(y) rounded to nearest even and saturated to +-65504
+ * (the activation of the one-pass FP16 out-projection); Hyena operator
+ * only. */
 typedef enum evo_hip_dtype {
   EVO_HIP_F32 = 0,
   EVO_HIP_BF16 = 1,
   EVO_HIP_SPLIT = 2,
   EVO_HIP_BF16_SPLIT = 3,
+  EVO_HIP_F16 = 4,
+  EVO_HIP_BF16_F16 = 5,
   /* OR-ed into the Hyena operator's dtype: the projection holds stream s
    * (x2, x1, v) of channel c at column s*W + c instead of the reference's
    * 3c + s (the library permutes its projection weights this way). */

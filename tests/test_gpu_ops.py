@@ -446,11 +446,12 @@ def hyena_gpu(kind, case, dtype=N.DTYPE_F32, rows=None, caches=None, projection=
     ws_bytes = N.call("evo_hip_hyena_workspace_bytes", kind, length, width, state)
     ws = empty((max(ws_bytes, 256),), np.uint8)
     out_shape, out_type = ((length, width), np.float32)
-    if dtype == N.DTYPE_BF16:
+    if dtype in (N.DTYPE_BF16, N.DTYPE_F16, N.DTYPE_BF16_F16):
         out_shape, out_type = (length, width), np.uint16
     elif dtype in (N.DTYPE_SPLIT, N.DTYPE_BF16_SPLIT):
         out_shape, out_type = (2, length, width), np.uint16
-    proj_d = dev(bf16_bits(proj) if dtype in (N.DTYPE_BF16, N.DTYPE_BF16_SPLIT) else proj)
+    bf16_in = dtype in (N.DTYPE_BF16, N.DTYPE_BF16_SPLIT, N.DTYPE_BF16_F16)
+    proj_d = dev(bf16_bits(proj) if bf16_in else proj)
     full = None
     if guard:
         full, out = guarded(out_shape, out_type, guard)
@@ -474,6 +475,8 @@ def hyena_gpu(kind, case, dtype=N.DTYPE_F32, rows=None, caches=None, projection=
     if dtype in (N.DTYPE_SPLIT, N.DTYPE_BF16_SPLIT):
         planes = bf16_to_f32(result.view(np.uint16))
         return planes[0].astype(np.float64) + planes[1]
+    if dtype in (N.DTYPE_F16, N.DTYPE_BF16_F16):
+        return result.view(np.uint16).view(np.float16).astype(np.float32)
     return bf16_to_f32(result.view(np.uint16)) if dtype == N.DTYPE_BF16 else result
 
 
@@ -511,7 +514,7 @@ def test_hyena_fir_mfma_matches_oracle(kind, inner_len, length, width, groups):
 
 @pytest.mark.parametrize("kind,inner_len", KINDS)
 @pytest.mark.parametrize("dtype", [N.DTYPE_F32, N.DTYPE_BF16, N.DTYPE_SPLIT,
-                                   N.DTYPE_BF16_SPLIT])
+                                   N.DTYPE_BF16_SPLIT, N.DTYPE_BF16_F16])
 @pytest.mark.parametrize("length", [2, 3, 295, 1025, 1031])
 def test_hyena_leaves_rows_past_the_output(kind, inner_len, dtype, length):
     """Rows past the sequence end (the last chunk / segment / store pair is
@@ -521,12 +524,12 @@ def test_hyena_leaves_rows_past_the_output(kind, inner_len, dtype, length):
     runs the decode kernel)."""
     case = hyena_case(3 * length + kind, kind, length, 64, groups=4, inner_len=inner_len or 7)
     proj = case["projection"]
-    if dtype in (N.DTYPE_BF16, N.DTYPE_BF16_SPLIT):
+    if dtype in (N.DTYPE_BF16, N.DTYPE_BF16_SPLIT, N.DTYPE_BF16_F16):
         proj = bf16_to_f32(bf16_bits(proj))
     expected = hyena_oracle(kind, case, projection=proj)
     actual = hyena_gpu(kind, case, dtype=dtype, projection=proj, guard=64,
                        bf16_taps=kind == N.HYENA_HCM)
-    bound = 2.0 ** -8 if dtype == N.DTYPE_BF16 else 2e-5
+    bound = {N.DTYPE_BF16: 2.0 ** -8, N.DTYPE_BF16_F16: 2.0 ** -11 + 2e-5}.get(dtype, 2e-5)
     assert rel_err(actual, expected) < bound
 
 
@@ -536,6 +539,28 @@ def test_hyena_split_output(kind, inner_len):
     case = hyena_case(91 + kind, kind, 513, 96, inner_len=inner_len or 7)
     expected = hyena_oracle(kind, case)
     assert rel_err(hyena_gpu(kind, case, dtype=N.DTYPE_SPLIT), expected) < 2e-5
+
+
+@pytest.mark.parametrize("kind,inner_len", KINDS)
+@pytest.mark.parametrize("length", [1, 777])
+def test_hyena_f16_output(kind, inner_len, length):
+    """One FP16 plane out (the one-pass FP16 out-projection's activation):
+    with F32 input it is exactly fp16(y) of the F32-output kernel's y (RNE,
+    saturated to +-65504), including a large-valued case that saturates; with
+    BF16 input (the FP8 projection's output) it matches the oracle on the same
+    BF16-rounded projection to FP16 rounding."""
+    case = hyena_case(61 + kind + length, kind, length, 128, inner_len=inner_len or 7)
+    for scale in (1.0, 3000.0):  # 3000: |y| ~ 1e5..1e7 exceeds the FP16 range
+        big = dict(case, projection=(case["projection"] * scale).astype(np.float32))
+        y = hyena_gpu(kind, big)
+        expected16 = np.clip(y, -65504.0, 65504.0).astype(np.float16).astype(np.float32)
+        actual16 = hyena_gpu(kind, big, dtype=N.DTYPE_F16)
+        assert np.array_equal(actual16.view(np.uint32), expected16.view(np.uint32))
+    proj = bf16_to_f32(bf16_bits(case["projection"]))
+    expected = hyena_oracle(kind, case, projection=proj)
+    actual = hyena_gpu(kind, case, dtype=N.DTYPE_BF16_F16, projection=proj,
+                       bf16_taps=kind == N.HYENA_HCM)
+    assert rel_err(actual, expected) <= 2.0 ** -11 + 2e-5
 
 
 @pytest.mark.parametrize("kind,inner_len", KINDS)
