@@ -423,12 +423,13 @@ def main():
 
     samples = {}
 
-    def resident_rate(length, steps, warmup):
+    def resident_rate(length, steps, warmup, ctx_handle=None):
         tokens = torch.from_numpy(A.acgt_tokens(length, seed=2).astype(np.int32)).cuda()
         logits = torch.empty(length, shape.vocab, device="cuda")
+        target = handle if ctx_handle is None else ctx_handle
 
         def step():
-            status = lib.evo_hip_context_prefill_resident(handle, tokens.data_ptr(), length,
+            status = lib.evo_hip_context_prefill_resident(target, tokens.data_ptr(), length,
                                                          logits.data_ptr())
             if status != 0:
                 raise RuntimeError(lib.evo_last_error().decode())
@@ -452,6 +453,21 @@ def main():
     # (the last timed prefill's launches; every prefill rewrites the events)
     product_ms, product_launches = product_time()
     rate_1k, ms_1k = resident_rate(1024, max(args.steps, 5), 2)
+    # The same prefill with every product but the FP8 ones on split BF16
+    # (the context without EVO_CONTEXT_FLAG_HIP_F16_OUT), for reference.
+    split_out = None
+    if f16_out:
+        sparams = hip.lib.evo_context_default_params()
+        sparams.context_size = params.context_size
+        sparams.flags = params.flags & ~F16_OUT_FLAG
+        shandle = ctypes.c_void_p()
+        hip.check(hip.lib.evo_context_create(model.handle, ctypes.byref(sparams),
+                                             ctypes.byref(shandle)))
+        split_ctx = capi.Context(model, shandle)
+        srate, sms = resident_rate(args.tokens, max(args.steps // 2, 3), 1, shandle)
+        split_out = {"tok_s": round(srate, 1), "ms_per_step": round(sms, 3),
+                     "profile": split_ctx.profile}
+        split_ctx.close()
     # C-ABI rate with host logits (PCIe-inclusive; not the headline value):
     # a prefill needs a fresh context, so each run opens one (not timed);
     # one warm-up run, then the median of three.
@@ -537,7 +553,8 @@ def main():
                    "samples_ms_1k": samples.get(1024),
                    "c_abi_host_logits_tok_s": round(cabi_rate, 1),
                    "decode_tok_s_after_1k": round(decode_rate, 1) if decode_rate else None,
-                   "long_context_prefill": long_result},
+                   "long_context_prefill": long_result,
+                   "split_out_projections": split_out},
     }
     if not args.no_kernels:
         log("kernel rooflines")
