@@ -7,7 +7,8 @@ F32 path. CPU only (the oracle's emulation mode, oracle_set_lo_emulation).
 
 Masks: bit 0 BF16 projections, 1 out-projection, 2 MLP l1/l2, 3 MLP l3 (the
 E4M3-lo scheme); 16 attention keys and 32 values rounded to BF16 (two-pass
-split attention products). A fourth argument "one-of-each" uses the 7B-width
+split attention products); 512 the attention probabilities rounded to FP16
+before P.V (a two-pass FP16 P.V). A fourth argument "one-of-each" uses the 7B-width
 model with one block of each mixer (HCS, HCM, HCL, attention) instead of the
 32-block 7B shape.
 """

@@ -736,7 +736,7 @@ void linear_model(const std::vector<float> &input, size_t rows, size_t in,
 // E8M0 scale per row and 32-K block (2^ceil(log2(amax / 448)), so no block
 // saturates). q(W) is exact in BF16, so both products run as BF16-weight
 // dots. Used only to measure how such a GEMM's rounding reaches the logits.
-unsigned g_lo_emulation = 0;  // bit 0 projections, 1 out, 2 l1/l2, 3 l3; 4, 5 attention; 6 FP16 hi; 7 no lo; 8 row scales
+unsigned g_lo_emulation = 0;  // bit 0 projections, 1 out, 2 l1/l2, 3 l3; 4, 5 attention; 6 FP16 hi; 7 no lo; 8 row scales; 9 FP16 probabilities
 
 float e4m3_block_scale(const float *v, size_t n) {
   float amax = 0.0F;
@@ -1036,8 +1036,12 @@ void attention_model(const Model &m, const std::vector<float> &projected,
       denominator += score;
     }
     float *total = output->data() + query_base;  // zero-initialised above
+    // Design experiment (bit 9): the unnormalised probabilities enter P.V
+    // rounded to FP16 (a two-pass FP16 P.V with V split into FP16 planes);
+    // the denominator keeps their F32 sum.
+    const bool fp16_p = g_lo_emulation >> 9 & 1U;
     for (source = 0; source < sources; ++source) {
-      const float weight = scores[source] / denominator;
+      const float weight = (fp16_p ? fp16_round(scores[source]) : scores[source]) / denominator;
       const float *v = cache->value.data() + source * width + head * head_dim;
       for (size_t dimension = 0; dimension < head_dim; ++dimension)
         total[dimension] += weight * v[dimension];

@@ -647,6 +647,34 @@ def test_hcm_stream_continuation(split):
 
 
 # ----------------------------------------------------------- attention
+@pytest.mark.parametrize("heads,head_dim,rows,prefix", [(2, 128, 300, 0), (2, 64, 200, 70),
+                                                        (3, 32, 1, 500)])
+def test_attention_uniform_scores(heads, head_dim, rows, prefix):
+    """Q = 0: every score is 0, every probability exactly 1, so each output
+    row is the plain mean of V over its keys: the P.V path (V^T split BF16
+    planes, ~16 significant bits, F32 accumulation) to 2^-16 of max |v|.
+    A product that lost V's lo plane would miss by ~2^-9."""
+    r = rng(7 * heads + head_dim + rows)
+    width = heads * head_dim
+    total = prefix + rows
+    proj = r.standard_normal((total, 3 * width)).astype(np.float32)
+    qkv = proj.reshape(total, heads, 3, head_dim)
+    qkv[:, :, 0] = 0.0
+    v = qkv[:, :, 2].reshape(total, width).astype(np.float64)
+    expected = (np.cumsum(v, axis=0) / np.arange(1, total + 1)[:, None])[prefix:]
+    inv_freq = (1.0 / 10000 ** (np.arange(0, head_dim, 2) / head_dim)).astype(np.float32)
+    capacity = (total + 63) // 64 * 64
+    kc, vc = zeros((2, capacity, width), np.uint16), zeros((2, width, capacity), np.uint16)
+    query, out = empty((2, total, width), np.uint16), empty((total, width))
+    if prefix:
+        N.call("evo_hip_attention", p(dev(proj[:prefix])), prefix, width, heads, 1,
+               p(dev(inv_freq)), 8.0, 0, p(query), p(kc), p(vc), capacity, p(out), stream())
+    N.call("evo_hip_attention", p(dev(proj[prefix:])), rows, width, heads, 1,
+           p(dev(inv_freq)), 8.0, prefix, p(query), p(kc), p(vc), capacity, p(out), stream())
+    error = np.abs(host(out)[:rows] - expected).max() / np.abs(v).max()
+    assert error <= 2.0 ** -16
+
+
 @pytest.mark.parametrize("rows,heads,head_dim,prefix", [
     (70, 4, 16, 0), (130, 2, 128, 0), (64, 3, 64, 33), (300, 2, 128, 129), (1, 4, 32, 0),
     (257, 1, 32, 0), (1000, 2, 128, 0)])
