@@ -30,6 +30,17 @@
 #include "ops.hpp"
 
 namespace evo::hip {
+
+// FP16-plane attention output without a per-value range check: the outputs
+// are convex combinations of V rows, whose range qkv_rope checks as they
+// enter the cache.
+struct F16Plane {
+  uint16_t *out;
+};
+__device__ inline void put(const F16Plane &o, size_t i, float v) {
+  o.out[i] = f32_to_f16_sat(v);
+}
+
 namespace {
 
 __device__ inline void put_split(uint16_t *hi, uint16_t *lo, size_t i, float v) {
@@ -94,11 +105,12 @@ __global__ __launch_bounds__(256) void qkv_rope_kernel(
 __global__ __launch_bounds__(256) void v_transpose_kernel(
     const float *__restrict__ projected, size_t rows, size_t width, size_t head_dim,
     int column_split, size_t prefix, uint16_t *__restrict__ vt_cache, size_t cache_plane,
-    size_t capacity) {
+    size_t capacity, int *range_flag) {
   __shared__ float tile[64][65];
   const int tid = threadIdx.x;
   const size_t r0 = blockIdx.x * 64ULL, c0 = blockIdx.y * 64ULL;
   const size_t channel = c0 + (tid & 63);
+  bool out_of_range = false;
   for (int i = tid >> 6; i < 64; i += 4) {
     const size_t row = r0 + i;
     float value = 0.0F;
@@ -106,8 +118,11 @@ __global__ __launch_bounds__(256) void v_transpose_kernel(
       value = projected[row * width * 3 +
                         qkv_column(column_split, width, channel / head_dim, head_dim, 2,
                                    channel % head_dim)];
+    out_of_range |= !(__builtin_fabsf(value) <= 65504.0F);
     tile[tid & 63][i] = value;
   }
+  if (range_flag != nullptr && out_of_range)
+    atomicOr(range_flag, kFlagF16Range);
   __syncthreads();
   if (prefix % 16 == 0 && r0 + 64 <= rows && c0 + 64 <= width) {
     // Whole tile from a 16-aligned position: its 64 V^T columns per channel
@@ -633,7 +648,8 @@ Status launch_attention(const uint16_t *q, size_t q_plane, const uint16_t *k_cac
 Status qkv_rope(const float *projected, size_t rows, size_t width, size_t heads,
                 bool column_split, const float *inv_freq, float rope_scale,
                 size_t prefix, uint16_t *q, size_t q_plane, uint16_t *k_cache,
-                uint16_t *v_cache, size_t cache_plane, size_t capacity, hipStream_t stream) {
+                uint16_t *v_cache, size_t cache_plane, size_t capacity, hipStream_t stream,
+                int *v_range_flag) {
   if (projected == nullptr || inv_freq == nullptr || q == nullptr ||
       k_cache == nullptr || v_cache == nullptr || rows == 0 || heads == 0 ||
       width % heads != 0 || (width / heads) % 2 != 0 || !(rope_scale > 0.0F) ||
@@ -649,7 +665,8 @@ Status qkv_rope(const float *projected, size_t rows, size_t width, size_t heads,
   EVO_TRY(launch_status("qkv_rope_kernel"));
   hipLaunchKernelGGL(v_transpose_kernel, dim3(ceil_div(rows, 64), ceil_div(width, 64)),
                      dim3(256), 0, stream, projected, rows, width, width / heads,
-                     column_split ? 1 : 0, prefix, v_cache, cache_plane, capacity);
+                     column_split ? 1 : 0, prefix, v_cache, cache_plane, capacity,
+                     v_range_flag);
   return launch_status("v_transpose_kernel");
 }
 
@@ -685,7 +702,7 @@ Status causal_attention(const uint16_t *q, size_t q_plane, const uint16_t *k_cac
     if (out_f32 != nullptr)
       return run(out_f32);
     if (out_f16)
-      return run(F16Out{out_hi});
+      return run(F16Plane{out_hi});
     return run(SplitOut{out_hi, out_lo});
   }
   if (out_f32 != nullptr)
@@ -693,7 +710,7 @@ Status causal_attention(const uint16_t *q, size_t q_plane, const uint16_t *k_cac
                             heads, head_dim, out_f32, stream);
   if (out_f16)
     return launch_attention(q, q_plane, k_cache, v_cache, cache_plane, capacity, rows, prefix,
-                            heads, head_dim, F16Out{out_hi}, stream);
+                            heads, head_dim, F16Plane{out_hi}, stream);
   return launch_attention(q, q_plane, k_cache, v_cache, cache_plane, capacity, rows, prefix,
                           heads, head_dim, SplitOut{out_hi, out_lo}, stream);
 }

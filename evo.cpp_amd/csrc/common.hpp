@@ -165,7 +165,16 @@ __device__ inline void put(const SplitOut &out, size_t i, float v) {
 __device__ inline uint16_t f32_to_f16_sat(const float v) {
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(fminf(fmaxf(v, -65504.0F), 65504.0F)));
 }
-__device__ inline void put(const F16Out &out, size_t i, float v) { out.out[i] = f32_to_f16_sat(v); }
+// Raises kFlagF16Range in *flag (when given) for a value outside the FP16
+// range or NaN, which the saturating conversion would hide.
+__device__ inline void note_f16_range(int *flag, float v) {
+  if (flag != nullptr && !(__builtin_fabsf(v) <= 65504.0F))
+    atomicOr(flag, kFlagF16Range);
+}
+__device__ inline void put(const F16Out &out, size_t i, float v) {
+  note_f16_range(out.saturated, v);
+  out.out[i] = f32_to_f16_sat(v);
+}
 
 // Non-temporal variants for outputs no later part of the producing kernel
 // reads: the stores stream past the L2 instead of evicting its input lines.
@@ -176,6 +185,7 @@ __device__ inline void put_nt(uint16_t *out, size_t i, float v) {
   __builtin_nontemporal_store(f32_to_bf16(v), out + i);
 }
 __device__ inline void put_nt(const F16Out &out, size_t i, float v) {
+  note_f16_range(out.saturated, v);
   __builtin_nontemporal_store(f32_to_f16_sat(v), out.out + i);
 }
 __device__ inline void put_nt(const SplitOut &out, size_t i, float v) {

@@ -25,7 +25,7 @@ __global__ void embed_kernel(const uint32_t *__restrict__ tokens, size_t rows,
     const uint32_t token = tokens[row];
     if (token >= vocab) {
       out[i] = 0.0F;
-      *invalid = 1;
+      atomicOr(invalid, 1);
       continue;
     }
     out[i] = bf16_to_f32(table[static_cast<size_t>(token) * width + col]);

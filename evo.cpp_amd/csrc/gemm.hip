@@ -761,7 +761,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(
 // saturating), 8 elements per thread and step.
 __global__ void planes_to_f16_kernel(const uint16_t *__restrict__ hi,
                                      const uint16_t *__restrict__ lo, size_t n8,
-                                     _Float16 *__restrict__ out) {
+                                     _Float16 *__restrict__ out, int *saturated) {
   for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n8;
        i += static_cast<size_t>(gridDim.x) * blockDim.x) {
     const uint4 h = reinterpret_cast<const uint4 *>(hi)[i];
@@ -773,6 +773,8 @@ __global__ void planes_to_f16_kernel(const uint16_t *__restrict__ hi,
       const float a = __builtin_bit_cast(float, hw[q] << 16) + __builtin_bit_cast(float, lw[q] << 16);
       const float b = __builtin_bit_cast(float, hw[q] & 0xffff0000U) +
                       __builtin_bit_cast(float, lw[q] & 0xffff0000U);
+      note_f16_range(saturated, a);
+      note_f16_range(saturated, b);
       v[2 * q] = static_cast<_Float16>(fminf(fmaxf(a, -65504.0F), 65504.0F));
       v[2 * q + 1] = static_cast<_Float16>(fminf(fmaxf(b, -65504.0F), 65504.0F));
     }
@@ -864,7 +866,7 @@ __global__ void split_k_reduce_kernel(const float *__restrict__ part, int splits
 }  // namespace
 
 Status planes_to_f16(const uint16_t *hi, const uint16_t *lo, size_t n, uint16_t *out,
-                     hipStream_t stream) {
+                     hipStream_t stream, int *saturated) {
   if (hi == nullptr || lo == nullptr || out == nullptr || n % 8 != 0 ||
       reinterpret_cast<uintptr_t>(hi) % 16 != 0 || reinterpret_cast<uintptr_t>(lo) % 16 != 0 ||
       reinterpret_cast<uintptr_t>(out) % 16 != 0)
@@ -873,7 +875,7 @@ Status planes_to_f16(const uint16_t *hi, const uint16_t *lo, size_t n, uint16_t 
   const size_t n8 = n / 8;
   const unsigned blocks = static_cast<unsigned>(std::min<size_t>((n8 + 255) / 256, 16384));
   hipLaunchKernelGGL(planes_to_f16_kernel, dim3(blocks), dim3(256), 0, stream, hi, lo, n8,
-                     reinterpret_cast<_Float16 *>(out));
+                     reinterpret_cast<_Float16 *>(out), saturated);
   return launch_status("planes_to_f16_kernel");
 }
 

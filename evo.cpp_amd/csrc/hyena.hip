@@ -421,12 +421,30 @@ __device__ inline uint32_t pack_f16(float a, float b) {
 template <typename O> struct Plane16;
 template <> struct Plane16<uint16_t *> {
   static __device__ uint16_t *ptr(uint16_t *o) { return o; }
+  static __device__ int *flag(uint16_t *) { return nullptr; }
   static __device__ uint32_t pack(float a, float b) { return pack_bf16(a, b); }
 };
 template <> struct Plane16<F16Out> {
   static __device__ uint16_t *ptr(const F16Out &o) { return o.out; }
+  static __device__ int *flag(const F16Out &o) { return o.saturated; }
   static __device__ uint32_t pack(float a, float b) { return pack_f16(a, b); }
 };
+// Range check of FP16 outputs (no-op for BF16 planes, whose flag is null):
+// one branch per pair or per eight values.
+__device__ inline void note_pair(int *flag, float a, float b) {
+  if (flag != nullptr && !(__builtin_fabsf(a) <= 65504.0F && __builtin_fabsf(b) <= 65504.0F))
+    atomicOr(flag, kFlagF16Range);
+}
+__device__ inline void note_eight(int *flag, const float (&v)[8]) {
+  if (flag == nullptr)
+    return;
+  bool out_of_range = false;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    out_of_range |= !(__builtin_fabsf(v[i]) <= 65504.0F);
+  if (out_of_range)
+    atomicOr(flag, kFlagF16Range);
+}
 
 // Output of a channel pair through segment-bounded buffer resources:
 // `lane` is the pair's byte offset within a row of one plane, `row` the
@@ -448,10 +466,13 @@ template <> struct PairOut<float *> {
 };
 template <typename O> struct PairOut16 {
   __amdgpu_buffer_rsrc_t out;
+  int *flag;
   __device__ PairOut16(const O &o, size_t first, size_t rows, size_t W) {
     out = buffer_resource(Plane16<O>::ptr(o) + first * W, static_cast<uint32_t>(rows * W * 2));
+    flag = Plane16<O>::flag(o);
   }
   __device__ void put(uint32_t lane, uint32_t row, float a, float b) const {
+    note_pair(flag, a, b);
     __builtin_amdgcn_raw_buffer_store_b32(Plane16<O>::pack(a, b), out,
                                           static_cast<int>(lane + row), 0, kStreamStore);
   }
@@ -1104,12 +1125,18 @@ template <> struct HalfOut<float *> {
 };
 template <typename O> struct HalfOut16 {
   __amdgpu_buffer_rsrc_t out;
+  int *flag;
   __device__ HalfOut16(const O &o, size_t first, size_t rows, size_t W) {
     out = buffer_resource(Plane16<O>::ptr(o) + first * W, static_cast<uint32_t>(rows * W * 2));
+    flag = Plane16<O>::flag(o);
   }
   __device__ void put_rows(int half, uint32_t lane, uint32_t row, uint32_t row_bytes, float a0,
                            float b0, float a1, float b1) const {
     // Even lane row `row`, odd lane the next one.
+    if (half == 0)
+      note_pair(flag, a0, b0);
+    else
+      note_pair(flag, a1, b1);
     const uint32_t word = half == 0 ? Plane16<O>::pack(a0, b0) : Plane16<O>::pack(a1, b1);
     __builtin_amdgcn_raw_buffer_store_b32(word, out,
                                           static_cast<int>(lane + row + half * row_bytes), 0,
@@ -1298,6 +1325,7 @@ template <typename O> struct MsOut16 {
   __device__ static void flush(const float *src, const O &out, size_t index) {
     float v[8];
     load8(src, v);
+    note_eight(Plane16<O>::flag(out), v);
     uint32_t w[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -1857,6 +1885,7 @@ template <> struct HmOut<float *> {
 template <typename O> struct HmOut16 {
   __device__ static int stores(const O &) { return 1; }
   __device__ static void put(const float (&v)[8], const O &out, size_t index) {
+    note_eight(Plane16<O>::flag(out), v);
     u32x4 w;
 #pragma unroll
     for (int i = 0; i < 4; ++i)

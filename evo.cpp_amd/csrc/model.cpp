@@ -431,7 +431,7 @@ Status Context::initialize(std::shared_ptr<const Model> model, size_t capacity,
   EVO_TRY(gated_.allocate(R * c.inner * 4, "mlp gate"));
   EVO_TRY(logits_.allocate(R * c.vocab * 4, "logits"));
   EVO_TRY(codes_.allocate(R * w, "fp8 codes"));
-  EVO_TRY(flag_.allocate(sizeof(int), "token check flag"));
+  EVO_TRY(flag_.allocate(sizeof(int), "token and range check flag"));
   EVO_TRY(hip_check(hipMemsetAsync(flag_.as<void>(), 0, sizeof(int), stream_), "flag reset"));
   EVO_TRY(hip_check(hipHostMalloc(reinterpret_cast<void **>(&host_flag_), sizeof(int),
                                   hipHostMallocDefault), "pinned flag"));
@@ -555,7 +555,8 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
         // The normed rows as one FP16 plane (in the mixer output's buffer,
         // written only after this product) times the FP16 weight copy.
         uint16_t *normed16 = mixed_.as<uint16_t>();
-        EVO_TRY(planes_to_f16(normed_hi, normed_lo, rows * w, normed16, stream_));
+        EVO_TRY(planes_to_f16(normed_hi, normed_lo, rows * w, normed16, stream_,
+                              flag_.as<int>()));
         EVO_TRY(gemm_bf16w(Activation{normed16, nullptr, w, true},
                            L.projection16.as<uint16_t>(),
                            GemmOutput{projected, nullptr, nullptr, 3 * w}, rows, 3 * w, w,
@@ -575,9 +576,12 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
     if (L.type == Mixer::kAttention) {
       uint16_t *query = query_.as<uint16_t>();
       const size_t cache_plane = cache_capacity_ * w;
+      // With the FP16 output the range is checked on V as it enters the
+      // cache (the outputs are convex combinations of V rows), not per output.
       EVO_TRY(qkv_rope(projected, rows, w, c.heads, c.column_split, L.inv_freq.as<float>(),
                        c.rope_scale, position_, query, rows * w, k.keys.as<uint16_t>(),
-                       k.values.as<uint16_t>(), cache_plane, cache_capacity_, stream_));
+                       k.values.as<uint16_t>(), cache_plane, cache_capacity_, stream_,
+                       f16_out ? flag_.as<int>() : nullptr));
       EVO_TRY(causal_attention(query, rows * w, k.keys.as<uint16_t>(),
                                k.values.as<uint16_t>(), cache_plane, cache_capacity_, rows,
                                position_,
@@ -611,7 +615,7 @@ Status Context::run_layers(size_t rows, size_t capture_layer, float *capture) {
                                        workspace_.bytes(), out, stream_);
       };
       if (f16_out)
-        EVO_TRY(mixer(F16Out{mixed_hi}));
+        EVO_TRY(mixer(F16Out{mixed_hi, flag_.as<int>()}));
       else
         EVO_TRY(mixer(mixed_out));
     }
@@ -723,8 +727,13 @@ Status Context::finish() {
   EVO_TRY(hip_check(hipMemcpyAsync(host_flag_, flag_.as<void>(), sizeof(int),
                                    hipMemcpyDeviceToHost, stream_), "flag download"));
   EVO_TRY(hip_check(hipStreamSynchronize(stream_), "prefill"));
-  if (*host_flag_ != 0)
+  if (*host_flag_ & 1)
     return {ErrorCode::kInvalidArgument, "invalid_argument: token exceeds model vocabulary"};
+  if (*host_flag_ & kFlagF16Range)
+    return {ErrorCode::kUnsupported,
+            "unsupported: an activation of the FP16 one-pass products exceeded the FP16 "
+            "range (+-65504); use a context without EVO_CONTEXT_FLAG_HIP_F16_OUT / "
+            "EVO_CONTEXT_FLAG_HIP_F16_PROJ"};
   valid_ = true;
   return Status::Ok();
 }

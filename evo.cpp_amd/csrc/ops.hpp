@@ -29,10 +29,15 @@ struct SplitOut {
 };
 
 // Output of a producer kernel as one FP16 plane, fp16(v) rounded to nearest
-// even and saturated to +-65504, for the one-pass FP16 products.
+// even and saturated to +-65504, for the one-pass FP16 products. A value
+// outside the FP16 range (or NaN) sets bit 1 of *saturated when it is given.
 struct F16Out {
   uint16_t *out;
+  int *saturated = nullptr;
 };
+// Bit of the context's device flag that an out-of-range FP16 store raises
+// (bit 0: a token outside the vocabulary).
+constexpr int kFlagF16Range = 2;
 
 // A GEMM activation as split BF16 planes: hi = bf16(a), lo = bf16(a - hi)
 // (lo null: BF16 activations), row stride ld elements.
@@ -95,7 +100,7 @@ Status gemm_bf16w_normed(const RowNorm &norm, bool split, const uint16_t *W,
 // hi[i] = bf16(x[i]), lo[i] = bf16(x[i] - hi[i]) (lo may be null).
 // hi + lo (split BF16 planes) -> FP16 bits (RNE, saturating at 65504).
 Status planes_to_f16(const uint16_t *hi, const uint16_t *lo, size_t n, uint16_t *out,
-                     hipStream_t stream);
+                     hipStream_t stream, int *saturated = nullptr);
 // BF16 -> FP16 bits (RNE, saturating), e.g. a weight for FP16 products.
 Status bf16_to_f16(const uint16_t *x, size_t n, uint16_t *out, hipStream_t stream);
 Status split_planes(const float *x, size_t n, uint16_t *hi, uint16_t *lo,
@@ -200,15 +205,18 @@ Status hyena_forward(int kind, const T *projection, size_t length,
 // 12-15 (bits 2 and 3 of the position swapped). capacity is a multiple of
 // 64 and cache rows never written must hold finite values (zero them once).
 // qkv_rope splits the QKV projection [rows, 3W] into rotated Q, rotated K and
-// V, appending K/V at position `prefix` of the caches.
+// V, appending K/V at position `prefix` of the caches. With v_range_flag, a V
+// value outside the FP16 range (or NaN) raises kFlagF16Range there: the
+// attention outputs, convex combinations of V, then stay inside it.
 Status qkv_rope(const float *projected, size_t rows, size_t width, size_t heads,
                 bool column_split, const float *inv_freq, float rope_scale,
                 size_t prefix, uint16_t *q, size_t q_plane, uint16_t *k_cache,
-                uint16_t *v_cache, size_t cache_plane, size_t capacity, hipStream_t stream);
+                uint16_t *v_cache, size_t cache_plane, size_t capacity, hipStream_t stream,
+                int *v_range_flag = nullptr);
 // Causal attention of `rows` queries at positions prefix.. against keys
 // [0, prefix + rows). Layout [time, heads, head_dim] = [time, W]. Output F32
 // (out_f32), split planes (out_hi, out_lo), or with out_f16 one saturated
-// FP16 plane in out_hi.
+// FP16 plane in out_hi (its range follows from V's: see qkv_rope).
 Status causal_attention(const uint16_t *q, size_t q_plane, const uint16_t *k_cache,
                         const uint16_t *v_cache, size_t cache_plane, size_t capacity,
                         size_t rows, size_t prefix, size_t heads, size_t head_dim,

@@ -13,6 +13,7 @@ from typing import Callable, List, Optional
 import numpy as np
 
 EVO_STATUS_OK = 0
+EVO_STATUS_UNSUPPORTED = 5
 STATUS_NAMES = {0: "ok", 2: "invalid_argument", 3: "io", 4: "model_format",
                 5: "unsupported", 6: "cuda", 7: "mps", 8: "hip", 70: "internal"}
 BACKEND_AUTO, BACKEND_CUDA, BACKEND_CPU, BACKEND_MPS, BACKEND_HIP = 0, 1, 2, 3, 4

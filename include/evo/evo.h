@@ -92,7 +92,9 @@ enum {
    * Hyena projections are unchanged. */
   EVO_CONTEXT_FLAG_HIP_F16_PROJ = 1u << 11u,
   /* "+f16-out": only the out-projections run as one FP16 MFMA pass (the
-   * attention input projections stay split BF16); implied by F16_PROJ. */
+   * attention input projections stay split BF16); implied by F16_PROJ. With
+   * either flag, a prefill whose FP16 activations leave the FP16 range
+   * (+-65504) or hold NaN fails with EVO_STATUS_UNSUPPORTED. */
   EVO_CONTEXT_FLAG_HIP_F16_OUT = 1u << 12u
 };
 

@@ -197,6 +197,29 @@ def test_f16_projection_profile_tiny_chunks(hip, tmp_path, length, arena, flags,
     assert np.array_equal(actual.argmax(1), expected.argmax(1))
 
 
+
+@pytest.mark.parametrize("flags", [F16_OUT, F16_PROJ])
+def test_f16_profiles_refuse_out_of_range_activations(hip, tmp_path, flags):
+    """An FP16 one-pass product whose activation exceeds the FP16 range
+    (block 0's pre-norm scale x 1e5: the mixer output reaches ~1e12) makes
+    the prefill fail with EVO_STATUS_UNSUPPORTED instead of returning logits
+    of saturated values; the split-BF16 context runs the same artifact."""
+    shape = A.tiny_shape(width=64, layers=4, heads=2, inner=96, groups=16, attn=(3,))
+    art = A.random_artifact(shape, seed=21)
+    for spec in art.specs:
+        if spec.name == "blocks.0.pre_norm.scale":
+            base = spec.make
+            spec.make = lambda rng, base=base: base(rng) * np.float32(1e5)
+    path = str(tmp_path / "loud.safetensors")
+    art.write(path)
+    tokens = A.acgt_tokens(64, seed=21)
+    with pytest.raises(capi.EvoError, match="FP16 range") as failure:
+        run_hip(hip, path, tokens, flags=flags)
+    assert failure.value.status == capi.EVO_STATUS_UNSUPPORTED
+    logits, profile = run_hip(hip, path, tokens)
+    assert profile == "hip-f32"
+    assert np.isfinite(logits).all()
+
 def open_context(hip, path, capacity, flags=0):
     import ctypes
     model = hip.load(path, capi.BACKEND_HIP)
