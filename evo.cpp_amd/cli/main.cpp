@@ -206,8 +206,9 @@ void print_help() {
       "  -m, --model PATH      evo2-runtime-v1 Safetensors artifact\n"
       "  --ctx N               Context size in tokens, [1, 1048576] "
       "(default: 8192)\n"
-      "  --profile P           hip-f32 (default), hip-bf16, hip-f32+fp8-exact,\n"
-      "                        hip-bf16+fp8-exact; exact for --backend cpu\n"
+      "  --profile P           hip-f32 (default) or hip-bf16, then any of\n"
+      "                        +fp8-exact | +fp8-k32, +f16-out, +f16-proj (hip-f32\n"
+      "                        only), e.g. hip-f32+f16-out; exact for --backend cpu\n"
       "  --fp8-projections     Convert BF16 Hyena projections to E4M3 at load\n"
       "  --backend hip|cpu     Backend requested from the library (default: "
       "hip)\n"
@@ -409,16 +410,32 @@ Status context_flags(const Options &options, uint32_t *flags) {
       return invalid("--backend cpu supports --profile exact only");
     return {};
   }
-  if (p.empty() || p == "hip-f32")
+  if (p.empty())
     return {};
-  if (p == "hip-bf16") {
-    *flags = EVO_CONTEXT_FLAG_HIP_BF16;
-  } else if (p == "hip-f32+fp8-exact") {
-    *flags = EVO_CONTEXT_FLAG_HIP_FP8_EXACT;
-  } else if (p == "hip-bf16+fp8-exact") {
-    *flags = EVO_CONTEXT_FLAG_HIP_BF16 | EVO_CONTEXT_FLAG_HIP_FP8_EXACT;
-  } else {
-    return invalid("unknown --profile '" + p + "'");
+  // A base profile and '+'-separated options, as the library names the
+  // context's profile (evo_context_profile).
+  size_t start = 0;
+  bool first = true;
+  while (start <= p.size()) {
+    const size_t end = std::min(p.find('+', start), p.size());
+    const std::string part = p.substr(start, end - start);
+    if (first && part == "hip-f32") {
+    } else if (first && part == "hip-bf16") {
+      *flags |= EVO_CONTEXT_FLAG_HIP_BF16;
+    } else if (!first && part == "fp8-exact" && !(*flags & EVO_CONTEXT_FLAG_HIP_FP8_K32)) {
+      *flags |= EVO_CONTEXT_FLAG_HIP_FP8_EXACT;
+    } else if (!first && part == "fp8-k32" && !(*flags & EVO_CONTEXT_FLAG_HIP_FP8_EXACT)) {
+      *flags |= EVO_CONTEXT_FLAG_HIP_FP8_K32;
+    } else if (!first && part == "f16-out" && !(*flags & EVO_CONTEXT_FLAG_HIP_BF16)) {
+      *flags |= EVO_CONTEXT_FLAG_HIP_F16_OUT;
+    } else if (!first && part == "f16-proj" && !(*flags & EVO_CONTEXT_FLAG_HIP_BF16)) {
+      *flags |= EVO_CONTEXT_FLAG_HIP_F16_PROJ;
+    } else {
+      *flags = 0;
+      return invalid("unknown --profile '" + p + "'");
+    }
+    first = false;
+    start = end + 1;
   }
   return {};
 }

@@ -108,3 +108,25 @@ def test_bf16_profile_scores(files):
     assert a["profile"] == "hip-bf16"
     diff = np.abs(np.subtract(a["token_log_likelihoods"], b["token_log_likelihoods"]))
     assert diff.max() <= 2 * 1e-2 * 60.0
+
+
+@pytest.mark.parametrize("profile", ["hip-f32+f16-out", "hip-f32+f16-proj", "hip-f32+fp8-k32"])
+def test_composed_profiles_score(files, profile):
+    """--profile takes a base profile and '+'-options as the library names
+    them; the FP16 one-pass and FP8 options stay within the hip-f32 logits
+    contract against the reference on this tiny BF16 model (the FP8 option
+    only names the promotion mode: this artifact has no FP8 projections)."""
+    mine = hip("score", "-m", files["model"], "--input", files["raw"], "--profile", profile)
+    theirs = reference("score", "-m", files["model"], "--input", files["raw"])
+    assert mine.returncode == 0, mine.stderr
+    a, = C.jsonl(mine.stdout)
+    b, = C.jsonl(theirs.stdout)
+    assert a["profile"] == profile
+    diff = np.abs(np.subtract(a["token_log_likelihoods"], b["token_log_likelihoods"]))
+    assert diff.max() <= 2 * TOL * 60.0
+
+
+def test_unknown_composed_profile_is_rejected(files):
+    for profile in ("hip-f32+", "hip-bf16+f16-out", "hip-f32+fp8-exact+fp8-k32", "f16-out"):
+        run = hip("score", "-m", files["model"], "--input", files["raw"], "--profile", profile)
+        assert run.returncode != 0 and b"unknown --profile" in run.stderr
