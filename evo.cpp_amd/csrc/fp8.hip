@@ -194,19 +194,13 @@ __global__ __launch_bounds__(kWaves * 64, 2) void fp8_mfma_kernel(
     dst[i] = (is_a ? 0 : kBM * kBK) + chunk * 1024;
     from_a[i] = is_a;
   }
-  // DMA of step `step`'s K range into the buffer of step `slot`.
-  auto issue_into = [&](int slot, int step) {
-    uint8_t *stage = fp8_lds + (slot % kStages) * kStageBytes;
+  auto issue = [&](int step) {
+    uint8_t *stage = fp8_lds + (step % kStages) * kStageBytes;
     const int k0 = step * kBK;
 #pragma unroll
     for (int i = 0; i < kDmaPerWave; ++i)
       dma16((from_a[i] ? a_base : w_base) + k0, src[i], stage + dst[i]);
   };
-  auto issue = [&](int step) { issue_into(step, step); };
-  // The next step's DMA without a branch (a branch let the compiler move
-  // the MFMAs it should overlap behind it): the last step re-reads its own
-  // K range into the free buffer, waited for after the loop.
-  auto issue_next = [&](int s) { issue_into(s + 1, min(s + 1, K / kBK - 1)); };
 
   f32x16 acc[2][3];
 #pragma unroll
@@ -313,12 +307,8 @@ __global__ __launch_bounds__(kWaves * 64, 2) void fp8_mfma_kernel(
           acc[t / 3][t % 3] = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(
               av[0][t / 3], bv[0][t % 3], acc[t / 3][t % 3], 0, 0, 0);
         }
-        if (c == 0) {
-          // The next step's DMA goes out under the first chunk's MFMAs.
-          __builtin_amdgcn_sched_barrier(0);
-          issue_next(s);
-          __builtin_amdgcn_sched_barrier(0);
-        }
+        if (c == 0 && s + 1 < steps)
+          issue(s + 1);  // the next step's DMA, after the first chunk's reads
 #pragma unroll
         for (int t = 0; t < 6; ++t) {
           acc[t / 3][t % 3] = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(
@@ -333,7 +323,6 @@ __global__ __launch_bounds__(kWaves * 64, 2) void fp8_mfma_kernel(
       }
     }
   }
-  wait_dma<0>();  // the last step's extra DMA has landed before the block ends
   if constexpr (kChunk == 32) {
     // The last chunk's deferred promotion of the last tile.
 #pragma unroll
