@@ -232,17 +232,19 @@ def open_context(hip, path, capacity, flags=0):
     return capi.Context(model, handle)
 
 
-@pytest.mark.parametrize("groups,heads", [(16, 2), (4, 2), (16, 4)])
-def test_decode_matches_prefill_logits(hip, tmp_path, groups, heads):
+@pytest.mark.parametrize("groups,heads,flags", [(16, 2, 0), (4, 2, 0), (16, 4, 0),
+                                                (4, 2, F16_OUT)])
+def test_decode_matches_prefill_logits(hip, tmp_path, groups, heads, flags):
     """Prefill n tokens, then decode the rest one at a time: each decode row
     equals the oracle's full-sequence prefill row at that position (groups=4
     gives 16-channel filter groups, the MFMA FIR; heads 2/4 the MFMA/VALU
-    attention)."""
+    attention; F16_OUT: the prefill's out-projections on one FP16 pass, the
+    decode steps reading the caches it left)."""
     shape = A.tiny_shape(width=64, layers=8, heads=heads, inner=96, groups=groups, attn=(3,))
     path = make(tmp_path, shape, seed=31 + groups)
     tokens = A.acgt_tokens(96, seed=groups)
     expected = O.OracleModel(path).prefill(tokens)
-    ctx = open_context(hip, path, capacity=100)
+    ctx = open_context(hip, path, capacity=100, flags=flags)
     first = 80
     logits = ctx.prefill(tokens[:first].astype(np.uint8).tobytes())
     assert relmax(logits, expected[:first]) <= TOL
